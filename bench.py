@@ -1,0 +1,219 @@
+#!/usr/bin/env python3
+"""Batch-1 greedy decode benchmark on one MI355X.
+
+Workload: the Qwen2.5-0.5B-shaped decoder (24 layers, hidden 896, 14/2 heads,
+SwiGLU 4864, vocab 151936, tied bf16 LM head, qkv bias) with seeded random
+N(0, 0.02) bf16 weights.  A 40-token random prompt is prefilled position by
+position (the reference's prefill, npu_llm/runtime/generate.py:1110-1125),
+then greedy decode runs in 31-step runs at positions 40..70, i.e. 32 tokens
+per run with the prefill's token, the reference's "40-token prompt, 32
+tokens" protocol.  One step = one decode token: every layer, the final norm,
+the LM head and the argmax, with weights and KV resident in HBM.
+
+value = timed steps / wall seconds between two stream synchronisations.
+roofline: the kernel with the largest share of a step, timed with HIP events
+on the engine's stream over launches that rotate through all 24 layers'
+weights (419 MB for gate/up, more than the 256 MB Infinity Cache), against
+the MI355X's 8 TB/s HBM peak.
+cpu_baseline: the oracle (NumPy BF16 CPU restatement of the reference's CPU
+runtime) on a bounded sample of the same workload.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "hawkpoint-npu-llm_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "decode tok/s @batch1 + HBM GB/s (% peak), Qwen2.5-0.5B-shape bf16"
+HBM_PEAK_GBS = 8000.0
+PROMPT = 40
+RUN = 31  # decode steps per run after the prefill token (positions 40..70)
+REFERENCE_TOKS = 28.83  # XDNA1 Qwen2.5-0.5B engine decode (reference README.md:92)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def step_bytes(meta, position):
+    """Algorithmic HBM bytes of one decode step at `position`: every weight
+    once (bf16), qkv bias, norm gains, the embedding row, KV read for slots
+    0..position and the new slot written."""
+    h, i = meta["hidden_size"], meta["intermediate_size"]
+    nq, nkv, d = meta["attention_heads"], meta["kv_heads"], meta["head_dim"]
+    qkv = (nq + 2 * nkv) * d
+    per_layer = 2 * (qkv * h + h * nq * d + 2 * i * h + h * i) + 4 * qkv + 2 * 2 * h
+    head = 2 * meta["vocab_size"] * h + 2 * h
+    kv_slot = meta["layers"] * 2 * nkv * d * 2
+    return meta["layers"] * per_layer + head + 2 * h + kv_slot * (position + 1) + kv_slot
+
+
+def part_bytes(meta, part):
+    h, i = meta["hidden_size"], meta["intermediate_size"]
+    nq, nkv, d = meta["attention_heads"], meta["kv_heads"], meta["head_dim"]
+    qkv = (nq + 2 * nkv) * d
+    return {
+        "qkv": 2 * qkv * h + 2 * h + 2 * h + 4 * qkv + 2 * qkv,
+        "o_proj": 2 * h * nq * d + 2 * nq * d + 2 * h + 2 * h,
+        "gate_up": 2 * 2 * i * h + 2 * h + 2 * h + 2 * i,
+        "down_proj": 2 * h * i + 2 * i + 2 * h + 2 * h,
+        "lm_head": 2 * meta["vocab_size"] * h + 2 * h + 2 * h + 4 * meta["vocab_size"],
+    }.get(part)
+
+
+def cpu_baseline(model, prompt, decode_steps):
+    """Oracle decode tok/s on the host cores: a short prefill, then
+    `decode_steps` timed greedy steps (reference protocol: decode steps over
+    the seconds after TTFT)."""
+    from oracle.cpu_backend import OracleDecoder
+
+    threads = os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS")
+    cores = int(threads) if threads else len(os.sched_getaffinity(0))
+    oracle = OracleDecoder(model, len(prompt) + decode_steps + 1)
+    timings = []
+    oracle.generate_greedy(prompt, decode_steps + 1, keep_logits=False, timings=timings)
+    decode = timings[len(prompt):]
+    return {
+        "value": round(len(decode) / sum(decode), 3),
+        "unit": "tok/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{len(prompt)}-token prefill then {len(decode)} greedy decode steps of the same "
+        f"model; NumPy {__import__('numpy').__version__} float32 BLAS, {cores} threads",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3100)
+    ap.add_argument("--warmup", type=int, default=310)
+    ap.add_argument("--kernel-launches", type=int, default=240)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the engine runs on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    from runtime import hip
+    from runtime.qwen_engine import QwenDecoderEngine
+    from runtime.synthetic import QWEN25_05B, SyntheticModel
+
+    log("building the synthetic Qwen2.5-0.5B-shape model")
+    model = SyntheticModel(QWEN25_05B, seed=0)
+    meta = model.metadata
+    rng = np.random.default_rng(12)
+    prompt = [int(t) for t in rng.integers(0, meta["vocab_size"], PROMPT)]
+    engine = QwenDecoderEngine(model, context_length=4096)
+    lib = hip.lib()
+
+    def prefill():
+        for pos, tok in enumerate(prompt[:-1]):
+            engine.step_token(tok, pos, logits=False)
+        first, _ = engine.step_token(prompt[-1], PROMPT - 1, logits=True, want_logits_array=False)
+        return first
+
+    first = prefill()  # captures both graphs
+    t0 = time.perf_counter()
+    first = prefill()
+    ttft = time.perf_counter() - t0
+    log(f"prefill {PROMPT} positions: TTFT {ttft * 1e3:.2f} ms, first token {first}")
+
+    def decode(n):
+        tokens = []
+        while n > 0:
+            k = min(RUN, n)
+            tokens = engine.generate(first, PROMPT, k)
+            n -= k
+        return tokens
+
+    decode(args.warmup)
+    hip.check(lib.hk_stream_sync(engine.stream), "sync")
+    t0 = time.perf_counter()
+    decode(args.steps)
+    hip.check(lib.hk_stream_sync(engine.stream), "sync")
+    elapsed = time.perf_counter() - t0
+    tok_s = args.steps / elapsed
+    ms_step = elapsed / args.steps * 1e3
+    mean_pos = PROMPT + (RUN - 1) / 2.0
+    step_gbs = step_bytes(meta, mean_pos) / (ms_step * 1e-3) / 1e9
+    log(f"decode: {tok_s:.1f} tok/s, {ms_step * 1e3:.1f} us/step, {step_gbs:.0f} GB/s whole step")
+
+    # per-part kernel times (HIP events on the engine stream)
+    parts = {}
+    layers = meta["layers"]
+    stream = engine.stream
+    for name, part in hip.PARTS.items():
+        n = args.kernel_launches
+        ev0, ev1 = hip.Event(), hip.Event()
+        for i in range(8):
+            hip.check(lib.hk_engine_launch_part(engine._engine, part, i % layers), "launch_part")
+        ev0.record(stream)
+        for i in range(n):
+            hip.check(lib.hk_engine_launch_part(engine._engine, part, i % layers), "launch_part")
+        ev1.record(stream)
+        parts[name] = ev0.elapsed_ms(ev1) * 1e3 / n
+    per_step = {k: v * (1 if k == "lm_head" else layers) for k, v in parts.items()}
+    dominant = max((k for k in per_step if part_bytes(meta, k)), key=per_step.get)
+    dom_bytes = part_bytes(meta, dominant)
+    achieved = dom_bytes / (parts[dominant] * 1e-6) / 1e9
+    log("kernel us/launch: " + ", ".join(f"{k} {v:.2f}" for k, v in parts.items()))
+    engine.close()
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(tok_s / REFERENCE_TOKS, 2),
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2.5-0.5B-shape decoder (24L, H896, 14q/2kv heads, I4864, V151936, "
+            "tied head, qkv bias), seeded N(0,0.02) bf16 weights, batch 1, 40-token random prompt "
+            "prefilled per position, greedy decode at positions 40..70 in 31-step runs",
+            "batch": 1,
+            "prompt_tokens": PROMPT,
+            "decode_positions": [PROMPT, PROMPT + RUN - 1],
+            "kv_slots_allocated": 4096,
+        },
+        "ttft_ms": round(ttft * 1e3, 3),
+        "step_hbm_gbs": round(step_gbs, 1),
+        "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "step_bytes": int(step_bytes(meta, mean_pos)),
+        "kernel_us": {k: round(v, 3) for k, v in parts.items()},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"{dominant} GEMV (bytes/launch {dom_bytes})",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "baseline_source": "28.83 tok/s, XDNA1 NPU Qwen2.5-0.5B engine (reference README.md:92)",
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle")
+        result["cpu_baseline"] = cpu_baseline(model, prompt[:8], args.cpu_steps)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

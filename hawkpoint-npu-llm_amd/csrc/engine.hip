@@ -1,0 +1,700 @@
+// The decode engine and the C ABI of libhk.so (declared in include/hk.h).
+//
+// One decode step (npu_llm/runtime/cpu_backend.py:131-181 per layer, plus the
+// head) is five kernels per layer and one for the head:
+//   qkv     RMSNorm prologue + GEMV + bias           (gemv.hip)
+//   attn    RoPE + KV append + GQA attention         (attention.hip)
+//   o       GEMV + residual                          (gemv.hip)
+//   gate_up RMSNorm prologue + paired GEMV + SwiGLU  (gemv.hip)
+//   down    GEMV + residual                          (gemv.hip)
+//   head    RMSNorm prologue + GEMV (f32 logits) + argmax with token feedback
+// The kernels read the token and position from a device control block, so
+// one captured hipGraph per variant (with / without the head) serves every
+// position; the host only rewrites the control block between replays.
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/hk.h"
+#include "hk_common.h"
+#include "hk_internal.h"
+
+namespace hk {
+
+static thread_local std::string g_error;
+
+void set_error(const std::string& message) { g_error = message; }
+
+int fail(const std::string& message) {
+  set_error(message);
+  return HK_ERR_INVALID;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+  set_error(std::string(what) + ": " + hipGetErrorString(err));
+  return HK_ERR_HIP;
+}
+
+namespace {
+
+#define HK_CHECK(expr)                                   \
+  do {                                                   \
+    const hipError_t err_ = (expr);                      \
+    if (err_ != hipSuccess) return hip_fail(err_, #expr); \
+  } while (0)
+
+#define HK_TRY(expr)              \
+  do {                            \
+    const int rc_ = (expr);       \
+    if (rc_ != 0) return rc_;     \
+  } while (0)
+
+__global__ void set_ctrl_kernel(StepCtrl* ctrl, int32_t token, int32_t position, int32_t advance) {
+  ctrl->token = token;
+  ctrl->position = position;
+  ctrl->n_out = 0;
+  ctrl->advance = advance;
+}
+
+__global__ void store_i32_kernel(int32_t* dst, int32_t value) { *dst = value; }
+
+// Scratch shared by the single-operation entry points on one device.
+struct OpScratch {
+  int device = -1;
+  ArgmaxState* am = nullptr;
+  int32_t* position = nullptr;
+  float* partial = nullptr;
+  unsigned int* counters = nullptr;
+  size_t partial_floats = 0;
+  int counter_slots = 0;
+};
+std::mutex g_op_mutex;
+std::vector<OpScratch> g_op_scratch;
+
+int op_scratch(OpScratch** out, size_t partial_floats, int counter_slots) {
+  int dev = 0;
+  HK_CHECK(hipGetDevice(&dev));
+  if ((int)g_op_scratch.size() <= dev) g_op_scratch.resize(dev + 1);
+  OpScratch& s = g_op_scratch[dev];
+  if (s.am == nullptr) {
+    HK_CHECK(hipMalloc(&s.am, sizeof(ArgmaxState)));
+    HK_CHECK(hipMemset(s.am, 0, sizeof(ArgmaxState)));
+    HK_CHECK(hipMalloc(&s.position, sizeof(int32_t)));
+  }
+  if (partial_floats > s.partial_floats) {
+    if (s.partial) HK_CHECK(hipFree(s.partial));
+    HK_CHECK(hipMalloc(&s.partial, partial_floats * sizeof(float)));
+    s.partial_floats = partial_floats;
+  }
+  if (counter_slots > s.counter_slots) {
+    if (s.counters) HK_CHECK(hipFree(s.counters));
+    HK_CHECK(hipMalloc(&s.counters, counter_slots * sizeof(unsigned int)));
+    HK_CHECK(hipMemset(s.counters, 0, counter_slots * sizeof(unsigned int)));
+    s.counter_slots = counter_slots;
+  }
+  s.device = dev;
+  *out = &s;
+  return 0;
+}
+
+int gemv_common(const void* W, const float* scale, const uint16_t* x, const float* bias,
+                const uint16_t* residual, uint16_t* y, float* y_f32, int32_t M, int32_t K,
+                bool w8, void* stream) {
+  if (W == nullptr || x == nullptr) return fail("gemv: null weight or input pointer");
+  if (bias != nullptr && residual != nullptr) return fail("gemv: give bias or residual, not both");
+  GemvArgs a = {};
+  a.W = W;
+  a.scale = scale;
+  a.x = x;
+  a.y = y;
+  a.yf = y_f32;
+  a.bias = bias;
+  a.resid = residual;
+  a.M = M;
+  a.K = K;
+  a.pro = PRO_PLAIN;
+  if (y_f32 != nullptr) {
+    if (bias || residual) return fail("gemv: float32 output takes no bias or residual");
+    a.epi = EPI_F32;
+  } else {
+    a.epi = bias ? EPI_BIAS : residual ? EPI_RESID : EPI_BF16;
+  }
+  return launch_gemv(a, w8, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+}  // namespace hk
+
+using namespace hk;
+
+struct hk_engine {
+  std::mutex mu;
+  hk_model_desc d{};
+  std::vector<hk_layer_weights> layers;
+  hk_model_weights w{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool w8 = false;
+  int qkv_rows = 0;
+  int max_splits = 0;
+  // device state
+  uint16_t* h = nullptr;       // residual stream (layer input / down output)
+  uint16_t* h1 = nullptr;      // after attention + residual
+  uint16_t* qkv = nullptr;
+  uint16_t* attn = nullptr;
+  uint16_t* act = nullptr;
+  uint16_t* normed = nullptr;  // final RMSNorm output for hk_engine_final_hidden
+  float* logits = nullptr;
+  uint16_t* kcache = nullptr;  // [L][Hkv][max_ctx][64]
+  uint16_t* vcache = nullptr;
+  float* partial = nullptr;
+  unsigned int* counters = nullptr;
+  ArgmaxState* am = nullptr;
+  StepCtrl* ctrl = nullptr;
+  int32_t* out_tokens = nullptr;  // [max_ctx]
+  int32_t* result = nullptr;
+  hipGraphExec_t graph[2] = {nullptr, nullptr};
+  bool use_graph = true;
+};
+
+namespace {
+
+size_t kv_layer_elems(const hk_engine* e) {
+  return (size_t)e->d.kv_heads * (size_t)e->d.max_context * kHeadDim;
+}
+
+// Launch one part of the step for layer `l` (the head ignores `l`).
+int launch_part(hk_engine* e, int part, int l) {
+  const hk_model_desc& d = e->d;
+  const hipStream_t s = e->stream;
+  const hk_layer_weights& lw = e->layers[l];
+  switch (part) {
+    case HK_PART_QKV: {
+      GemvArgs q = {};
+      q.W = lw.qkv;
+      q.scale = lw.qkv_scale;
+      q.x = e->h;
+      if (l == 0) {
+        q.x_index = &e->ctrl->token;
+        q.x_table = e->w.token_embedding;
+        q.x_copy = e->h;
+        q.vocab_limit = d.vocab;
+      }
+      q.gamma = lw.input_norm;
+      q.eps = d.rms_eps;
+      q.bias = lw.qkv_bias;
+      q.y = e->qkv;
+      q.M = e->qkv_rows;
+      q.K = d.hidden;
+      q.pro = PRO_NORM;
+      q.epi = lw.qkv_bias ? EPI_BIAS : EPI_BF16;
+      return launch_gemv(q, e->w8, s);
+    }
+    case HK_PART_ATTENTION: {
+      AttnArgs at = {};
+      at.qkv = e->qkv;
+      at.cos_tab = e->w.rope_cos;
+      at.sin_tab = e->w.rope_sin;
+      at.kcache = e->kcache + (size_t)l * kv_layer_elems(e);
+      at.vcache = e->vcache + (size_t)l * kv_layer_elems(e);
+      at.position = &e->ctrl->position;
+      at.out = e->attn;
+      at.partial = e->partial;
+      at.counters = e->counters;
+      at.q_heads = d.q_heads;
+      at.kv_heads = d.kv_heads;
+      at.max_ctx = d.max_context;
+      at.max_splits = e->max_splits;
+      return launch_attention_decode(at, s);
+    }
+    case HK_PART_O: {
+      GemvArgs o = {};
+      o.W = lw.o_proj;
+      o.scale = lw.o_scale;
+      o.x = e->attn;
+      o.resid = e->h;
+      o.y = e->h1;
+      o.M = d.hidden;
+      o.K = d.q_heads * kHeadDim;
+      o.pro = PRO_PLAIN;
+      o.epi = EPI_RESID;
+      return launch_gemv(o, e->w8, s);
+    }
+    case HK_PART_GATE_UP: {
+      GemvArgs g = {};
+      g.W = lw.gate_up;
+      g.scale = lw.gate_up_scale;
+      g.x = e->h1;
+      g.gamma = lw.post_attn_norm;
+      g.eps = d.rms_eps;
+      g.y = e->act;
+      g.M = d.intermediate;
+      g.K = d.hidden;
+      g.pro = PRO_NORM;
+      g.epi = EPI_SWIGLU;
+      return launch_gemv(g, e->w8, s);
+    }
+    case HK_PART_DOWN: {
+      GemvArgs dn = {};
+      dn.W = lw.down_proj;
+      dn.scale = lw.down_scale;
+      dn.x = e->act;
+      dn.resid = e->h1;
+      dn.y = e->h;
+      dn.M = d.hidden;
+      dn.K = d.intermediate;
+      dn.pro = PRO_PLAIN;
+      dn.epi = EPI_RESID;
+      return launch_gemv(dn, e->w8, s);
+    }
+    case HK_PART_HEAD: {
+      GemvArgs hd = {};
+      hd.W = e->w.lm_head;
+      hd.x = e->h;
+      hd.gamma = e->w.final_norm;
+      hd.eps = d.rms_eps;
+      hd.yf = e->logits;
+      hd.am = e->am;
+      hd.ctrl = e->ctrl;
+      hd.out_tokens = e->out_tokens;
+      hd.out_cap = d.max_context;
+      hd.token_out = e->result;
+      hd.M = d.vocab;
+      hd.K = d.hidden;
+      hd.pro = PRO_NORM;
+      hd.epi = EPI_F32_ARGMAX;
+      return launch_gemv(hd, false, s);
+    }
+    default:
+      return fail("unknown step part");
+  }
+}
+
+int enqueue_step(hk_engine* e, bool head) {
+  for (int l = 0; l < e->d.layers; ++l)
+    for (int part = HK_PART_QKV; part <= HK_PART_DOWN; ++part) HK_TRY(launch_part(e, part, l));
+  if (head) HK_TRY(launch_part(e, HK_PART_HEAD, 0));
+  return 0;
+}
+
+int run_step(hk_engine* e, bool head) {
+  if (!e->use_graph) return enqueue_step(e, head);
+  hipGraphExec_t& exec = e->graph[head ? 1 : 0];
+  if (exec == nullptr) {
+    hipGraph_t graph = nullptr;
+    HK_CHECK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_step(e, head);
+    const hipError_t end = hipStreamEndCapture(e->stream, &graph);
+    if (rc != 0) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return rc;
+    }
+    if (end != hipSuccess) return hip_fail(end, "hipStreamEndCapture");
+    const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (inst != hipSuccess) {
+      exec = nullptr;
+      return hip_fail(inst, "hipGraphInstantiate");
+    }
+  }
+  HK_CHECK(hipGraphLaunch(exec, e->stream));
+  return 0;
+}
+
+// Turn off token feedback without touching token/position (for timing the
+// head on its own).
+__global__ void ctrl_no_advance_kernel(StepCtrl* ctrl) { ctrl->advance = 0; }
+
+int set_ctrl_keep(hk_engine* e) {
+  hipLaunchKernelGGL(ctrl_no_advance_kernel, dim3(1), dim3(1), 0, e->stream, e->ctrl);
+  HK_CHECK(hipGetLastError());
+  return 0;
+}
+
+int set_ctrl(hk_engine* e, int32_t token, int32_t position, int32_t advance) {
+  hipLaunchKernelGGL(set_ctrl_kernel, dim3(1), dim3(1), 0, e->stream, e->ctrl, token, position,
+                     advance);
+  HK_CHECK(hipGetLastError());
+  return 0;
+}
+
+void free_engine(hk_engine* e) {
+  for (auto& g : e->graph)
+    if (g) (void)hipGraphExecDestroy(g);
+  void* bufs[] = {e->h,       e->h1,       e->qkv,      e->attn,     e->act,
+                  e->normed,  e->logits,   e->kcache,   e->vcache,   e->partial,
+                  e->counters, e->am,      e->ctrl,     e->out_tokens, e->result};
+  for (void* p : bufs)
+    if (p) (void)hipFree(p);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+template <typename T>
+int dalloc(T** p, size_t count) {
+  HK_CHECK(hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T)));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t hk_abi_version(void) { return 1; }
+
+const char* hk_last_error(void) { return g_error.c_str(); }
+
+int hk_init(int32_t device_ordinal) {
+  int count = 0;
+  HK_CHECK(hipGetDeviceCount(&count));
+  if (device_ordinal < 0 || device_ordinal >= count)
+    return fail("hk_init: device ordinal out of range");
+  HK_CHECK(hipSetDevice(device_ordinal));
+  hipDeviceProp_t prop;
+  HK_CHECK(hipGetDeviceProperties(&prop, device_ordinal));
+  if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0) {
+    set_error(std::string("hk_init: libhk.so is built for gfx950 (MI355X); device is ") +
+              prop.gcnArchName);
+    return HK_ERR_UNSUPPORTED;
+  }
+  return 0;
+}
+
+int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
+                     hk_engine** out) {
+  if (!desc || !weights || !out) return fail("hk_engine_create: null argument");
+  *out = nullptr;
+  const hk_model_desc& d = *desc;
+  if (d.layers <= 0 || d.hidden <= 0 || d.intermediate <= 0 || d.vocab <= 0 || d.max_context <= 0)
+    return fail("hk_engine_create: sizes must be positive");
+  if (d.head_dim != kHeadDim) {
+    set_error("hk_engine_create: only head_dim 64 is supported");
+    return HK_ERR_UNSUPPORTED;
+  }
+  if (d.kv_heads <= 0 || d.q_heads % d.kv_heads != 0 || d.q_heads / d.kv_heads > kMaxQPerKV)
+    return fail("hk_engine_create: q_heads must be a multiple of kv_heads (ratio <= 16)");
+  const bool w8 = (d.flags & HK_MODEL_W8) != 0;
+  const int align = w8 ? 16 : 8;
+  if (d.hidden % align || d.intermediate % align || (d.q_heads * kHeadDim) % align)
+    return fail("hk_engine_create: hidden/intermediate sizes must be multiples of 8 (16 for W8)");
+  if (!weights->token_embedding || !weights->lm_head || !weights->final_norm ||
+      !weights->rope_cos || !weights->rope_sin || !weights->layers)
+    return fail("hk_engine_create: missing model tensor");
+  for (int l = 0; l < d.layers; ++l) {
+    const hk_layer_weights& lw = weights->layers[l];
+    if (!lw.qkv || !lw.o_proj || !lw.gate_up || !lw.down_proj || !lw.input_norm ||
+        !lw.post_attn_norm)
+      return fail("hk_engine_create: missing layer tensor in layer " + std::to_string(l));
+    if (w8 && (!lw.qkv_scale || !lw.o_scale || !lw.gate_up_scale || !lw.down_scale))
+      return fail("hk_engine_create: W8 layer without scales in layer " + std::to_string(l));
+    if ((d.flags & HK_MODEL_QKV_BIAS) && !lw.qkv_bias)
+      return fail("hk_engine_create: qkv bias missing in layer " + std::to_string(l));
+  }
+
+  hk_engine* e = new hk_engine();
+  e->d = d;
+  e->w8 = w8;
+  e->layers.assign(weights->layers, weights->layers + d.layers);
+  if (!(d.flags & HK_MODEL_QKV_BIAS))
+    for (auto& lw : e->layers) lw.qkv_bias = nullptr;
+  e->w = *weights;
+  e->w.layers = e->layers.data();
+  e->qkv_rows = (d.q_heads + 2 * d.kv_heads) * kHeadDim;
+  e->max_splits = (d.max_context + kAttnChunk - 1) / kAttnChunk;
+  const char* env = getenv("HK_EAGER");
+  e->use_graph = !(env && env[0] == '1');
+
+  int rc = 0;
+  auto body = [&]() -> int {
+    HK_CHECK(hipGetDevice(&e->device));
+    HK_CHECK(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    HK_TRY(dalloc(&e->h, d.hidden));
+    HK_TRY(dalloc(&e->h1, d.hidden));
+    HK_TRY(dalloc(&e->qkv, e->qkv_rows));
+    HK_TRY(dalloc(&e->attn, (size_t)d.q_heads * kHeadDim));
+    HK_TRY(dalloc(&e->act, d.intermediate));
+    HK_TRY(dalloc(&e->normed, d.hidden));
+    HK_TRY(dalloc(&e->logits, d.vocab));
+    const size_t kv = (size_t)d.layers * kv_layer_elems(e);
+    HK_TRY(dalloc(&e->kcache, kv));
+    HK_TRY(dalloc(&e->vcache, kv));
+    HK_TRY(dalloc(&e->partial, (size_t)d.kv_heads * e->max_splits * kMaxQPerKV * (kHeadDim + 2)));
+    HK_TRY(dalloc(&e->counters, d.kv_heads));
+    HK_TRY(dalloc(&e->am, 1));
+    HK_TRY(dalloc(&e->ctrl, 1));
+    HK_TRY(dalloc(&e->out_tokens, d.max_context));
+    HK_TRY(dalloc(&e->result, 1));
+    HK_CHECK(hipMemset(e->kcache, 0, kv * sizeof(uint16_t)));
+    HK_CHECK(hipMemset(e->vcache, 0, kv * sizeof(uint16_t)));
+    HK_CHECK(hipMemset(e->h, 0, d.hidden * sizeof(uint16_t)));
+    HK_CHECK(hipMemset(e->counters, 0, d.kv_heads * sizeof(unsigned int)));
+    HK_CHECK(hipMemset(e->am, 0, sizeof(ArgmaxState)));
+    HK_CHECK(hipMemset(e->ctrl, 0, sizeof(StepCtrl)));
+    HK_CHECK(hipDeviceSynchronize());
+    return 0;
+  };
+  rc = body();
+  if (rc != 0) {
+    free_engine(e);
+    return rc;
+  }
+  *out = e;
+  return 0;
+}
+
+int hk_engine_step(hk_engine* e, int32_t token, int32_t position, int32_t want_logits,
+                   const uint16_t* embedding_host, float* logits_host, int32_t* next_token_host) {
+  if (!e) return fail("hk_engine_step: null engine");
+  std::lock_guard<std::mutex> lock(e->mu);
+  if (position < 0 || position >= e->d.max_context)
+    return fail("position outside the " + std::to_string(e->d.max_context) + "-token context");
+  if (embedding_host == nullptr && (token < 0 || token >= e->d.vocab))
+    return fail("token id outside the vocabulary");
+  if (!want_logits && (logits_host || next_token_host))
+    return fail("hk_engine_step: outputs requested without want_logits");
+  HK_CHECK(hipSetDevice(e->device));
+  if (embedding_host != nullptr) {
+    HK_CHECK(hipMemcpyAsync(e->h, embedding_host, e->d.hidden * sizeof(uint16_t),
+                            hipMemcpyHostToDevice, e->stream));
+    HK_TRY(set_ctrl(e, -1, position, 0));
+  } else {
+    HK_TRY(set_ctrl(e, token, position, 0));
+  }
+  HK_TRY(run_step(e, want_logits != 0));
+  if (logits_host)
+    HK_CHECK(hipMemcpyAsync(logits_host, e->logits, (size_t)e->d.vocab * sizeof(float),
+                            hipMemcpyDeviceToHost, e->stream));
+  if (next_token_host)
+    HK_CHECK(hipMemcpyAsync(next_token_host, e->result, sizeof(int32_t), hipMemcpyDeviceToHost,
+                            e->stream));
+  if (embedding_host || logits_host || next_token_host) HK_CHECK(hipStreamSynchronize(e->stream));
+  return 0;
+}
+
+int hk_engine_generate(hk_engine* e, int32_t token, int32_t position, int32_t n_steps,
+                       int32_t* tokens_host) {
+  if (!e || !tokens_host) return fail("hk_engine_generate: null argument");
+  std::lock_guard<std::mutex> lock(e->mu);
+  if (n_steps <= 0) return fail("hk_engine_generate: n_steps must be positive");
+  if (position < 0 || (int64_t)position + n_steps > e->d.max_context)
+    return fail("position outside the " + std::to_string(e->d.max_context) + "-token context");
+  if (token < 0 || token >= e->d.vocab) return fail("token id outside the vocabulary");
+  HK_CHECK(hipSetDevice(e->device));
+  HK_TRY(set_ctrl(e, token, position, 1));
+  for (int i = 0; i < n_steps; ++i) HK_TRY(run_step(e, true));
+  HK_CHECK(hipMemcpyAsync(tokens_host, e->out_tokens, (size_t)n_steps * sizeof(int32_t),
+                          hipMemcpyDeviceToHost, e->stream));
+  HK_CHECK(hipStreamSynchronize(e->stream));
+  return 0;
+}
+
+int hk_engine_final_hidden(hk_engine* e, uint16_t* hidden_host) {
+  if (!e || !hidden_host) return fail("hk_engine_final_hidden: null argument");
+  std::lock_guard<std::mutex> lock(e->mu);
+  HK_CHECK(hipSetDevice(e->device));
+  HK_TRY(launch_rmsnorm(e->h, e->w.final_norm, e->d.rms_eps, e->normed, e->d.hidden, e->stream));
+  HK_CHECK(hipMemcpyAsync(hidden_host, e->normed, e->d.hidden * sizeof(uint16_t),
+                          hipMemcpyDeviceToHost, e->stream));
+  HK_CHECK(hipStreamSynchronize(e->stream));
+  return 0;
+}
+
+int hk_engine_launch_part(hk_engine* e, int32_t part, int32_t layer) {
+  if (!e) return fail("hk_engine_launch_part: null engine");
+  std::lock_guard<std::mutex> lock(e->mu);
+  if (part < HK_PART_QKV || part > HK_PART_HEAD) return fail("hk_engine_launch_part: unknown part");
+  if (layer < 0 || layer >= e->d.layers) return fail("hk_engine_launch_part: layer out of range");
+  HK_CHECK(hipSetDevice(e->device));
+  if (part == HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
+  return launch_part(e, part, layer);
+}
+
+int hk_engine_read_kv(hk_engine* e, int32_t layer, int32_t slot, uint16_t* k_host,
+                      uint16_t* v_host) {
+  if (!e || !k_host || !v_host) return fail("hk_engine_read_kv: null argument");
+  std::lock_guard<std::mutex> lock(e->mu);
+  if (layer < 0 || layer >= e->d.layers) return fail("hk_engine_read_kv: layer out of range");
+  if (slot < 0 || slot >= e->d.max_context) return fail("hk_engine_read_kv: slot out of range");
+  HK_CHECK(hipSetDevice(e->device));
+  HK_CHECK(hipStreamSynchronize(e->stream));
+  const size_t row = kHeadDim * sizeof(uint16_t);
+  for (int g = 0; g < e->d.kv_heads; ++g) {
+    const size_t off = (size_t)layer * kv_layer_elems(e) + ((size_t)g * e->d.max_context + slot) * kHeadDim;
+    HK_CHECK(hipMemcpy(k_host + g * kHeadDim, e->kcache + off, row, hipMemcpyDeviceToHost));
+    HK_CHECK(hipMemcpy(v_host + g * kHeadDim, e->vcache + off, row, hipMemcpyDeviceToHost));
+  }
+  return 0;
+}
+
+int hk_engine_reset(hk_engine* e) {
+  if (!e) return fail("hk_engine_reset: null engine");
+  std::lock_guard<std::mutex> lock(e->mu);
+  HK_CHECK(hipSetDevice(e->device));
+  const size_t kv = (size_t)e->d.layers * kv_layer_elems(e) * sizeof(uint16_t);
+  HK_CHECK(hipMemsetAsync(e->kcache, 0, kv, e->stream));
+  HK_CHECK(hipMemsetAsync(e->vcache, 0, kv, e->stream));
+  HK_CHECK(hipStreamSynchronize(e->stream));
+  return 0;
+}
+
+void* hk_engine_stream(hk_engine* e) { return e ? (void*)e->stream : nullptr; }
+
+void hk_engine_destroy(hk_engine* e) {
+  if (!e) return;
+  {
+    std::lock_guard<std::mutex> lock(e->mu);
+    (void)hipSetDevice(e->device);
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+  }
+  free_engine(e);
+}
+
+int hk_gemv_bf16(const uint16_t* W, const uint16_t* x, const float* bias,
+                 const uint16_t* residual, uint16_t* y, float* y_f32, int32_t M, int32_t K,
+                 void* stream) {
+  return gemv_common(W, nullptr, x, bias, residual, y, y_f32, M, K, false, stream);
+}
+
+int hk_gemv_w8(const int8_t* Wq, const float* scale, const uint16_t* x, const float* bias,
+               const uint16_t* residual, uint16_t* y, float* y_f32, int32_t M, int32_t K,
+               void* stream) {
+  return gemv_common(Wq, scale, x, bias, residual, y, y_f32, M, K, true, stream);
+}
+
+int hk_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* out, int32_t n,
+               void* stream) {
+  if (!x || !gamma || !out) return fail("hk_rmsnorm: null pointer");
+  return launch_rmsnorm(x, gamma, eps, out, n, static_cast<hipStream_t>(stream));
+}
+
+int hk_swiglu(const uint16_t* gate_up, uint16_t* act, int32_t intermediate, void* stream) {
+  if (!gate_up || !act) return fail("hk_swiglu: null pointer");
+  return launch_swiglu(gate_up, act, intermediate, static_cast<hipStream_t>(stream));
+}
+
+int hk_argmax_f32(const float* x, int32_t n, int32_t* index_device, void* stream) {
+  if (!x || !index_device) return fail("hk_argmax_f32: null pointer");
+  std::lock_guard<std::mutex> lock(g_op_mutex);
+  OpScratch* s = nullptr;
+  HK_TRY(op_scratch(&s, 0, 0));
+  return launch_argmax(x, n, s->am, index_device, static_cast<hipStream_t>(stream));
+}
+
+int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float* rope_sin,
+                        uint16_t* kcache, uint16_t* vcache, int32_t position,
+                        int32_t max_context, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, uint16_t* out, void* stream) {
+  if (!qkv || !rope_cos || !rope_sin || !kcache || !vcache || !out)
+    return fail("hk_attention_decode: null pointer");
+  if (head_dim != kHeadDim) {
+    set_error("hk_attention_decode: only head_dim 64 is supported");
+    return HK_ERR_UNSUPPORTED;
+  }
+  if (max_context <= 0 || position < 0 || position >= max_context)
+    return fail("hk_attention_decode: position outside the context");
+  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0)
+    return fail("hk_attention_decode: q_heads must be a multiple of kv_heads");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> lock(g_op_mutex);
+  const int splits = (max_context + kAttnChunk - 1) / kAttnChunk;
+  OpScratch* s = nullptr;
+  HK_TRY(op_scratch(&s, (size_t)kv_heads * splits * kMaxQPerKV * (kHeadDim + 2), kv_heads));
+  hipLaunchKernelGGL(store_i32_kernel, dim3(1), dim3(1), 0, st, s->position, position);
+  HK_CHECK(hipGetLastError());
+  AttnArgs a = {};
+  a.qkv = qkv;
+  a.cos_tab = rope_cos;
+  a.sin_tab = rope_sin;
+  a.kcache = kcache;
+  a.vcache = vcache;
+  a.position = s->position;
+  a.out = out;
+  a.partial = s->partial;
+  a.counters = s->counters;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.max_ctx = max_context;
+  a.max_splits = splits;
+  return launch_attention_decode(a, st);
+}
+
+int hk_stream_sync(void* stream) {
+  HK_CHECK(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  return 0;
+}
+
+int hk_malloc(uint64_t bytes, void** device_ptr) {
+  if (!device_ptr) return fail("hk_malloc: null output");
+  *device_ptr = nullptr;
+  if (bytes == 0) return fail("hk_malloc: zero bytes");
+  HK_CHECK(hipMalloc(device_ptr, bytes));
+  return 0;
+}
+
+int hk_free(void* device_ptr) {
+  if (device_ptr) HK_CHECK(hipFree(device_ptr));
+  return 0;
+}
+
+int hk_memcpy_h2d(void* device_dst, const void* host_src, uint64_t bytes) {
+  if (bytes == 0) return 0;
+  if (!device_dst || !host_src) return fail("hk_memcpy_h2d: null pointer");
+  HK_CHECK(hipMemcpy(device_dst, host_src, bytes, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int hk_memcpy_d2h(void* host_dst, const void* device_src, uint64_t bytes) {
+  if (bytes == 0) return 0;
+  if (!host_dst || !device_src) return fail("hk_memcpy_d2h: null pointer");
+  HK_CHECK(hipMemcpy(host_dst, device_src, bytes, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+int hk_memset(void* device_dst, int32_t value, uint64_t bytes) {
+  if (bytes == 0) return 0;
+  if (!device_dst) return fail("hk_memset: null pointer");
+  HK_CHECK(hipMemset(device_dst, value, bytes));
+  HK_CHECK(hipDeviceSynchronize());
+  return 0;
+}
+
+int hk_stream_create(void** stream) {
+  if (!stream) return fail("hk_stream_create: null output");
+  hipStream_t s = nullptr;
+  HK_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return 0;
+}
+
+int hk_stream_destroy(void* stream) {
+  if (stream) HK_CHECK(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return 0;
+}
+
+int hk_event_create(void** event) {
+  if (!event) return fail("hk_event_create: null output");
+  hipEvent_t ev = nullptr;
+  HK_CHECK(hipEventCreate(&ev));
+  *event = ev;
+  return 0;
+}
+
+int hk_event_destroy(void* event) {
+  if (event) HK_CHECK(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return 0;
+}
+
+int hk_event_record(void* event, void* stream) {
+  if (!event) return fail("hk_event_record: null event");
+  HK_CHECK(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)));
+  return 0;
+}
+
+int hk_event_elapsed_ms(void* start, void* end, float* ms) {
+  if (!start || !end || !ms) return fail("hk_event_elapsed_ms: null argument");
+  HK_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(end)));
+  HK_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)));
+  return 0;
+}
+
+}  // extern "C"

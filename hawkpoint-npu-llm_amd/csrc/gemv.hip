@@ -1,0 +1,280 @@
+// Batch-1 GEMV for the decode step: y = W @ x with W row-major BF16 or int8.
+//
+// Covers every projection of the reference's decode step
+// (npu_llm/runtime/cpu_backend.py:64-69 `project`, used by `layer` :131-171
+// and `logits` :173-181) and the W8 device formula of
+// npu_llm/kernels/project_w8bf16.cc:14-38.
+//
+// Mapping (wave64): `LPR` lanes share one output row; a wave owns 64/LPR rows
+// and a 256-thread workgroup 4 waves.  Each lane streams NJ 16-byte chunks of
+// its row (8 bf16 or 16 int8 weights per chunk) with non-temporal loads that
+// are issued *before* the prologue, so the RMSNorm/x staging latency hides
+// under the HBM fetch.  x lives in LDS as float32.  Partial sums are reduced
+// across the LPR lanes with butterfly shuffles.
+//
+// Rounding points follow the reference exactly:
+//   EPI_BF16   bf16(acc)                         project()
+//   EPI_BIAS   bf16(f32(bf16(acc)) + bias)       cpu_backend.py:140-143
+//   EPI_RESID  bf16(f32(bf16(acc)) + f32(res))   cpu_backend.py:145-150, 166-171
+//   EPI_F32    acc (no rounding)                 cpu_backend.py:179-181
+//   EPI_SWIGLU bf16((g / (1 + exp(-clip(g)))) * u) on bf16 g, u   :154-165
+// W8 rows are dequantised after accumulation: acc * scale[row], then as above.
+#include "hk_common.h"
+#include "hk_internal.h"
+
+namespace hk {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+// Stage x (optionally RMS-normalised) into LDS as float32.
+// RMSNorm follows cpu_backend.py:71-76: v = f32(bf16 x); mean of v*v in f32;
+// inv = 1 / sqrt(mean + eps); out = bf16((v * inv) * gamma).
+__device__ __forceinline__ void stage_x(const GemvArgs& a, float* xs, float* red) {
+  const int tid = threadIdx.x;
+  const int K = a.K;
+  const uint16_t* x = a.x;
+  bool copy = false;
+  if (a.x_index != nullptr) {
+    int t = *a.x_index;
+    if (t >= 0) {
+      if (t >= a.vocab_limit) t = a.vocab_limit - 1;
+      x = a.x_table + (size_t)t * (size_t)K;
+      copy = (a.x_copy != nullptr) && blockIdx.x == 0;
+    }
+  }
+  const uint32_t* x2 = reinterpret_cast<const uint32_t*>(x);
+  float ss = 0.0f;
+  for (int i = tid; i < K / 2; i += kThreads) {
+    const uint32_t w = x2[i];
+    const float v0 = bf_lo(w), v1 = bf_hi(w);
+    xs[2 * i] = v0;
+    xs[2 * i + 1] = v1;
+    if (copy) reinterpret_cast<uint32_t*>(a.x_copy)[i] = w;
+    ss += v0 * v0;
+    ss += v1 * v1;
+  }
+  if (a.pro != PRO_NORM) return;
+  ss = group_sum<64>(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float total = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) total += red[w];
+  const float mean = total / (float)K;
+  const float inv = 1.0f / sqrtf(mean + a.eps);
+  const uint32_t* g2 = reinterpret_cast<const uint32_t*>(a.gamma);
+  for (int i = tid; i < K / 2; i += kThreads) {
+    const uint32_t g = g2[i];
+    xs[2 * i] = round_bf16((xs[2 * i] * inv) * bf_lo(g));
+    xs[2 * i + 1] = round_bf16((xs[2 * i + 1] * inv) * bf_hi(g));
+  }
+}
+
+template <bool W8>
+__device__ __forceinline__ void fma_chunk(const u32x4 w, const float* xs, int c, float& a0,
+                                          float& a1) {
+  if constexpr (!W8) {
+    const float4* xv = reinterpret_cast<const float4*>(xs + c * 8);
+    const float4 p = xv[0], q = xv[1];
+    a0 = fmaf(bf_lo(w.x), p.x, a0);
+    a1 = fmaf(bf_hi(w.x), p.y, a1);
+    a0 = fmaf(bf_lo(w.y), p.z, a0);
+    a1 = fmaf(bf_hi(w.y), p.w, a1);
+    a0 = fmaf(bf_lo(w.z), q.x, a0);
+    a1 = fmaf(bf_hi(w.z), q.y, a1);
+    a0 = fmaf(bf_lo(w.w), q.z, a0);
+    a1 = fmaf(bf_hi(w.w), q.w, a1);
+  } else {
+    const float4* xv = reinterpret_cast<const float4*>(xs + c * 16);
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 p = xv[k];
+      const int32_t v = (int32_t)words[k];
+      a0 = fmaf((float)((v << 24) >> 24), p.x, a0);
+      a1 = fmaf((float)((v << 16) >> 24), p.y, a1);
+      a0 = fmaf((float)((v << 8) >> 24), p.z, a0);
+      a1 = fmaf((float)(v >> 24), p.w, a1);
+    }
+  }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float clipped = fminf(fmaxf(g, -80.0f), 80.0f);
+  const float denom = 1.0f + expf(-clipped);
+  return (g / denom) * u;
+}
+
+template <int LPR, int NJ, bool W8, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+  extern __shared__ float smem[];
+  float* xs = smem;
+  float* red = smem + a.K;
+  __shared__ unsigned long long wave_keys[kWaves];
+
+  constexpr int RPW = 64 / LPR;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l = lane % LPR;
+  const int row = (blockIdx.x * kWaves + wave) * RPW + lane / LPR;
+  const bool live = row < a.M;
+  const int CH = W8 ? (a.K >> 4) : (a.K >> 3);
+  const size_t row_bytes = W8 ? (size_t)a.K : (size_t)a.K * 2;
+  const char* wrow = static_cast<const char*>(a.W) + (size_t)(live ? row : 0) * row_bytes;
+  const char* urow = wrow + (size_t)a.M * row_bytes;
+
+  u32x4 w[NJ];
+  u32x4 u[PAIR ? NJ : 1];
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  auto load_batch = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = base + l + j * LPR;
+      const bool ok = live && c < CH;
+      w[j] = ok ? load_stream16(wrow + (size_t)c * 16) : zero;
+      if constexpr (PAIR) u[j] = ok ? load_stream16(urow + (size_t)c * 16) : zero;
+    }
+  };
+
+  float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+  int base = 0;
+  load_batch(base);
+  stage_x(a, xs, red);
+  __syncthreads();
+  for (;;) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = base + l + j * LPR;
+      if (c < CH) {
+        fma_chunk<W8>(w[j], xs, c, a0, a1);
+        if constexpr (PAIR) fma_chunk<W8>(u[j], xs, c, b0, b1);
+      }
+    }
+    base += LPR * NJ;
+    if (base >= CH) break;
+    load_batch(base);
+  }
+
+  float acc = group_sum<LPR>(a0 + a1);
+  float accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
+  if constexpr (W8) {
+    if (live) {
+      acc = acc * a.scale[row];
+      if constexpr (PAIR) accu = accu * a.scale[row + a.M];
+    }
+  }
+
+  if (a.epi == EPI_F32_ARGMAX) {
+    if (live && l == 0) a.yf[row] = acc;
+    unsigned long long key = (live && l == 0) ? argmax_key(acc, (uint32_t)row) : 0ull;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) key = umax64(key, shfl_xor_u64(key, m));
+    if (lane == 0) wave_keys[wave] = key;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long k = wave_keys[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; ++i) k = umax64(k, wave_keys[i]);
+      atomicMax(&a.am->key, k);
+      __threadfence();
+      const unsigned int ticket = atomicAdd(&a.am->count, 1u);
+      if (ticket == gridDim.x - 1) {
+        __threadfence();
+        const unsigned long long final_key = atomicAdd(&a.am->key, 0ull);
+        const int32_t index = (int32_t)argmax_key_index(final_key);
+        if (a.token_out) *a.token_out = index;
+        if (a.ctrl != nullptr && a.ctrl->advance) {
+          StepCtrl* c = a.ctrl;
+          if (a.out_tokens && c->n_out >= 0 && c->n_out < a.out_cap) a.out_tokens[c->n_out] = index;
+          c->n_out = c->n_out + 1;
+          c->token = index;
+          c->position = c->position + 1;
+        }
+        atomicExch(&a.am->key, 0ull);
+        atomicExch(&a.am->count, 0u);
+      }
+    }
+    return;
+  }
+
+  if (!live || l != 0) return;
+  switch (a.epi) {
+    case EPI_BF16:
+      a.y[row] = (uint16_t)f32_to_bf16(acc);
+      break;
+    case EPI_BIAS:
+      a.y[row] = (uint16_t)f32_to_bf16(round_bf16(acc) + a.bias[row]);
+      break;
+    case EPI_RESID:
+      a.y[row] = (uint16_t)f32_to_bf16(round_bf16(acc) + bf16_to_f32(a.resid[row]));
+      break;
+    case EPI_F32:
+      a.yf[row] = acc;
+      break;
+    case EPI_SWIGLU:
+      a.y[row] = (uint16_t)f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu)));
+      break;
+    default:
+      break;
+  }
+}
+
+template <int LPR, int NJ, bool W8, bool PAIR>
+int launch_cfg(const GemvArgs& a, hipStream_t stream) {
+  constexpr int rows_per_block = kWaves * (64 / LPR);
+  const int blocks = (a.M + rows_per_block - 1) / rows_per_block;
+  const size_t lds = (size_t)(a.K + 8) * sizeof(float);
+  hipLaunchKernelGGL((gemv_kernel<LPR, NJ, W8, PAIR>), dim3(blocks), dim3(kThreads), lds, stream,
+                     a);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "gemv launch");
+}
+
+template <int LPR, bool W8, bool PAIR>
+int launch_nj(int nj, const GemvArgs& a, hipStream_t stream) {
+  if (nj <= 6) return launch_cfg<LPR, 6, W8, PAIR>(a, stream);
+  if (nj <= 7) return launch_cfg<LPR, 7, W8, PAIR>(a, stream);
+  if (nj <= 8) return launch_cfg<LPR, 8, W8, PAIR>(a, stream);
+  if (nj <= 10) return launch_cfg<LPR, 10, W8, PAIR>(a, stream);
+  return launch_cfg<LPR, 12, W8, PAIR>(a, stream);
+}
+
+template <bool W8, bool PAIR>
+int launch_shape(const GemvArgs& a, hipStream_t stream) {
+  const int CH = W8 ? a.K / 16 : a.K / 8;
+  // Fewest lanes per row that keep every lane's chunk count at or below 12;
+  // very long rows fall back to 64 lanes with several passes of 8 chunks.
+  if ((CH + 7) / 8 <= 12) return launch_nj<8, W8, PAIR>((CH + 7) / 8, a, stream);
+  if ((CH + 15) / 16 <= 12) return launch_nj<16, W8, PAIR>((CH + 15) / 16, a, stream);
+  if ((CH + 31) / 32 <= 12) return launch_nj<32, W8, PAIR>((CH + 31) / 32, a, stream);
+  if ((CH + 63) / 64 <= 12) return launch_nj<64, W8, PAIR>((CH + 63) / 64, a, stream);
+  return launch_cfg<64, 8, W8, PAIR>(a, stream);
+}
+
+}  // namespace
+
+int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream) {
+  if (a.M <= 0 || a.K <= 0) return fail("gemv: M and K must be positive");
+  if (a.K % (w8 ? 16 : 8) != 0)
+    return fail(w8 ? "gemv: K must be a multiple of 16 for int8 weights"
+                   : "gemv: K must be a multiple of 8 for bf16 weights");
+  if (a.K > 16384) return fail("gemv: K above 16384 is not supported");
+  if (a.pro == PRO_NORM && a.gamma == nullptr) return fail("gemv: RMSNorm needs gamma");
+  if (w8 && a.scale == nullptr) return fail("gemv: int8 weights need per-row scales");
+  const bool pair = a.epi == EPI_SWIGLU;
+  if ((a.epi == EPI_F32 || a.epi == EPI_F32_ARGMAX) && a.yf == nullptr)
+    return fail("gemv: float32 output missing");
+  if (a.epi != EPI_F32 && a.epi != EPI_F32_ARGMAX && a.y == nullptr)
+    return fail("gemv: bf16 output missing");
+  if (a.epi == EPI_BIAS && a.bias == nullptr) return fail("gemv: bias missing");
+  if (a.epi == EPI_RESID && a.resid == nullptr) return fail("gemv: residual missing");
+  if (a.epi == EPI_F32_ARGMAX && a.am == nullptr) return fail("gemv: argmax state missing");
+  if (w8) return pair ? launch_shape<true, true>(a, stream) : launch_shape<true, false>(a, stream);
+  return pair ? launch_shape<false, true>(a, stream) : launch_shape<false, false>(a, stream);
+}
+
+}  // namespace hk

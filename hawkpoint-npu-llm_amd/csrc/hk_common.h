@@ -1,0 +1,86 @@
+// Device-side helpers shared by every hk kernel (gfx950, wave64).
+//
+// BF16 values travel as uint16 bit patterns.  The float32 -> bfloat16 cast is
+// round-to-nearest-even with a quiet-NaN branch, the same rounding the
+// reference's CPU runtime gets from ml_dtypes (npu_llm/runtime/cpu_backend.py:7-8)
+// and writes out as integer code in npu_llm/kernels/qwen_engine_common.h:35-46.
+//
+// All hk sources are compiled with -ffp-contract=off, so a*b+c below is two
+// rounded operations exactly as NumPy evaluates it; fused multiply-adds are
+// written out as fmaf() where the reference's summation order is not fixed
+// anyway (dot products).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hk {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) & 0x8000u) | 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+// Low / high bf16 of a packed 32-bit word (element 2i is the low half).
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Streaming 16-byte load that does not allocate in the caches: every weight
+// byte is read exactly once per decode step.
+__device__ __forceinline__ u32x4 load_stream16(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Butterfly sum over groups of `width` adjacent lanes (width a power of two).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = width / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int m = width / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Order-preserving 64-bit key for argmax: larger logit wins; on equal logits
+// the lower index wins (np.argmax returns the first maximum).  -0.0 is folded
+// into +0.0 so the two compare equal, as they do in NumPy.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
+  v = v + 0.0f;
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - index);
+}
+
+__device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
+  return 0xffffffffu - (uint32_t)(key & 0xffffffffu);
+}
+
+}  // namespace hk

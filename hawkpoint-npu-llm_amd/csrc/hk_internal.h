@@ -1,0 +1,103 @@
+// Host-side declarations shared between the hk translation units: kernel
+// argument blocks and the launch functions each .hip file exports.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace hk {
+
+// Per-thread error message behind hk_last_error().
+void set_error(const std::string& message);
+int fail(const std::string& message);           // set_error + return HK_ERR_INVALID
+int hip_fail(hipError_t err, const char* what);  // set_error + return HK_ERR_HIP
+
+// Result of the last-workgroup argmax reduction (see argmax_key in
+// hk_common.h).  `key` and `count` must be zero before a launch that uses
+// them; the last workgroup of that launch leaves them zero again.
+struct ArgmaxState {
+  unsigned long long key;
+  unsigned int count;
+  unsigned int pad;
+};
+
+// Decode-step control block, read by the kernels of a captured step so the
+// same graph serves every position.
+struct StepCtrl {
+  int32_t token;     // token whose embedding row feeds layer 0; -1: hidden preloaded
+  int32_t position;  // KV slot written and last slot attended
+  int32_t n_out;     // tokens emitted so far by device-driven decode
+  int32_t advance;   // 1: the LM head writes its argmax to `token` and bumps `position`
+};
+
+enum GemvEpilogue : int {
+  EPI_BF16 = 0,        // y = bf16(acc)
+  EPI_BIAS = 1,        // y = bf16(f32(bf16(acc)) + bias)
+  EPI_RESID = 2,       // y = bf16(f32(bf16(acc)) + f32(resid))
+  EPI_F32 = 3,         // yf = acc (unrounded)
+  EPI_F32_ARGMAX = 4,  // yf = acc, plus argmax over all rows into `am`
+  EPI_SWIGLU = 5,      // rows i and M+i: y = bf16(silu(bf16(g)) * bf16(u))
+};
+
+enum GemvPrologue : int {
+  PRO_PLAIN = 0,  // x as given
+  PRO_NORM = 1,   // x = bf16((v * inv_rms) * gamma), the reference's RMSNorm
+};
+
+struct GemvArgs {
+  const void* W;             // [rows, K] bf16 bits, or int8 when w8
+  const float* scale;        // [rows] per-row dequant scale (w8)
+  const uint16_t* x;         // [K] bf16 input
+  const int32_t* x_index;    // optional: x = x_table + (*x_index) * K when *x_index >= 0
+  const uint16_t* x_table;
+  uint16_t* x_copy;          // optional: workgroup 0 stores the looked-up x row here
+  const uint16_t* gamma;     // [K] RMSNorm gain (PRO_NORM)
+  float eps;
+  const float* bias;         // [M] (EPI_BIAS)
+  const uint16_t* resid;     // [M] (EPI_RESID)
+  uint16_t* y;               // [M] bf16 output
+  float* yf;                 // [M] f32 output
+  ArgmaxState* am;           // EPI_F32_ARGMAX
+  StepCtrl* ctrl;            // EPI_F32_ARGMAX: optional token feedback
+  int32_t* out_tokens;       // EPI_F32_ARGMAX: optional emitted-token log
+  int32_t* token_out;        // EPI_F32_ARGMAX: optional single result
+  int out_cap;               // capacity of out_tokens
+  int M, K, vocab_limit;
+  int pro, epi;
+};
+
+// Launches y = W @ x with the given prologue/epilogue.  Returns 0 or an
+// hk error code (message via set_error).
+int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream);
+
+struct AttnArgs {
+  const uint16_t* qkv;       // [(Hq + 2 Hkv) * 64] bf16: q heads, k heads, v heads
+  const float* cos_tab;      // [max_ctx, 32]
+  const float* sin_tab;      // [max_ctx, 32]
+  uint16_t* kcache;          // this layer: [Hkv, max_ctx, 64] bf16
+  uint16_t* vcache;          // this layer: [Hkv, max_ctx, 64] bf16
+  const int32_t* position;   // device scalar
+  uint16_t* out;             // [Hq * 64] bf16
+  float* partial;            // [Hkv, max_splits, qpk, 66] split-KV partials
+  unsigned int* counters;    // [Hkv] zero between launches
+  int q_heads, kv_heads, max_ctx, max_splits;
+};
+
+constexpr int kHeadDim = 64;
+constexpr int kAttnChunk = 256;  // positions per split-KV workgroup
+constexpr int kMaxQPerKV = 16;
+
+int launch_attention_decode(const AttnArgs& a, hipStream_t stream);
+
+// Standalone RMSNorm: out = bf16((v * inv_rms) * gamma).
+int launch_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* out,
+                   int n, hipStream_t stream);
+// Elementwise SwiGLU over a [2I] gate|up vector.
+int launch_swiglu(const uint16_t* gate_up, uint16_t* act, int inter, hipStream_t stream);
+// Argmax over n float32 values (first maximum).
+int launch_argmax(const float* x, int n, ArgmaxState* am, int32_t* out_index,
+                  hipStream_t stream);
+
+}  // namespace hk

@@ -1,0 +1,211 @@
+/* hk -- MI355X (gfx950) decode engine: the C ABI of libhk.so.
+ *
+ * Plain C types only: device pointers are `const void*` / typed pointers into
+ * HIP device memory, streams are `void*` (a hipStream_t, NULL = the default
+ * stream), host buffers are ordinary pointers.  Every function returns 0 on
+ * success or one of the HK_ERR_* codes; hk_last_error() then holds a message
+ * for the calling thread.  Calls on one engine must be serialised by the
+ * caller (the reference serialises its decoder behind one lock,
+ * npu_llm/api_server.py:559, 657); the engine also takes its own mutex.
+ *
+ * BF16 tensors are uint16 bit patterns.  Weight tensors use the reference's
+ * package layout (npu_llm/tools/convert_smollm2.py:220-311): qkv rows are
+ * q heads, k heads, v heads; gate_up rows are gate then up; row-major [M, K];
+ * int8 weights carry a float32 scale per output row (convert_smollm2.py:81-86).
+ */
+#ifndef HK_H
+#define HK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HK_OK 0
+#define HK_ERR_INVALID 1     /* bad argument: the reference raises ValueError */
+#define HK_ERR_HIP 2         /* HIP runtime error: the reference's RuntimeError */
+#define HK_ERR_UNSUPPORTED 3 /* shape or device this build does not handle */
+
+#define HK_MODEL_QKV_BIAS 1u /* layers carry a float32 qkv bias */
+#define HK_MODEL_W8 2u       /* layer projections are int8 + per-row scale */
+
+typedef struct hk_engine hk_engine;
+
+/* Model shape; fields as in the package metadata.json
+ * (npu_llm/tools/convert_smollm2.py:188-210). */
+typedef struct hk_model_desc {
+  int32_t layers;
+  int32_t hidden;       /* hidden_size */
+  int32_t intermediate; /* intermediate_size */
+  int32_t q_heads;      /* attention_heads */
+  int32_t kv_heads;
+  int32_t head_dim;     /* must be 64 */
+  int32_t vocab;        /* vocab_size */
+  int32_t max_context;  /* KV slots allocated per layer and head */
+  float rms_eps;        /* rms_norm_eps, as float32 */
+  uint32_t flags;       /* HK_MODEL_* */
+} hk_model_desc;
+
+/* Device pointers of one decoder layer (names as in the package manifest). */
+typedef struct hk_layer_weights {
+  const void* qkv;          /* [(Hq + 2 Hkv) * D, H] bf16 or int8 */
+  const float* qkv_scale;   /* [(Hq + 2 Hkv) * D] (W8) */
+  const float* qkv_bias;    /* [(Hq + 2 Hkv) * D] float32 (HK_MODEL_QKV_BIAS) */
+  const void* o_proj;       /* [H, Hq * D] */
+  const float* o_scale;
+  const void* gate_up;      /* [2 I, H]: gate rows then up rows */
+  const float* gate_up_scale;
+  const void* down_proj;    /* [H, I] */
+  const float* down_scale;
+  const uint16_t* input_norm;     /* [H] bf16 */
+  const uint16_t* post_attn_norm; /* [H] bf16 */
+} hk_layer_weights;
+
+typedef struct hk_model_weights {
+  const uint16_t* token_embedding; /* [V, H] bf16 */
+  const uint16_t* lm_head;         /* [V, H] bf16 (the embedding when tied) */
+  const uint16_t* final_norm;      /* [H] bf16 */
+  const float* rope_cos;           /* [max_context, D/2]: np.cos(f32(p) * inv_freq) */
+  const float* rope_sin;           /* [max_context, D/2]: np.sin(f32(p) * inv_freq) */
+  const hk_layer_weights* layers;  /* host array of `layers` entries */
+} hk_model_weights;
+
+/* Version of this ABI (bumped on any incompatible change). */
+int32_t hk_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* hk_last_error(void);
+
+/* Select the HIP device and check it is a gfx950 (MI355X).
+ * Replaces set_current_device(from_name("npu", n_cols=4)),
+ * npu_llm/runtime/generate.py:131-132. */
+int hk_init(int32_t device_ordinal);
+
+/* Build a decode engine over caller-owned device weights (the caller keeps
+ * them alive until hk_engine_destroy).  The engine allocates its own KV cache,
+ * activations, logits and a stream.  Replaces QwenDecoderEngine.__init__
+ * (npu_llm/runtime/qwen_engine.py:41-63) and DecoderEngine.__init__
+ * (npu_llm/runtime/engine.py:32-49). */
+int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
+                     hk_engine** out);
+
+/* One decode step at `position`: every layer for one token, KV appended at
+ * slot `position`, attention over slots 0..position.  The token's embedding
+ * row comes from the device table, or from `embedding_host` ([H] bf16) when
+ * that is non-NULL.  With `want_logits` the final RMSNorm, LM head and argmax
+ * run too; `logits_host` ([V] float32) and `next_token_host` receive them.
+ * Without outputs the call returns without waiting for the GPU.
+ * Replaces QwenDecoderEngine.step (npu_llm/runtime/qwen_engine.py:77-94) and
+ * the device program qwen_engine(...) (npu_llm/designs/qwen_engine.py:72-81).
+ * HK_ERR_INVALID if position is outside [0, max_context) or token outside
+ * [0, vocab) (the reference's ValueError, qwen_engine.py:84-85). */
+int hk_engine_step(hk_engine* engine, int32_t token, int32_t position, int32_t want_logits,
+                   const uint16_t* embedding_host, float* logits_host,
+                   int32_t* next_token_host);
+
+/* Greedy decode of `n_steps` tokens without host round trips: step i feeds
+ * the argmax of step i-1, starting from `token` at `position`.  Writes the
+ * n_steps emitted token ids to `tokens_host`.  Equivalent to n_steps calls of
+ * hk_engine_step with argmax selection (npu_llm/runtime/generate.py:1130-1158
+ * with the greedy sampler). */
+int hk_engine_generate(hk_engine* engine, int32_t token, int32_t position, int32_t n_steps,
+                       int32_t* tokens_host);
+
+/* Final-RMSNorm output ([H] bf16) of the hidden state left by the last step:
+ * the value DecoderEngine.step returns (npu_llm/runtime/engine.py:65-82). */
+int hk_engine_final_hidden(hk_engine* engine, uint16_t* hidden_host);
+
+/* Copy KV-cache slot `slot` of layer `layer` to the host: k_host and v_host
+ * each receive [kv_heads, 64] bf16.  The reference keeps this cache on the
+ * host and reads it back as a view (runtime/qwen_engine.py:60-63, 92-93). */
+int hk_engine_read_kv(hk_engine* engine, int32_t layer, int32_t slot, uint16_t* k_host,
+                      uint16_t* v_host);
+
+/* Parts of one decode step, in launch order within a layer. */
+#define HK_PART_QKV 0       /* RMSNorm + qkv projection + bias */
+#define HK_PART_ATTENTION 1 /* RoPE + KV append + GQA attention */
+#define HK_PART_O 2         /* o_proj + residual */
+#define HK_PART_GATE_UP 3   /* RMSNorm + gate/up projection + SwiGLU */
+#define HK_PART_DOWN 4      /* down_proj + residual */
+#define HK_PART_HEAD 5      /* final RMSNorm + LM head + argmax */
+
+/* Enqueue one part of the step for `layer` on the engine stream, without
+ * waiting, using the token/position of the last step.  For timing single
+ * kernels with events on hk_engine_stream(); the head's token feedback is
+ * switched off.  No reference counterpart: the NPU engine runs its step as
+ * one opaque dispatch (designs/qwen_engine.py:72-341). */
+int hk_engine_launch_part(hk_engine* engine, int32_t part, int32_t layer);
+
+/* Zero the KV cache (QwenDecoderEngine.reset, qwen_engine.py:65-66). */
+int hk_engine_reset(hk_engine* engine);
+
+/* The engine's HIP stream (hipStream_t), for timing with events. */
+void* hk_engine_stream(hk_engine* engine);
+
+/* Release everything the engine allocated; NULL is accepted
+ * (QwenDecoderEngine.close, qwen_engine.py:96-102). */
+void hk_engine_destroy(hk_engine* engine);
+
+/* ---- single operations (device pointers; asynchronous on `stream`) ---- */
+
+/* y = W @ x for bf16 W [M, K], bf16 x [K].  Outputs: `y_f32` receives the
+ * unrounded float32 sums when non-NULL; otherwise `y` receives
+ * bf16(f32(bf16(acc)) + bias) with `bias` (float32 [M]) or `residual`
+ * (bf16 [M]) added when given (at most one).  Replaces the reference's BF16
+ * projection (npu_llm/runtime/cpu_backend.py:64-69; designs/project_bf16.py). */
+int hk_gemv_bf16(const uint16_t* W, const uint16_t* x, const float* bias,
+                 const uint16_t* residual, uint16_t* y, float* y_f32, int32_t M, int32_t K,
+                 void* stream);
+
+/* W8 form: acc = sum_k f32(Wq[m,k]) * f32(x[k]); value = acc * scale[m]; then
+ * as hk_gemv_bf16.  Replaces project_w8bf16_acc32 + project_dequant_bf16
+ * (npu_llm/kernels/project_w8bf16.cc:14-38; designs/project.py:21-108). */
+int hk_gemv_w8(const int8_t* Wq, const float* scale, const uint16_t* x, const float* bias,
+               const uint16_t* residual, uint16_t* y, float* y_f32, int32_t M, int32_t K,
+               void* stream);
+
+/* out = bf16((v * inv_rms) * gamma) (cpu_backend.py:71-76; designs/rmsnorm.py). */
+int hk_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* out, int32_t n,
+               void* stream);
+
+/* act[i] = bf16((g / (1 + exp(-clip(g, -80, 80)))) * u) over gate_up = [g | u]
+ * (cpu_backend.py:154-165; designs/elementwise.py swiglu). */
+int hk_swiglu(const uint16_t* gate_up, uint16_t* act, int32_t intermediate, void* stream);
+
+/* index of the first maximum of x[0..n) (np.argmax, generate.py:709-714). */
+int hk_argmax_f32(const float* x, int32_t n, int32_t* index_device, void* stream);
+
+/* RoPE + KV append + GQA attention for one layer at `position`
+ * (cpu_backend.py:95-129).  kcache/vcache: [kv_heads, max_context, 64] bf16;
+ * cos/sin: [max_context, 32] float32; out: [q_heads * 64] bf16. */
+int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float* rope_sin,
+                        uint16_t* kcache, uint16_t* vcache, int32_t position,
+                        int32_t max_context, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, uint16_t* out, void* stream);
+
+/* Wait for all work on `stream`. */
+int hk_stream_sync(void* stream);
+
+/* ---- device memory, streams and events (the engine's buffer plumbing) ----
+ * They stand in for the reference's XRT buffer objects (iron.tensor /
+ * iron.zeros, npu_llm/runtime/qwen_engine.py:52-59) so a host needs no other
+ * GPU library.  Copies are synchronous. */
+int hk_malloc(uint64_t bytes, void** device_ptr);
+int hk_free(void* device_ptr);
+int hk_memcpy_h2d(void* device_dst, const void* host_src, uint64_t bytes);
+int hk_memcpy_d2h(void* host_dst, const void* device_src, uint64_t bytes);
+int hk_memset(void* device_dst, int32_t value, uint64_t bytes);
+int hk_stream_create(void** stream);
+int hk_stream_destroy(void* stream);
+int hk_event_create(void** event);
+int hk_event_destroy(void* event);
+int hk_event_record(void* event, void* stream);
+/* Milliseconds between two recorded events (waits for `end`). */
+int hk_event_elapsed_ms(void* start, void* end, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HK_H */

@@ -1,0 +1,48 @@
+"""The C ABI library loads and exports every function include/hk.h declares,
+and the ctypes binding covers exactly that set.  No GPU work is done."""
+
+import ctypes
+import re
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "hk.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(hk_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_the_engine_surface():
+    names = _declared()
+    for required in ("hk_init", "hk_engine_create", "hk_engine_step", "hk_engine_generate",
+                     "hk_engine_reset", "hk_engine_destroy", "hk_gemv_bf16", "hk_gemv_w8",
+                     "hk_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from runtime import hip
+
+    assert hip.LIB_PATH.is_file(), "build libhk.so first (python hawkpoint-npu-llm_amd/csrc/build.py)"
+    lib = ctypes.CDLL(str(hip.LIB_PATH))
+    missing = [n for n in sorted(_declared()) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_matches_header():
+    from runtime import hip
+
+    assert set(hip.EXPORTED) == _declared()
+
+
+def test_error_path_without_gpu_work():
+    from runtime import hip
+
+    lib = hip.lib()
+    assert lib.hk_abi_version() == 1
+    # null arguments are rejected before any device call
+    rc = lib.hk_engine_create(None, None, None)
+    assert rc == hip.HK_ERR_INVALID
+    assert "null" in hip.last_error()

@@ -1,0 +1,136 @@
+"""Whole-model decode parity on the GPU: the hk engine against the oracle
+(the reference's NumPy BF16 CPU runtime restated in oracle/).
+
+Protocol (the reference's own gates, npu_llm/tests/validate_qwen_tokens.py and
+validate_engine_npu.py):
+- teacher-forced: both sides see the oracle's token sequence; per-step logits
+  must agree within rel-L2 <= 1e-2 and the argmax must agree unless the
+  oracle's top-2 gap is below 2**-7 relative (a bf16 near-tie);
+- free-running greedy: the engine's own generated ids equal the oracle's up to
+  the first near-tie step;
+- KV slot indexing: slot p is written at step p only (slots above the last
+  position stay zero after a reset) and holds the oracle's values.
+"""
+
+import numpy as np
+import pytest
+
+from _util import announce, near_tie, rel_l2
+from oracle import bf16
+from oracle.cpu_backend import OracleDecoder
+from runtime.synthetic import QWEN25_05B, SMOLLM2_135M, SyntheticModel
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qwen_model():
+    return SyntheticModel(QWEN25_05B, seed=0)
+
+
+@pytest.fixture(scope="module")
+def smol_model():
+    return SyntheticModel(SMOLLM2_135M, seed=0)
+
+
+def _prompt(vocab, n, seed):
+    rng = np.random.default_rng(seed)
+    return [int(t) for t in rng.integers(0, vocab, n)]
+
+
+def _check_decode(model, prompt, new_tokens, context, *, w8=False, label=""):
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce(f"engine parity {label}: prompt {len(prompt)} new {new_tokens} ctx {context} w8={w8}")
+    oracle = OracleDecoder(model, context, w8=w8)
+    ref_tokens, ref_logits = oracle.generate_greedy(prompt, new_tokens)
+    engine = QwenDecoderEngine(model, context_length=context, w8=w8)
+    try:
+        # teacher-forced per-step logits
+        seq = list(prompt) + ref_tokens[:-1]
+        last = len(prompt) - 1
+        errors, mismatches = [], []
+        for pos, tok in enumerate(seq):
+            want = pos >= last
+            got_tok, got_logits = engine.step_token(tok, pos, logits=want)
+            if not want:
+                continue
+            i = pos - last
+            ref = ref_logits[i]
+            errors.append(rel_l2(got_logits, ref))
+            if got_tok != int(np.argmax(ref)) and not near_tie(ref):
+                mismatches.append((pos, got_tok, int(np.argmax(ref))))
+        announce(f"  max rel-L2 {max(errors):.3e}, argmax mismatches {mismatches}")
+        assert max(errors) <= 1e-2
+        assert not mismatches
+
+        # free-running greedy through the device-driven loop
+        engine.reset()
+        for pos, tok in enumerate(prompt[:-1]):
+            engine.step_token(tok, pos, logits=False)
+        gen = engine.generate(prompt[-1], len(prompt) - 1, new_tokens)
+        for i, (a, b) in enumerate(zip(gen, ref_tokens)):
+            if a != b:
+                assert near_tie(ref_logits[i]), f"token {i}: gpu {a} oracle {b}"
+                break
+        announce(f"  greedy ids match: {gen == ref_tokens}")
+
+        # KV slot indexing after the free run: slots written = positions used
+        last_pos = len(prompt) - 1 + new_tokens - 1
+        stage = oracle.stage
+        for layer in (0, model.metadata["layers"] - 1):
+            for slot in (0, len(prompt) - 1, last_pos - 1):
+                k, v = engine.read_kv(layer, slot)
+                assert np.any(k != 0) and np.any(v != 0)
+                ok = np.abs(bf16.from_bits(k) - bf16.from_bits(stage.key_cache[layer][:, slot]))
+                assert ok.max() <= 0.05 * np.abs(bf16.from_bits(stage.key_cache[layer][:, slot])).max() + 1e-3
+            if last_pos + 1 < context:
+                k, v = engine.read_kv(layer, last_pos + 1)
+                assert np.all(k == 0) and np.all(v == 0)
+    finally:
+        engine.close()
+
+
+def test_smollm_135m_shape_decode(smol_model):
+    """SmolLM2-135M shape: 35-token prompt, greedy 16 tokens, 64-slot context."""
+    _check_decode(smol_model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m")
+
+
+def test_qwen_05b_shape_decode(qwen_model):
+    """Qwen2.5-0.5B shape: 40-token prompt, greedy 32 tokens (slots 0..70)."""
+    _check_decode(qwen_model, _prompt(151936, 40, 12), 32, 72, label="qwen2.5-0.5b")
+
+
+def test_qwen_05b_shape_w8_decode(qwen_model):
+    """W8 layer projections (int8 + per-row scale), bf16 LM head."""
+    _check_decode(qwen_model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen2.5-0.5b-w8")
+
+
+def test_long_context_split_kv():
+    """Positions past 256 take the split-KV attention path (several chunks
+    merged by log-sum-exp); 2-layer model keeps the oracle quick."""
+    model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
+    _check_decode(model, _prompt(151936, 600, 14), 8, 4096, label="qwen2-layer-ctx4096")
+
+
+def test_step_contract_errors(qwen_model):
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("engine step contract errors")
+    model = SyntheticModel(QWEN25_05B, seed=1, layers=1)
+    engine = QwenDecoderEngine(model, context_length=8)
+    try:
+        with pytest.raises(ValueError):
+            engine.step_token(0, 8)
+        with pytest.raises(ValueError):
+            engine.step_token(0, -1)
+        with pytest.raises(ValueError):
+            engine.step_token(151936, 0)
+        # embedding-row form equals the token form
+        row = model.bf16_projection("token_embedding")[123]
+        a = engine.step(row, 0)
+        _, b = engine.step_token(123, 0)
+        np.testing.assert_array_equal(a, b)
+    finally:
+        engine.close()
+        engine.close()  # idempotent
