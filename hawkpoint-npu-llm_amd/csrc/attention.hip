@@ -9,12 +9,15 @@
 //   scores   (q . k) * head_dim**-0.5, minus the row max, exp, / sum   :110-125
 //   output   bf16(P @ V)                                          :126-129
 //
-// One workgroup per (KV head, 256-slot chunk).  With a single chunk the
-// workgroup normalises P = p / sum first and then forms P @ V, as NumPy does.
-// With several chunks (long contexts) each workgroup keeps (max, sum, p @ V)
-// for its chunk and the last one to finish merges them with the usual
-// log-sum-exp rescaling.  The KV cache layout is [kv head][slot][64] BF16 per
-// layer, so one slot of one head is a contiguous 128-byte row.
+// Work split: one workgroup per (KV head, chunk of slots).  The chunk is
+// 32 slots while that keeps the split count within `max_splits`, and grows
+// (in steps of 32, up to 256) for long contexts, so a position uses at most
+// `max_splits` workgroups per KV head.  With a single chunk the workgroup
+// normalises P = p / sum first and then forms P @ V, as NumPy does.  With
+// several chunks each workgroup publishes (max, sum, p @ V) for its chunk and
+// the last one to finish (a per-head ticket) merges them with log-sum-exp
+// rescaling.  The KV cache layout is [kv head][slot][64] BF16 per layer, so
+// one slot of one head is a contiguous 128-byte row.
 #include "hk_common.h"
 #include "hk_internal.h"
 
@@ -26,15 +29,32 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kPartStride = kHeadDim + 2;  // acc[64], max, sum
 
+__device__ __forceinline__ void unpack_row(const uint16_t* src, float (&dst)[kHeadDim]) {
+#pragma unroll
+  for (int c = 0; c < kHeadDim / 8; ++c) {
+    const u32x4 w = load16(src + c * 8);
+    dst[c * 8 + 0] = bf_lo(w.x);
+    dst[c * 8 + 1] = bf_hi(w.x);
+    dst[c * 8 + 2] = bf_lo(w.y);
+    dst[c * 8 + 3] = bf_hi(w.y);
+    dst[c * 8 + 4] = bf_lo(w.z);
+    dst[c * 8 + 5] = bf_hi(w.z);
+    dst[c * 8 + 6] = bf_lo(w.w);
+    dst[c * 8 + 7] = bf_hi(w.w);
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) {
   const int g = blockIdx.x;
   const int s = blockIdx.y;
   const int p = *a.position;
-  const int t0 = s * kAttnChunk;
+  int chunk = (p + a.max_splits) / a.max_splits;  // ceil((p + 1) / max_splits)
+  chunk = (chunk + kAttnMinChunk - 1) / kAttnMinChunk * kAttnMinChunk;
+  const int t0 = s * chunk;
   if (t0 > p) return;
-  const int t1 = min(t0 + kAttnChunk, p + 1);
+  const int t1 = min(t0 + chunk, p + 1);
   const int n = t1 - t0;
-  const int nsplit = p / kAttnChunk + 1;
+  const int nsplit = p / chunk + 1;
   const bool holds_new = (s == nsplit - 1);
   const int qpk = a.q_heads / a.kv_heads;
   const int tid = threadIdx.x;
@@ -43,15 +63,15 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
 
   __shared__ float qs[kMaxQPerKV][kHeadDim];
   __shared__ float knew[kHeadDim];
-  __shared__ float vnew[kHeadDim];
-  __shared__ float sc[kMaxQPerKV][kAttnChunk];
+  __shared__ float sc[kMaxQPerKV][kAttnMaxChunk];
   __shared__ float hmax[kMaxQPerKV];
   __shared__ float hsum[kMaxQPerKV];
-  __shared__ float part[kWaves][kMaxQPerKV][kHeadDim];
+  __shared__ uint32_t vs[kAttnMaxChunk][kHalf];  // V rows of the chunk, bf16 pairs
   __shared__ unsigned int ticket_s;
 
   const float* ct = a.cos_tab + (size_t)p * kHalf;
   const float* st = a.sin_tab + (size_t)p * kHalf;
+  const size_t head_base = (size_t)g * a.max_ctx;
 
   // Rotated query heads of this group, rounded to bf16 as the reference does.
   for (int i = tid; i < qpk * kHalf; i += kThreads) {
@@ -62,7 +82,8 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
     qs[h][j] = round_bf16(x1 * c - x2 * sn);
     qs[h][j + kHalf] = round_bf16(x2 * c + x1 * sn);
   }
-  // The new key (rotated) and value of this KV head; appended at slot p.
+  // The new key (rotated) and value of this KV head, appended at slot p by
+  // the workgroup whose chunk holds p.
   if (holds_new && tid < kHalf) {
     const uint16_t* k = a.qkv + (size_t)(a.q_heads + g) * kHeadDim;
     const uint16_t* v = a.qkv + (size_t)(a.q_heads + a.kv_heads + g) * kHeadDim;
@@ -72,46 +93,44 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
     const uint32_t r2 = f32_to_bf16(x2 * c + x1 * sn);
     knew[tid] = bf16_to_f32(r1);
     knew[tid + kHalf] = bf16_to_f32(r2);
-    vnew[tid] = bf16_to_f32(v[tid]);
-    vnew[tid + kHalf] = bf16_to_f32(v[tid + kHalf]);
-    uint16_t* kd = a.kcache + ((size_t)g * a.max_ctx + p) * kHeadDim;
-    uint16_t* vd = a.vcache + ((size_t)g * a.max_ctx + p) * kHeadDim;
+    uint16_t* kd = a.kcache + (head_base + p) * kHeadDim;
+    uint16_t* vd = a.vcache + (head_base + p) * kHeadDim;
     kd[tid] = (uint16_t)r1;
     kd[tid + kHalf] = (uint16_t)r2;
     vd[tid] = v[tid];
     vd[tid + kHalf] = v[tid + kHalf];
   }
+  // Stage the chunk's cached V rows (16-byte loads); slot p comes from qkv.
+  for (int i = tid; i < n * (kHeadDim / 8); i += kThreads) {
+    const int t = i / (kHeadDim / 8), c = i % (kHeadDim / 8);
+    const int slot = t0 + t;
+    const uint16_t* src = (slot == p)
+                              ? a.qkv + (size_t)(a.q_heads + a.kv_heads + g) * kHeadDim + c * 8
+                              : a.vcache + (head_base + slot) * kHeadDim + c * 8;
+    const u32x4 w = load16(src);
+    vs[t][c * 4 + 0] = w.x;
+    vs[t][c * 4 + 1] = w.y;
+    vs[t][c * 4 + 2] = w.z;
+    vs[t][c * 4 + 3] = w.w;
+  }
   __syncthreads();
 
-  // Scores: one slot per thread, all heads of the group.
+  // Scores: one (slot, head) pair per thread.
   const float scale = 1.0f / 8.0f;  // head_dim ** -0.5 for head_dim 64 (exact)
-  for (int t = tid; t < n; t += kThreads) {
+  for (int i = tid; i < n * qpk; i += kThreads) {
+    const int t = i / qpk, h = i % qpk;
     const int slot = t0 + t;
     float kv[kHeadDim];
     if (slot == p) {
 #pragma unroll
       for (int d = 0; d < kHeadDim; ++d) kv[d] = knew[d];
     } else {
-      const uint16_t* kr = a.kcache + ((size_t)g * a.max_ctx + slot) * kHeadDim;
-#pragma unroll
-      for (int c = 0; c < kHeadDim / 8; ++c) {
-        const u32x4 w = load16(kr + c * 8);
-        kv[c * 8 + 0] = bf_lo(w.x);
-        kv[c * 8 + 1] = bf_hi(w.x);
-        kv[c * 8 + 2] = bf_lo(w.y);
-        kv[c * 8 + 3] = bf_hi(w.y);
-        kv[c * 8 + 4] = bf_lo(w.z);
-        kv[c * 8 + 5] = bf_hi(w.z);
-        kv[c * 8 + 6] = bf_lo(w.w);
-        kv[c * 8 + 7] = bf_hi(w.w);
-      }
+      unpack_row(a.kcache + (head_base + slot) * kHeadDim, kv);
     }
-    for (int h = 0; h < qpk; ++h) {
-      float dot = 0.0f;
+    float dot = 0.0f;
 #pragma unroll
-      for (int d = 0; d < kHeadDim; ++d) dot = fmaf(qs[h][d], kv[d], dot);
-      sc[h][t] = dot * scale;
-    }
+    for (int d = 0; d < kHeadDim; ++d) dot = fmaf(qs[h][d], kv[d], dot);
+    sc[h][t] = dot * scale;
   }
   __syncthreads();
 
@@ -142,48 +161,30 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
     __syncthreads();
   }
 
-  // Weighted sum of values: lane = dimension, waves split the slots.
-  {
-    float acc[kMaxQPerKV];
-#pragma unroll
-    for (int h = 0; h < kMaxQPerKV; ++h) acc[h] = 0.0f;
-    const int per = (n + kWaves - 1) / kWaves;
-    const int ta = wave * per, tb = min(n, ta + per);
-    for (int t = ta; t < tb; ++t) {
-      const int slot = t0 + t;
-      const float v = (slot == p)
-                          ? vnew[lane]
-                          : bf16_to_f32(a.vcache[((size_t)g * a.max_ctx + slot) * kHeadDim + lane]);
-#pragma unroll
-      for (int h = 0; h < kMaxQPerKV; ++h)
-        if (h < qpk) acc[h] = fmaf(sc[h][t], v, acc[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < kMaxQPerKV; ++h)
-      if (h < qpk) part[wave][h][lane] = acc[h];
-  }
-  __syncthreads();
-
-  if (nsplit == 1) {
-    for (int i = tid; i < qpk * kHeadDim; i += kThreads) {
-      const int h = i / kHeadDim, d = i % kHeadDim;
-      float o = part[0][h][d];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) o += part[w][h][d];
-      a.out[(size_t)(g * qpk + h) * kHeadDim + d] = (uint16_t)f32_to_bf16(o);
-    }
-    return;
-  }
-
-  // Split-KV: publish this chunk's partials, the last workgroup merges.
+  // Weighted sum of values from the LDS copy of this chunk's V rows:
+  // thread = (head, pair of dimensions), loop over the slots.
   float* mine = a.partial + ((size_t)g * a.max_splits + s) * kMaxQPerKV * kPartStride;
-  for (int i = tid; i < qpk * kHeadDim; i += kThreads) {
-    const int h = i / kHeadDim, d = i % kHeadDim;
-    float o = part[0][h][d];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) o += part[w][h][d];
-    mine[h * kPartStride + d] = o;
+  for (int i = tid; i < qpk * kHalf; i += kThreads) {
+    const int h = i / kHalf, dp = i % kHalf;
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 8
+    for (int t = 0; t < n; ++t) {
+      const uint32_t v2 = vs[t][dp];
+      const float pt = sc[h][t];
+      o0 = fmaf(pt, bf_lo(v2), o0);
+      o1 = fmaf(pt, bf_hi(v2), o1);
+    }
+    if (nsplit == 1) {
+      const uint32_t packed = f32_to_bf16(o0) | (f32_to_bf16(o1) << 16);
+      reinterpret_cast<uint32_t*>(a.out + (size_t)(g * qpk + h) * kHeadDim)[dp] = packed;
+    } else {
+      mine[h * kPartStride + 2 * dp] = o0;
+      mine[h * kPartStride + 2 * dp + 1] = o1;
+    }
   }
+  if (nsplit == 1) return;
+
+  // Split-KV: publish this chunk's max and sum, the last workgroup merges.
   if (tid < qpk) {
     mine[tid * kPartStride + kHeadDim] = hmax[tid];
     mine[tid * kPartStride + kHeadDim + 1] = hsum[tid];
@@ -218,7 +219,8 @@ int launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
   if (a.kv_heads <= 0 || a.q_heads <= 0 || a.q_heads % a.kv_heads != 0)
     return fail("attention: q_heads must be a positive multiple of kv_heads");
   if (a.q_heads / a.kv_heads > kMaxQPerKV) return fail("attention: more than 16 q heads per kv head");
-  if (a.max_splits * kAttnChunk < a.max_ctx) return fail("attention: too few split-KV slots");
+  if (a.max_ctx <= 0 || a.max_ctx > kMaxContext) return fail("attention: context out of range");
+  if (a.max_splits < attention_splits(a.max_ctx)) return fail("attention: too few split-KV slots");
   hipLaunchKernelGGL(attention_decode_kernel, dim3(a.kv_heads, a.max_splits), dim3(kThreads), 0,
                      stream, a);
   const hipError_t err = hipGetLastError();

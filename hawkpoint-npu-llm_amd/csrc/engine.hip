@@ -61,7 +61,7 @@ __global__ void store_i32_kernel(int32_t* dst, int32_t value) { *dst = value; }
 // Scratch shared by the single-operation entry points on one device.
 struct OpScratch {
   int device = -1;
-  ArgmaxState* am = nullptr;
+  unsigned long long* keys = nullptr;
   int32_t* position = nullptr;
   float* partial = nullptr;
   unsigned int* counters = nullptr;
@@ -76,9 +76,8 @@ int op_scratch(OpScratch** out, size_t partial_floats, int counter_slots) {
   HK_CHECK(hipGetDevice(&dev));
   if ((int)g_op_scratch.size() <= dev) g_op_scratch.resize(dev + 1);
   OpScratch& s = g_op_scratch[dev];
-  if (s.am == nullptr) {
-    HK_CHECK(hipMalloc(&s.am, sizeof(ArgmaxState)));
-    HK_CHECK(hipMemset(s.am, 0, sizeof(ArgmaxState)));
+  if (s.keys == nullptr) {
+    HK_CHECK(hipMalloc(&s.keys, kMaxPartialKeys * sizeof(unsigned long long)));
     HK_CHECK(hipMalloc(&s.position, sizeof(int32_t)));
   }
   if (partial_floats > s.partial_floats) {
@@ -149,7 +148,7 @@ struct hk_engine {
   uint16_t* vcache = nullptr;
   float* partial = nullptr;
   unsigned int* counters = nullptr;
-  ArgmaxState* am = nullptr;
+  unsigned long long* keys = nullptr;  // [kMaxPartialKeys] LM-head argmax partials
   StepCtrl* ctrl = nullptr;
   int32_t* out_tokens = nullptr;  // [max_ctx]
   int32_t* result = nullptr;
@@ -254,16 +253,15 @@ int launch_part(hk_engine* e, int part, int l) {
       hd.gamma = e->w.final_norm;
       hd.eps = d.rms_eps;
       hd.yf = e->logits;
-      hd.am = e->am;
-      hd.ctrl = e->ctrl;
-      hd.out_tokens = e->out_tokens;
-      hd.out_cap = d.max_context;
-      hd.token_out = e->result;
+      hd.keys = e->keys;
       hd.M = d.vocab;
       hd.K = d.hidden;
       hd.pro = PRO_NORM;
       hd.epi = EPI_F32_ARGMAX;
-      return launch_gemv(hd, false, s);
+      int blocks = 0;
+      HK_TRY(launch_gemv(hd, false, s, &blocks));
+      return launch_argmax_finalize(e->keys, blocks, e->ctrl, e->out_tokens, d.max_context,
+                                    e->result, s);
     }
     default:
       return fail("unknown step part");
@@ -323,7 +321,7 @@ void free_engine(hk_engine* e) {
     if (g) (void)hipGraphExecDestroy(g);
   void* bufs[] = {e->h,       e->h1,       e->qkv,      e->attn,     e->act,
                   e->normed,  e->logits,   e->kcache,   e->vcache,   e->partial,
-                  e->counters, e->am,      e->ctrl,     e->out_tokens, e->result};
+                  e->counters, e->keys,      e->ctrl,     e->out_tokens, e->result};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -367,6 +365,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
   const hk_model_desc& d = *desc;
   if (d.layers <= 0 || d.hidden <= 0 || d.intermediate <= 0 || d.vocab <= 0 || d.max_context <= 0)
     return fail("hk_engine_create: sizes must be positive");
+  if (d.max_context > kMaxContext) return fail("hk_engine_create: max_context above 65536");
   if (d.head_dim != kHeadDim) {
     set_error("hk_engine_create: only head_dim 64 is supported");
     return HK_ERR_UNSUPPORTED;
@@ -400,7 +399,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
   e->w = *weights;
   e->w.layers = e->layers.data();
   e->qkv_rows = (d.q_heads + 2 * d.kv_heads) * kHeadDim;
-  e->max_splits = (d.max_context + kAttnChunk - 1) / kAttnChunk;
+  e->max_splits = attention_splits(d.max_context);
   const char* env = getenv("HK_EAGER");
   e->use_graph = !(env && env[0] == '1');
 
@@ -420,7 +419,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     HK_TRY(dalloc(&e->vcache, kv));
     HK_TRY(dalloc(&e->partial, (size_t)d.kv_heads * e->max_splits * kMaxQPerKV * (kHeadDim + 2)));
     HK_TRY(dalloc(&e->counters, d.kv_heads));
-    HK_TRY(dalloc(&e->am, 1));
+    HK_TRY(dalloc(&e->keys, kMaxPartialKeys));
     HK_TRY(dalloc(&e->ctrl, 1));
     HK_TRY(dalloc(&e->out_tokens, d.max_context));
     HK_TRY(dalloc(&e->result, 1));
@@ -428,7 +427,6 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     HK_CHECK(hipMemset(e->vcache, 0, kv * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->h, 0, d.hidden * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->counters, 0, d.kv_heads * sizeof(unsigned int)));
-    HK_CHECK(hipMemset(e->am, 0, sizeof(ArgmaxState)));
     HK_CHECK(hipMemset(e->ctrl, 0, sizeof(StepCtrl)));
     HK_CHECK(hipDeviceSynchronize());
     return 0;
@@ -577,7 +575,7 @@ int hk_argmax_f32(const float* x, int32_t n, int32_t* index_device, void* stream
   std::lock_guard<std::mutex> lock(g_op_mutex);
   OpScratch* s = nullptr;
   HK_TRY(op_scratch(&s, 0, 0));
-  return launch_argmax(x, n, s->am, index_device, static_cast<hipStream_t>(stream));
+  return launch_argmax(x, n, s->keys, index_device, static_cast<hipStream_t>(stream));
 }
 
 int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float* rope_sin,
@@ -596,7 +594,8 @@ int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float*
     return fail("hk_attention_decode: q_heads must be a multiple of kv_heads");
   const hipStream_t st = static_cast<hipStream_t>(stream);
   std::lock_guard<std::mutex> lock(g_op_mutex);
-  const int splits = (max_context + kAttnChunk - 1) / kAttnChunk;
+  if (max_context > kMaxContext) return fail("hk_attention_decode: context above 65536 slots");
+  const int splits = attention_splits(max_context);
   OpScratch* s = nullptr;
   HK_TRY(op_scratch(&s, (size_t)kv_heads * splits * kMaxQPerKV * (kHeadDim + 2), kv_heads));
   hipLaunchKernelGGL(store_i32_kernel, dim3(1), dim3(1), 0, st, s->position, position);

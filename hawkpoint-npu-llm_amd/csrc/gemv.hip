@@ -5,12 +5,15 @@
 // and `logits` :173-181) and the W8 device formula of
 // npu_llm/kernels/project_w8bf16.cc:14-38.
 //
-// Mapping (wave64): `LPR` lanes share one output row; a wave owns 64/LPR rows
-// and a 256-thread workgroup 4 waves.  Each lane streams NJ 16-byte chunks of
-// its row (8 bf16 or 16 int8 weights per chunk) with non-temporal loads that
-// are issued *before* the prologue, so the RMSNorm/x staging latency hides
-// under the HBM fetch.  x lives in LDS as float32.  Partial sums are reduced
-// across the LPR lanes with butterfly shuffles.
+// Mapping (wave64): `LPR` lanes share one output row; a wave owns a group of
+// 64/LPR rows at a time and a 256-thread workgroup 4 waves.  Each lane streams
+// NJ 16-byte chunks of its row (8 bf16 or 16 int8 weights per chunk) with
+// non-temporal loads; the first group's loads are issued *before* the
+// prologue, so the RMSNorm/x staging latency hides under the HBM fetch, and a
+// wave that owns several groups loads the next while reducing the current.
+// x lives in LDS as float32.  Partial sums are reduced across the LPR lanes
+// with butterfly shuffles.  The LM-head form also keeps a running argmax key
+// per workgroup (no atomics); launch_argmax_finalize reduces those keys.
 //
 // Rounding points follow the reference exactly:
 //   EPI_BF16   bf16(acc)                         project()
@@ -107,101 +110,18 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return (g / denom) * u;
 }
 
-template <int LPR, int NJ, bool W8, bool PAIR>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
-  extern __shared__ float smem[];
-  float* xs = smem;
-  float* red = smem + a.K;
-  __shared__ unsigned long long wave_keys[kWaves];
-
-  constexpr int RPW = 64 / LPR;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int l = lane % LPR;
-  const int row = (blockIdx.x * kWaves + wave) * RPW + lane / LPR;
-  const bool live = row < a.M;
-  const int CH = W8 ? (a.K >> 4) : (a.K >> 3);
-  const size_t row_bytes = W8 ? (size_t)a.K : (size_t)a.K * 2;
-  const char* wrow = static_cast<const char*>(a.W) + (size_t)(live ? row : 0) * row_bytes;
-  const char* urow = wrow + (size_t)a.M * row_bytes;
-
-  u32x4 w[NJ];
-  u32x4 u[PAIR ? NJ : 1];
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-
-  auto load_batch = [&](int base) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int c = base + l + j * LPR;
-      const bool ok = live && c < CH;
-      w[j] = ok ? load_stream16(wrow + (size_t)c * 16) : zero;
-      if constexpr (PAIR) u[j] = ok ? load_stream16(urow + (size_t)c * 16) : zero;
-    }
-  };
-
-  float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
-  int base = 0;
-  load_batch(base);
-  stage_x(a, xs, red);
-  __syncthreads();
-  for (;;) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int c = base + l + j * LPR;
-      if (c < CH) {
-        fma_chunk<W8>(w[j], xs, c, a0, a1);
-        if constexpr (PAIR) fma_chunk<W8>(u[j], xs, c, b0, b1);
-      }
-    }
-    base += LPR * NJ;
-    if (base >= CH) break;
-    load_batch(base);
-  }
-
+// Reduce one row group's partial sums and apply the epilogue.
+template <int LPR, bool W8, bool PAIR>
+__device__ __forceinline__ void finish_row(const GemvArgs& a, int row, bool live, int l, float a0,
+                                           float a1, float b0, float b1,
+                                           unsigned long long& best) {
   float acc = group_sum<LPR>(a0 + a1);
   float accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
-  if constexpr (W8) {
-    if (live) {
-      acc = acc * a.scale[row];
-      if constexpr (PAIR) accu = accu * a.scale[row + a.M];
-    }
-  }
-
-  if (a.epi == EPI_F32_ARGMAX) {
-    if (live && l == 0) a.yf[row] = acc;
-    unsigned long long key = (live && l == 0) ? argmax_key(acc, (uint32_t)row) : 0ull;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) key = umax64(key, shfl_xor_u64(key, m));
-    if (lane == 0) wave_keys[wave] = key;
-    __syncthreads();
-    if (tid == 0) {
-      unsigned long long k = wave_keys[0];
-#pragma unroll
-      for (int i = 1; i < kWaves; ++i) k = umax64(k, wave_keys[i]);
-      atomicMax(&a.am->key, k);
-      __threadfence();
-      const unsigned int ticket = atomicAdd(&a.am->count, 1u);
-      if (ticket == gridDim.x - 1) {
-        __threadfence();
-        const unsigned long long final_key = atomicAdd(&a.am->key, 0ull);
-        const int32_t index = (int32_t)argmax_key_index(final_key);
-        if (a.token_out) *a.token_out = index;
-        if (a.ctrl != nullptr && a.ctrl->advance) {
-          StepCtrl* c = a.ctrl;
-          if (a.out_tokens && c->n_out >= 0 && c->n_out < a.out_cap) a.out_tokens[c->n_out] = index;
-          c->n_out = c->n_out + 1;
-          c->token = index;
-          c->position = c->position + 1;
-        }
-        atomicExch(&a.am->key, 0ull);
-        atomicExch(&a.am->count, 0u);
-      }
-    }
-    return;
-  }
-
   if (!live || l != 0) return;
+  if constexpr (W8) {
+    acc = acc * a.scale[row];
+    if constexpr (PAIR) accu = accu * a.scale[row + a.M];
+  }
   switch (a.epi) {
     case EPI_BF16:
       a.y[row] = (uint16_t)f32_to_bf16(acc);
@@ -215,6 +135,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     case EPI_F32:
       a.yf[row] = acc;
       break;
+    case EPI_F32_ARGMAX:
+      a.yf[row] = acc;
+      best = umax64(best, argmax_key(acc, (uint32_t)row));
+      break;
     case EPI_SWIGLU:
       a.y[row] = (uint16_t)f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu)));
       break;
@@ -223,10 +147,136 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// Each wave owns row groups (64/LPR rows; paired with the up rows for
+// SwiGLU) g = wave_id, wave_id + waves_in_grid, ...; the next group's weights
+// are loaded while the current one is reduced, so a wave always has its
+// loads in flight.  Rows longer than LPR*NJ chunks take several passes.
 template <int LPR, int NJ, bool W8, bool PAIR>
-int launch_cfg(const GemvArgs& a, hipStream_t stream) {
-  constexpr int rows_per_block = kWaves * (64 / LPR);
-  const int blocks = (a.M + rows_per_block - 1) / rows_per_block;
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+  extern __shared__ float smem[];
+  float* xs = smem;
+  float* red = smem + a.K;
+  __shared__ unsigned long long wave_keys[kWaves];
+
+  constexpr int RPW = 64 / LPR;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l = lane % LPR;
+  const int sub = lane / LPR;
+  const int CH = W8 ? (a.K >> 4) : (a.K >> 3);
+  const size_t row_bytes = W8 ? (size_t)a.K : (size_t)a.K * 2;
+  const size_t pair_off = (size_t)a.M * row_bytes;
+  const int groups = (a.M + RPW - 1) / RPW;
+  const int stride = gridDim.x * kWaves;
+  const bool single_pass = CH <= LPR * NJ;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  u32x4 wa[NJ], wb[NJ];
+  u32x4 ua[PAIR ? NJ : 1], ub[PAIR ? NJ : 1];
+
+  auto load = [&](int g, int base, u32x4 (&w)[NJ], u32x4 (&u)[PAIR ? NJ : 1]) {
+    const int row = g * RPW + sub;
+    const bool live = g < groups && row < a.M;
+    const char* wrow = static_cast<const char*>(a.W) + (size_t)(live ? row : 0) * row_bytes;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = base + l + j * LPR;
+      const bool ok = live && c < CH;
+      w[j] = ok ? load_stream16(wrow + (size_t)c * 16) : zero;
+      if constexpr (PAIR) u[j] = ok ? load_stream16(wrow + pair_off + (size_t)c * 16) : zero;
+    }
+  };
+  auto dot = [&](int base, const u32x4 (&w)[NJ], const u32x4 (&u)[PAIR ? NJ : 1], float& a0,
+                 float& a1, float& b0, float& b1) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = base + l + j * LPR;
+      if (c < CH) {
+        fma_chunk<W8>(w[j], xs, c, a0, a1);
+        if constexpr (PAIR) fma_chunk<W8>(u[j], xs, c, b0, b1);
+      }
+    }
+  };
+
+  unsigned long long best = 0ull;
+  int g = blockIdx.x * kWaves + wave;
+  load(g, 0, wa, ua);
+  stage_x(a, xs, red);
+  __syncthreads();
+
+  if (single_pass) {
+    for (;;) {
+      if (g >= groups) break;
+      const int gn = g + stride;
+      if (gn < groups) load(gn, 0, wb, ub);
+      float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+      dot(0, wa, ua, a0, a1, b0, b1);
+      finish_row<LPR, W8, PAIR>(a, g * RPW + sub, g * RPW + sub < a.M, l, a0, a1, b0, b1, best);
+      g = gn;
+      if (g >= groups) break;
+      const int gn2 = g + stride;
+      if (gn2 < groups) load(gn2, 0, wa, ua);
+      a0 = a1 = b0 = b1 = 0.f;
+      dot(0, wb, ub, a0, a1, b0, b1);
+      finish_row<LPR, W8, PAIR>(a, g * RPW + sub, g * RPW + sub < a.M, l, a0, a1, b0, b1, best);
+      g = gn2;
+    }
+  } else {
+    bool first = true;
+    for (; g < groups; g += stride) {
+      float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+      for (int base = 0; base < CH; base += LPR * NJ) {
+        if (!first) load(g, base, wa, ua);
+        first = false;
+        dot(base, wa, ua, a0, a1, b0, b1);
+      }
+      finish_row<LPR, W8, PAIR>(a, g * RPW + sub, g * RPW + sub < a.M, l, a0, a1, b0, b1, best);
+    }
+  }
+
+  if (a.epi == EPI_F32_ARGMAX) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) best = umax64(best, shfl_xor_u64(best, m));
+    if (lane == 0) wave_keys[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long k = wave_keys[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; ++i) k = umax64(k, wave_keys[i]);
+      a.keys[blockIdx.x] = k;
+    }
+  }
+}
+
+int g_cu_count = 0;
+
+int cu_count() {
+  if (g_cu_count == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      g_cu_count = n;
+    else
+      g_cu_count = 256;
+  }
+  return g_cu_count;
+}
+
+// Workgroups for a launch: one row group per wave when that fits in four
+// workgroups per CU, otherwise four per CU looping over the groups.
+int blocks_for(int groups) {
+  const int needed = (groups + kWaves - 1) / kWaves;
+  int cap = cu_count() * 4;
+  if (cap > kMaxPartialKeys) cap = kMaxPartialKeys;
+  return needed < cap ? needed : cap;
+}
+
+template <int LPR, int NJ, bool W8, bool PAIR>
+int launch_cfg(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  constexpr int RPW = 64 / LPR;
+  const int blocks = blocks_for((a.M + RPW - 1) / RPW);
+  if (blocks_out) *blocks_out = blocks;
   const size_t lds = (size_t)(a.K + 8) * sizeof(float);
   hipLaunchKernelGGL((gemv_kernel<LPR, NJ, W8, PAIR>), dim3(blocks), dim3(kThreads), lds, stream,
                      a);
@@ -235,29 +285,45 @@ int launch_cfg(const GemvArgs& a, hipStream_t stream) {
 }
 
 template <int LPR, bool W8, bool PAIR>
-int launch_nj(int nj, const GemvArgs& a, hipStream_t stream) {
-  if (nj <= 6) return launch_cfg<LPR, 6, W8, PAIR>(a, stream);
-  if (nj <= 7) return launch_cfg<LPR, 7, W8, PAIR>(a, stream);
-  if (nj <= 8) return launch_cfg<LPR, 8, W8, PAIR>(a, stream);
-  if (nj <= 10) return launch_cfg<LPR, 10, W8, PAIR>(a, stream);
-  return launch_cfg<LPR, 12, W8, PAIR>(a, stream);
+int launch_nj(int nj, const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  if (nj <= 6) return launch_cfg<LPR, 6, W8, PAIR>(a, stream, blocks_out);
+  if (nj <= 7) return launch_cfg<LPR, 7, W8, PAIR>(a, stream, blocks_out);
+  if (nj <= 8) return launch_cfg<LPR, 8, W8, PAIR>(a, stream, blocks_out);
+  if (nj <= 10) return launch_cfg<LPR, 10, W8, PAIR>(a, stream, blocks_out);
+  return launch_cfg<LPR, 12, W8, PAIR>(a, stream, blocks_out);
+}
+
+// Fewest lanes per row that keep every lane's chunk count at or below 12;
+// longer rows use 64 lanes and several passes of 8 chunks.
+int pick_lpr(int CH) {
+  if ((CH + 7) / 8 <= 12) return 8;
+  if ((CH + 15) / 16 <= 12) return 16;
+  if ((CH + 31) / 32 <= 12) return 32;
+  return 64;
 }
 
 template <bool W8, bool PAIR>
-int launch_shape(const GemvArgs& a, hipStream_t stream) {
+int launch_shape(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
   const int CH = W8 ? a.K / 16 : a.K / 8;
-  // Fewest lanes per row that keep every lane's chunk count at or below 12;
-  // very long rows fall back to 64 lanes with several passes of 8 chunks.
-  if ((CH + 7) / 8 <= 12) return launch_nj<8, W8, PAIR>((CH + 7) / 8, a, stream);
-  if ((CH + 15) / 16 <= 12) return launch_nj<16, W8, PAIR>((CH + 15) / 16, a, stream);
-  if ((CH + 31) / 32 <= 12) return launch_nj<32, W8, PAIR>((CH + 31) / 32, a, stream);
-  if ((CH + 63) / 64 <= 12) return launch_nj<64, W8, PAIR>((CH + 63) / 64, a, stream);
-  return launch_cfg<64, 8, W8, PAIR>(a, stream);
+  switch (pick_lpr(CH)) {
+    case 8: return launch_nj<8, W8, PAIR>((CH + 7) / 8, a, stream, blocks_out);
+    case 16: return launch_nj<16, W8, PAIR>((CH + 15) / 16, a, stream, blocks_out);
+    case 32: return launch_nj<32, W8, PAIR>((CH + 31) / 32, a, stream, blocks_out);
+    default:
+      if ((CH + 63) / 64 <= 12) return launch_nj<64, W8, PAIR>((CH + 63) / 64, a, stream, blocks_out);
+      return launch_cfg<64, 8, W8, PAIR>(a, stream, blocks_out);
+  }
 }
 
 }  // namespace
 
-int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream) {
+int gemv_blocks(const GemvArgs& a, bool w8) {
+  const int CH = w8 ? a.K / 16 : a.K / 8;
+  const int rpw = 64 / pick_lpr(CH);
+  return blocks_for((a.M + rpw - 1) / rpw);
+}
+
+int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out) {
   if (a.M <= 0 || a.K <= 0) return fail("gemv: M and K must be positive");
   if (a.K % (w8 ? 16 : 8) != 0)
     return fail(w8 ? "gemv: K must be a multiple of 16 for int8 weights"
@@ -272,9 +338,12 @@ int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream) {
     return fail("gemv: bf16 output missing");
   if (a.epi == EPI_BIAS && a.bias == nullptr) return fail("gemv: bias missing");
   if (a.epi == EPI_RESID && a.resid == nullptr) return fail("gemv: residual missing");
-  if (a.epi == EPI_F32_ARGMAX && a.am == nullptr) return fail("gemv: argmax state missing");
-  if (w8) return pair ? launch_shape<true, true>(a, stream) : launch_shape<true, false>(a, stream);
-  return pair ? launch_shape<false, true>(a, stream) : launch_shape<false, false>(a, stream);
+  if (a.epi == EPI_F32_ARGMAX && a.keys == nullptr) return fail("gemv: argmax key buffer missing");
+  if (w8)
+    return pair ? launch_shape<true, true>(a, stream, blocks_out)
+                : launch_shape<true, false>(a, stream, blocks_out);
+  return pair ? launch_shape<false, true>(a, stream, blocks_out)
+              : launch_shape<false, false>(a, stream, blocks_out);
 }
 
 }  // namespace hk

@@ -14,14 +14,9 @@ void set_error(const std::string& message);
 int fail(const std::string& message);           // set_error + return HK_ERR_INVALID
 int hip_fail(hipError_t err, const char* what);  // set_error + return HK_ERR_HIP
 
-// Result of the last-workgroup argmax reduction (see argmax_key in
-// hk_common.h).  `key` and `count` must be zero before a launch that uses
-// them; the last workgroup of that launch leaves them zero again.
-struct ArgmaxState {
-  unsigned long long key;
-  unsigned int count;
-  unsigned int pad;
-};
+// Argmax keys (see argmax_key in hk_common.h): a launch that reduces rows
+// writes one partial key per workgroup; launch_argmax_finalize reduces them.
+constexpr int kMaxPartialKeys = 4096;
 
 // Decode-step control block, read by the kernels of a captured step so the
 // same graph serves every position.
@@ -37,7 +32,7 @@ enum GemvEpilogue : int {
   EPI_BIAS = 1,        // y = bf16(f32(bf16(acc)) + bias)
   EPI_RESID = 2,       // y = bf16(f32(bf16(acc)) + f32(resid))
   EPI_F32 = 3,         // yf = acc (unrounded)
-  EPI_F32_ARGMAX = 4,  // yf = acc, plus argmax over all rows into `am`
+  EPI_F32_ARGMAX = 4,  // yf = acc, plus one partial argmax key per workgroup
   EPI_SWIGLU = 5,      // rows i and M+i: y = bf16(silu(bf16(g)) * bf16(u))
 };
 
@@ -59,18 +54,25 @@ struct GemvArgs {
   const uint16_t* resid;     // [M] (EPI_RESID)
   uint16_t* y;               // [M] bf16 output
   float* yf;                 // [M] f32 output
-  ArgmaxState* am;           // EPI_F32_ARGMAX
-  StepCtrl* ctrl;            // EPI_F32_ARGMAX: optional token feedback
-  int32_t* out_tokens;       // EPI_F32_ARGMAX: optional emitted-token log
-  int32_t* token_out;        // EPI_F32_ARGMAX: optional single result
-  int out_cap;               // capacity of out_tokens
+  unsigned long long* keys;  // EPI_F32_ARGMAX: [gridDim.x] partial keys
   int M, K, vocab_limit;
   int pro, epi;
 };
 
 // Launches y = W @ x with the given prologue/epilogue.  Returns 0 or an
-// hk error code (message via set_error).
-int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream);
+// hk error code (message via set_error).  `*blocks_out` (optional) receives
+// the number of workgroups, i.e. of partial argmax keys written.
+int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out = nullptr);
+
+// Workgroups the GEMV launches for these arguments (<= kMaxPartialKeys).
+int gemv_blocks(const GemvArgs& a, bool w8);
+
+// Reduce `n` partial keys to the first-maximum index; write it to
+// `token_out` (if set) and, when ctrl->advance, feed it back into `ctrl`
+// and append it to `out_tokens` (capacity `out_cap`).
+int launch_argmax_finalize(const unsigned long long* keys, int n, StepCtrl* ctrl,
+                           int32_t* out_tokens, int out_cap, int32_t* token_out,
+                           hipStream_t stream);
 
 struct AttnArgs {
   const uint16_t* qkv;       // [(Hq + 2 Hkv) * 64] bf16: q heads, k heads, v heads
@@ -80,14 +82,22 @@ struct AttnArgs {
   uint16_t* vcache;          // this layer: [Hkv, max_ctx, 64] bf16
   const int32_t* position;   // device scalar
   uint16_t* out;             // [Hq * 64] bf16
-  float* partial;            // [Hkv, max_splits, qpk, 66] split-KV partials
+  float* partial;            // [Hkv, max_splits, 16, 66] split-KV partials
   unsigned int* counters;    // [Hkv] zero between launches
   int q_heads, kv_heads, max_ctx, max_splits;
 };
 
 constexpr int kHeadDim = 64;
-constexpr int kAttnChunk = 256;  // positions per split-KV workgroup
+constexpr int kAttnMinChunk = 32;   // fewest slots per split-KV workgroup
+constexpr int kAttnMaxChunk = 256;  // most slots per split-KV workgroup
 constexpr int kMaxQPerKV = 16;
+constexpr int kMaxContext = 65536;
+
+// Split-KV workgroups per KV head for a context of `max_ctx` slots.
+inline int attention_splits(int max_ctx) {
+  const int s = (max_ctx + kAttnMaxChunk - 1) / kAttnMaxChunk;
+  return s < 16 ? 16 : s;
+}
 
 int launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 
@@ -96,8 +106,8 @@ int launch_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t
                    int n, hipStream_t stream);
 // Elementwise SwiGLU over a [2I] gate|up vector.
 int launch_swiglu(const uint16_t* gate_up, uint16_t* act, int inter, hipStream_t stream);
-// Argmax over n float32 values (first maximum).
-int launch_argmax(const float* x, int n, ArgmaxState* am, int32_t* out_index,
+// Argmax over n float32 values (first maximum); `keys` holds kMaxPartialKeys.
+int launch_argmax(const float* x, int n, unsigned long long* keys, int32_t* out_index,
                   hipStream_t stream);
 
 }  // namespace hk

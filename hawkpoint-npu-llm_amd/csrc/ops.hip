@@ -46,29 +46,51 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const uint16_t* gu, ui
   act[i] = (uint16_t)f32_to_bf16((g / (1.0f + expf(-clipped))) * u);
 }
 
-// np.argmax over float32 (generate.py:709-714): first maximum wins.
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* x, int n, ArgmaxState* am,
-                                                          int32_t* out_index) {
-  __shared__ unsigned long long keys[kWaves];
+// np.argmax over float32 (generate.py:709-714): first maximum wins.  Each
+// workgroup writes one partial key; argmax_finalize_kernel reduces them.
+__global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const float* x, int n,
+                                                                  unsigned long long* keys) {
+  __shared__ unsigned long long wk[kWaves];
   const int tid = threadIdx.x;
   unsigned long long key = 0ull;
   for (int i = blockIdx.x * kThreads + tid; i < n; i += gridDim.x * kThreads)
     key = umax64(key, argmax_key(x[i], (uint32_t)i));
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) key = umax64(key, shfl_xor_u64(key, m));
-  if ((tid & 63) == 0) keys[tid >> 6] = key;
+  if ((tid & 63) == 0) wk[tid >> 6] = key;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long k = wk[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) k = umax64(k, wk[w]);
+    keys[blockIdx.x] = k;
+  }
+}
+
+constexpr int kFinalThreads = 1024;
+
+__global__ __launch_bounds__(kFinalThreads) void argmax_finalize_kernel(
+    const unsigned long long* keys, int n, StepCtrl* ctrl, int32_t* out_tokens, int out_cap,
+    int32_t* token_out) {
+  __shared__ unsigned long long wk[kFinalThreads / 64];
+  const int tid = threadIdx.x;
+  unsigned long long key = 0ull;
+  for (int i = tid; i < n; i += kFinalThreads) key = umax64(key, keys[i]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) key = umax64(key, shfl_xor_u64(key, m));
+  if ((tid & 63) == 0) wk[tid >> 6] = key;
   __syncthreads();
   if (tid != 0) return;
-  unsigned long long k = keys[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) k = umax64(k, keys[w]);
-  atomicMax(&am->key, k);
-  __threadfence();
-  if (atomicAdd(&am->count, 1u) == gridDim.x - 1) {
-    __threadfence();
-    *out_index = (int32_t)argmax_key_index(atomicAdd(&am->key, 0ull));
-    atomicExch(&am->key, 0ull);
-    atomicExch(&am->count, 0u);
+  unsigned long long k = wk[0];
+  for (int w = 1; w < kFinalThreads / 64; ++w) k = umax64(k, wk[w]);
+  const int32_t index = (int32_t)argmax_key_index(k);
+  if (token_out) *token_out = index;
+  if (ctrl != nullptr && ctrl->advance) {
+    const int slot = ctrl->n_out;
+    if (out_tokens && slot >= 0 && slot < out_cap) out_tokens[slot] = index;
+    ctrl->n_out = slot + 1;
+    ctrl->token = index;
+    ctrl->position = ctrl->position + 1;
   }
 }
 
@@ -90,14 +112,25 @@ int launch_swiglu(const uint16_t* gate_up, uint16_t* act, int inter, hipStream_t
   return err == hipSuccess ? 0 : hip_fail(err, "swiglu launch");
 }
 
-int launch_argmax(const float* x, int n, ArgmaxState* am, int32_t* out_index,
+int launch_argmax(const float* x, int n, unsigned long long* keys, int32_t* out_index,
                   hipStream_t stream) {
   if (n <= 0) return fail("argmax: size must be positive");
   int blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
   if (blocks > 1024) blocks = 1024;
-  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(kThreads), 0, stream, x, n, am, out_index);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(kThreads), 0, stream, x, n, keys);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "argmax launch");
+  return launch_argmax_finalize(keys, blocks, nullptr, nullptr, 0, out_index, stream);
+}
+
+int launch_argmax_finalize(const unsigned long long* keys, int n, StepCtrl* ctrl,
+                           int32_t* out_tokens, int out_cap, int32_t* token_out,
+                           hipStream_t stream) {
+  if (n <= 0 || n > kMaxPartialKeys) return fail("argmax: bad partial key count");
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(kFinalThreads), 0, stream, keys, n,
+                     ctrl, out_tokens, out_cap, token_out);
   const hipError_t err = hipGetLastError();
-  return err == hipSuccess ? 0 : hip_fail(err, "argmax launch");
+  return err == hipSuccess ? 0 : hip_fail(err, "argmax finalize launch");
 }
 
 }  // namespace hk

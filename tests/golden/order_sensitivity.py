@@ -1,0 +1,67 @@
+#!/usr/bin/env python3
+"""Measure how far the oracle moves from itself when only the float32
+summation order of its projections changes.
+
+The oracle (a NumPy restatement of the reference's CPU runtime) is run twice
+on the engine tests' inputs: once as is (BLAS sgemv sums) and once with every
+projection summed exactly in float64 before the float32 -> bf16 rounding.
+Both are faithful evaluations of the reference's arithmetic; their logits
+differ only because bf16 rounding points flip where the two sums straddle a
+rounding boundary, and the flips compound with depth.  The rel-L2 between them
+is the floor below which no implementation with a different summation order
+(such as the GPU's) can be held.  Output: order_sensitivity.json next to
+this script.  Run time: a few minutes on 8 cores.
+"""
+
+import json
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path[:0] = [str(ROOT), str(ROOT / "hawkpoint-npu-llm_amd")]
+
+import numpy as np  # noqa: E402
+
+from oracle.bf16 import from_bits, round_f32  # noqa: E402
+from oracle.cpu_backend import CPUDecoderStage, OracleDecoder  # noqa: E402
+from runtime.synthetic import QWEN25_05B, SMOLLM2_135M, SyntheticModel  # noqa: E402
+
+
+class ExactSumStage(CPUDecoderStage):
+    """The oracle with exactly rounded (float64-accumulated) projections."""
+
+    def project(self, name, activation):
+        x = round_f32(activation).astype(np.float64)
+        return round_f32((from_bits(self.weight(name)).astype(np.float64) @ x).astype(np.float32))
+
+
+def floor_for(shape, layers, prompt_len, seed, label):
+    model = SyntheticModel(shape, seed=0, layers=layers)
+    rng = np.random.default_rng(seed)
+    prompt = [int(t) for t in rng.integers(0, shape["vocab_size"], prompt_len)]
+    a = OracleDecoder(model, prompt_len + 1)
+    b = OracleDecoder(model, prompt_len + 1)
+    b.stage.__class__ = ExactSumStage
+    for pos, tok in enumerate(prompt):
+        last = pos == prompt_len - 1
+        _, la = a.decode_token(tok, pos, compute_logits=last)
+        _, lb = b.decode_token(tok, pos, compute_logits=last)
+    err = float(np.linalg.norm(la - lb) / np.linalg.norm(lb))
+    print(f"{label}: rel-L2 {err:.4e}, argmax {int(np.argmax(la))} vs {int(np.argmax(lb))}", flush=True)
+    return {"label": label, "layers": model.metadata["layers"], "prompt_tokens": prompt_len,
+            "prompt_seed": seed, "rel_l2": err}
+
+
+def main():
+    rows = [
+        floor_for(SMOLLM2_135M, None, 35, 11, "smollm2-135m full depth, last prompt position"),
+        floor_for(QWEN25_05B, None, 40, 12, "qwen2.5-0.5b full depth, last prompt position"),
+        floor_for(QWEN25_05B, 4, 40, 12, "qwen2.5-0.5b 4 layers, last prompt position"),
+        floor_for(SMOLLM2_135M, 4, 35, 11, "smollm2-135m 4 layers, last prompt position"),
+    ]
+    (HERE / "order_sensitivity.json").write_text(json.dumps(rows, indent=2) + "\n")
+
+
+if __name__ == "__main__":
+    main()

@@ -6,6 +6,12 @@ validate_engine_npu.py):
 - teacher-forced: both sides see the oracle's token sequence; per-step logits
   must agree within rel-L2 <= 1e-2 and the argmax must agree unless the
   oracle's top-2 gap is below 2**-7 relative (a bf16 near-tie);
+  at full depth (24 / 30 layers) the oracle itself moves by 1.4-1.6% rel-L2
+  when only its float32 summation order changes (tests/golden/
+  order_sensitivity.json, made by order_sensitivity.py there), so no
+  reordered implementation can meet 1e-2 there; full-depth models are held
+  to 2.5e-2 and the 1e-2 bound is checked on 4-layer models of the same width
+  (floor 0.65-0.7%);
 - free-running greedy: the engine's own generated ids equal the oracle's up to
   the first near-tie step;
 - KV slot indexing: slot p is written at step p only (slots above the last
@@ -38,7 +44,7 @@ def _prompt(vocab, n, seed):
     return [int(t) for t in rng.integers(0, vocab, n)]
 
 
-def _check_decode(model, prompt, new_tokens, context, *, w8=False, label=""):
+def _check_decode(model, prompt, new_tokens, context, *, w8=False, label="", tol=1e-2):
     from runtime.qwen_engine import QwenDecoderEngine
 
     announce(f"engine parity {label}: prompt {len(prompt)} new {new_tokens} ctx {context} w8={w8}")
@@ -61,7 +67,7 @@ def _check_decode(model, prompt, new_tokens, context, *, w8=False, label=""):
             if got_tok != int(np.argmax(ref)) and not near_tie(ref):
                 mismatches.append((pos, got_tok, int(np.argmax(ref))))
         announce(f"  max rel-L2 {max(errors):.3e}, argmax mismatches {mismatches}")
-        assert max(errors) <= 1e-2
+        assert max(errors) <= tol
         assert not mismatches
 
         # free-running greedy through the device-driven loop
@@ -69,17 +75,22 @@ def _check_decode(model, prompt, new_tokens, context, *, w8=False, label=""):
         for pos, tok in enumerate(prompt[:-1]):
             engine.step_token(tok, pos, logits=False)
         gen = engine.generate(prompt[-1], len(prompt) - 1, new_tokens)
+        agree = new_tokens
         for i, (a, b) in enumerate(zip(gen, ref_tokens)):
             if a != b:
                 assert near_tie(ref_logits[i]), f"token {i}: gpu {a} oracle {b}"
+                agree = i
                 break
-        announce(f"  greedy ids match: {gen == ref_tokens}")
+        announce(f"  greedy ids match: {gen == ref_tokens} (first {agree} of {new_tokens})")
 
-        # KV slot indexing after the free run: slots written = positions used
+        # KV slot indexing after the free run: slots written = positions used;
+        # values are compared where both runs saw the same tokens (the slot of
+        # generated token i is written by the step that consumes it)
         last_pos = len(prompt) - 1 + new_tokens - 1
+        same_until = len(prompt) - 1 + agree  # slots 0..same_until hold shared history
         stage = oracle.stage
         for layer in (0, model.metadata["layers"] - 1):
-            for slot in (0, len(prompt) - 1, last_pos - 1):
+            for slot in sorted({0, len(prompt) - 1, min(last_pos - 1, same_until)}):
                 k, v = engine.read_kv(layer, slot)
                 assert np.any(k != 0) and np.any(v != 0)
                 ok = np.abs(bf16.from_bits(k) - bf16.from_bits(stage.key_cache[layer][:, slot]))
@@ -91,19 +102,40 @@ def _check_decode(model, prompt, new_tokens, context, *, w8=False, label=""):
         engine.close()
 
 
+FULL_DEPTH_TOL = 2.5e-2  # 1.6-1.8x the oracle's own summation-order floor
+
+
 def test_smollm_135m_shape_decode(smol_model):
     """SmolLM2-135M shape: 35-token prompt, greedy 16 tokens, 64-slot context."""
-    _check_decode(smol_model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m")
+    _check_decode(smol_model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m",
+                  tol=FULL_DEPTH_TOL)
+
+
+def test_smollm_4_layer_decode_within_1e2():
+    model = SyntheticModel(SMOLLM2_135M, seed=0, layers=4)
+    _check_decode(model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m-4L")
 
 
 def test_qwen_05b_shape_decode(qwen_model):
     """Qwen2.5-0.5B shape: 40-token prompt, greedy 32 tokens (slots 0..70)."""
-    _check_decode(qwen_model, _prompt(151936, 40, 12), 32, 72, label="qwen2.5-0.5b")
+    _check_decode(qwen_model, _prompt(151936, 40, 12), 32, 72, label="qwen2.5-0.5b",
+                  tol=FULL_DEPTH_TOL)
+
+
+def test_qwen_4_layer_decode_within_1e2():
+    model = SyntheticModel(QWEN25_05B, seed=0, layers=4)
+    _check_decode(model, _prompt(151936, 40, 12), 32, 72, label="qwen2.5-0.5b-4L")
 
 
 def test_qwen_05b_shape_w8_decode(qwen_model):
     """W8 layer projections (int8 + per-row scale), bf16 LM head."""
-    _check_decode(qwen_model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen2.5-0.5b-w8")
+    _check_decode(qwen_model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen2.5-0.5b-w8",
+                  tol=FULL_DEPTH_TOL)
+
+
+def test_qwen_4_layer_w8_decode_within_1e2():
+    model = SyntheticModel(QWEN25_05B, seed=0, layers=4)
+    _check_decode(model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen2.5-0.5b-4L-w8")
 
 
 def test_long_context_split_kv():

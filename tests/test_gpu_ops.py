@@ -41,6 +41,21 @@ def _bound(w64, x64, exact):
     return 1.01 * gamma * (np.abs(w64) @ np.abs(x64)) + 1e-30
 
 
+def _ulp(x):
+    x = np.abs(np.asarray(x, np.float64))
+    return 2.0 ** (np.floor(np.log2(np.maximum(x, 2.0**-126))) - 7)
+
+
+def _check_bf16(y_bits, ref_bits, sum_bound):
+    """GPU and oracle each round a float32 sum carrying at most `sum_bound`
+    error; their bf16 results may differ by the two sum errors plus one bf16
+    step, and should agree exactly almost everywhere."""
+    y = bf16.from_bits(y_bits).astype(np.float64)
+    ref = bf16.from_bits(ref_bits).astype(np.float64)
+    assert np.all(np.abs(y - ref) <= _ulp(ref) + 2 * sum_bound)
+    assert (y_bits == ref_bits).mean() >= 0.97
+
+
 @pytest.mark.parametrize("m,k,bias", QWEN_SHAPES + SMOL_SHAPES)
 def test_gemv_bf16_matches_oracle(hk_lib, m, k, bias):
     from runtime import hip
@@ -70,9 +85,7 @@ def test_gemv_bf16_matches_oracle(hk_lib, m, k, bias):
     ref = bf16.round_f32(bf16.from_bits(w_bits) @ bf16.from_bits(x_bits))
     if bias:
         ref = bf16.round_f32(ref + b)
-    diff = bf16_ulp_diff(y, bf16.to_bits(ref))
-    assert diff.max() <= 1
-    assert (diff == 0).mean() >= 0.97
+    _check_bf16(y, bf16.to_bits(ref), _bound(w64, x64, exact))
 
 
 @pytest.mark.parametrize("m,k", [(896, 896), (896, 4864), (9728, 896), (1152, 896), (576, 1536)])
@@ -95,9 +108,7 @@ def test_gemv_w8_matches_oracle(hk_lib, m, k):
     exact = (q64 @ x.astype(np.float64)) * s
     bound = _bound(q64, x.astype(np.float64), exact) * s + 2e-7 * np.abs(exact)
     assert np.all(np.abs(_read(Yf, np.float32, m) - exact) <= bound)
-    diff = bf16_ulp_diff(_read(Y, np.uint16, m), bf16.to_bits(project_w8(q, s, x)))
-    assert diff.max() <= 1
-    assert (diff == 0).mean() >= 0.97
+    _check_bf16(_read(Y, np.uint16, m), bf16.to_bits(project_w8(q, s, x)), bound)
 
 
 def test_gemv_residual_epilogue(hk_lib):
@@ -115,8 +126,11 @@ def test_gemv_residual_epilogue(hk_lib):
     hip.check(hk_lib.hk_stream_sync(None), "sync")
     proj = bf16.round_f32(bf16.from_bits(w_bits) @ bf16.from_bits(x_bits))
     ref = bf16.to_bits(proj + bf16.from_bits(r_bits))
-    diff = bf16_ulp_diff(_read(Y, np.uint16, m), ref)
-    assert diff.max() <= 1 and (diff == 0).mean() >= 0.97
+    w64 = bf16.from_bits(w_bits).astype(np.float64)
+    x64 = bf16.from_bits(x_bits).astype(np.float64)
+    # a one-step difference in the rounded projection carries into the sum
+    bound = _bound(w64, x64, None) + _ulp(proj)
+    _check_bf16(_read(Y, np.uint16, m), ref, bound)
 
 
 def test_gemv_rejects_bad_shapes(hk_lib):
@@ -224,6 +238,8 @@ def test_attention_decode_matches_oracle(hk_lib, q_heads, kv_heads, ctx, positio
     # the KV append is bit-exact: same RoPE tables, same rounding points
     np.testing.assert_array_equal(kc_gpu, stage.key_cache[0])
     np.testing.assert_array_equal(vc_gpu, stage.value_cache[0])
-    diff = bf16_ulp_diff(out, bf16.to_bits(ref))
-    assert diff.max() <= 2
-    assert (diff == 0).mean() >= 0.95
+    # softmax-weighted sums in a different float32 order: one bf16 step plus
+    # an absolute term for outputs near zero (values are O(1))
+    got = bf16.from_bits(out).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= _ulp(ref) + 1e-5)
+    assert (out == bf16.to_bits(ref)).mean() >= 0.95
