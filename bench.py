@@ -90,6 +90,29 @@ def cpu_baseline(model, prompt, decode_steps):
     }
 
 
+COPY_BYTES = 256 << 20
+
+
+def probe(engine, meta, launches):
+    """Workload for the rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE): the
+    dominant kernel (gate/up GEMV, rotating through every layer's weights)
+    and, as the calibration of the counters, device-to-device copies of a
+    known size (256 MiB read + 256 MiB written per copy)."""
+    from runtime import hip
+
+    lib = hip.lib()
+    layers = meta["layers"]
+    for i in range(launches):
+        hip.check(lib.hk_engine_launch_part(engine._engine, hip.PARTS["gate_up"], i % layers), "launch")
+    hip.check(lib.hk_stream_sync(engine.stream), "sync")
+    src, dst = hip.DeviceBuffer(COPY_BYTES), hip.DeviceBuffer(COPY_BYTES)
+    src.zero()
+    for _ in range(4):
+        hip.check(lib.hk_memcpy_d2d(dst.ptr, src.ptr, COPY_BYTES), "copy")
+    print(json.dumps({"probe": "gate_up", "launches": launches,
+                      "bytes_per_launch": part_bytes(meta, "gate_up"), "copy_bytes": COPY_BYTES}))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,6 +121,9 @@ def main():
     ap.add_argument("--kernel-launches", type=int, default=240)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--probe", action="store_true",
+                    help="only the counter-calibration workload: launches of the gate/up "
+                    "GEMV over all layers, then 4 device copies of 256 MiB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -125,6 +151,9 @@ def main():
         return first
 
     first = prefill()  # captures both graphs
+    if args.probe:
+        probe(engine, meta, args.kernel_launches)
+        return
     t0 = time.perf_counter()
     first = prefill()
     ttft = time.perf_counter() - t0
@@ -170,6 +199,11 @@ def main():
     achieved = dom_bytes / (parts[dominant] * 1e-6) / 1e9
     log("kernel us/launch: " + ", ".join(f"{k} {v:.2f}" for k, v in parts.items()))
     engine.close()
+    traffic = None
+    tfile = ROOT / "profiles" / f"traffic_{dominant}_qwen05b.json"
+    if tfile.is_file():
+        # HBM bytes per launch from the committed rocprofv3 --pmc runs
+        traffic = json.loads(tfile.read_text()).get("traffic_bytes_per_launch")
 
     result = {
         "metric": METRIC,
@@ -205,7 +239,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
         "baseline_source": "28.83 tok/s, XDNA1 NPU Qwen2.5-0.5B engine (reference README.md:92)",
     }

@@ -9,11 +9,10 @@
 //   scores   (q . k) * head_dim**-0.5, minus the row max, exp, / sum   :110-125
 //   output   bf16(P @ V)                                          :126-129
 //
-// Work split: one workgroup per (KV head, chunk of slots).  The chunk is
-// 32 slots while that keeps the split count within `max_splits`, and grows
-// (in steps of 32, up to 256) for long contexts, so a position uses at most
-// `max_splits` workgroups per KV head.  With a single chunk the workgroup
-// normalises P = p / sum first and then forms P @ V, as NumPy does.  With
+// Work split: one workgroup per (KV head, chunk of 256 slots), so positions
+// below 256 use one workgroup per KV head and no merge.  With a single chunk
+// the workgroup normalises P = p / sum first and then forms P @ V, as NumPy
+// does.  With
 // several chunks each workgroup publishes (max, sum, p @ V) for its chunk and
 // the last one to finish (a per-head ticket) merges them with log-sum-exp
 // rescaling.  The KV cache layout is [kv head][slot][64] BF16 per layer, so
@@ -48,13 +47,11 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
   const int g = blockIdx.x;
   const int s = blockIdx.y;
   const int p = *a.position;
-  int chunk = (p + a.max_splits) / a.max_splits;  // ceil((p + 1) / max_splits)
-  chunk = (chunk + kAttnMinChunk - 1) / kAttnMinChunk * kAttnMinChunk;
-  const int t0 = s * chunk;
+  const int t0 = s * kAttnChunk;
   if (t0 > p) return;
-  const int t1 = min(t0 + chunk, p + 1);
+  const int t1 = min(t0 + kAttnChunk, p + 1);
   const int n = t1 - t0;
-  const int nsplit = p / chunk + 1;
+  const int nsplit = p / kAttnChunk + 1;
   const bool holds_new = (s == nsplit - 1);
   const int qpk = a.q_heads / a.kv_heads;
   const int tid = threadIdx.x;
@@ -63,10 +60,10 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
 
   __shared__ float qs[kMaxQPerKV][kHeadDim];
   __shared__ float knew[kHeadDim];
-  __shared__ float sc[kMaxQPerKV][kAttnMaxChunk];
+  __shared__ float sc[kMaxQPerKV][kAttnChunk];
   __shared__ float hmax[kMaxQPerKV];
   __shared__ float hsum[kMaxQPerKV];
-  __shared__ uint32_t vs[kAttnMaxChunk][kHalf];  // V rows of the chunk, bf16 pairs
+  __shared__ uint32_t vs[kAttnChunk][kHalf];  // V rows of the chunk, bf16 pairs
   __shared__ unsigned int ticket_s;
 
   const float* ct = a.cos_tab + (size_t)p * kHalf;

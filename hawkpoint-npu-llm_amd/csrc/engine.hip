@@ -649,6 +649,13 @@ int hk_memcpy_d2h(void* host_dst, const void* device_src, uint64_t bytes) {
   return 0;
 }
 
+int hk_memcpy_d2d(void* device_dst, const void* device_src, uint64_t bytes) {
+  if (bytes == 0) return 0;
+  if (!device_dst || !device_src) return fail("hk_memcpy_d2d: null pointer");
+  HK_CHECK(hipMemcpy(device_dst, device_src, bytes, hipMemcpyDeviceToDevice));
+  return 0;
+}
+
 int hk_memset(void* device_dst, int32_t value, uint64_t bytes) {
   if (bytes == 0) return 0;
   if (!device_dst) return fail("hk_memset: null pointer");

@@ -82,22 +82,18 @@ struct AttnArgs {
   uint16_t* vcache;          // this layer: [Hkv, max_ctx, 64] bf16
   const int32_t* position;   // device scalar
   uint16_t* out;             // [Hq * 64] bf16
-  float* partial;            // [Hkv, max_splits, 16, 66] split-KV partials
+  float* partial;            // [Hkv, max_splits, 16, 66] split-KV partials (contexts > 256)
   unsigned int* counters;    // [Hkv] zero between launches
   int q_heads, kv_heads, max_ctx, max_splits;
 };
 
 constexpr int kHeadDim = 64;
-constexpr int kAttnMinChunk = 32;   // fewest slots per split-KV workgroup
-constexpr int kAttnMaxChunk = 256;  // most slots per split-KV workgroup
+constexpr int kAttnChunk = 256;  // slots per split-KV workgroup
 constexpr int kMaxQPerKV = 16;
 constexpr int kMaxContext = 65536;
 
 // Split-KV workgroups per KV head for a context of `max_ctx` slots.
-inline int attention_splits(int max_ctx) {
-  const int s = (max_ctx + kAttnMaxChunk - 1) / kAttnMaxChunk;
-  return s < 16 ? 16 : s;
-}
+inline int attention_splits(int max_ctx) { return (max_ctx + kAttnChunk - 1) / kAttnChunk; }
 
 int launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 

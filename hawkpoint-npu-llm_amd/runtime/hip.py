@@ -110,6 +110,7 @@ _SIGNATURES = {
     "hk_free": (ctypes.c_int, [_vp]),
     "hk_memcpy_h2d": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64]),
     "hk_memcpy_d2h": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64]),
+    "hk_memcpy_d2d": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64]),
     "hk_memset": (ctypes.c_int, [_vp, _i32, ctypes.c_uint64]),
     "hk_stream_create": (ctypes.c_int, [ctypes.POINTER(_vp)]),
     "hk_stream_destroy": (ctypes.c_int, [_vp]),

@@ -195,6 +195,7 @@ int hk_malloc(uint64_t bytes, void** device_ptr);
 int hk_free(void* device_ptr);
 int hk_memcpy_h2d(void* device_dst, const void* host_src, uint64_t bytes);
 int hk_memcpy_d2h(void* host_dst, const void* device_src, uint64_t bytes);
+int hk_memcpy_d2d(void* device_dst, const void* device_src, uint64_t bytes);
 int hk_memset(void* device_dst, int32_t value, uint64_t bytes);
 int hk_stream_create(void** stream);
 int hk_stream_destroy(void* stream);
