@@ -11,6 +11,7 @@
 // The kernels read the token and position from a device control block, so
 // one captured hipGraph per variant (with / without the head) serves every
 // position; the host only rewrites the control block between replays.
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -154,6 +155,16 @@ struct hk_engine {
   int32_t* result = nullptr;
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   bool use_graph = true;
+  // batched-prefill workspace, allocated on first use for kPrefillRows tokens
+  int pf_rows = 0;
+  uint16_t* pf_x = nullptr;    // layer input / down output [rows, H]
+  uint16_t* pf_h1 = nullptr;   // after attention + residual [rows, H]
+  uint16_t* pf_xn = nullptr;   // normalised rows [rows, H]
+  uint16_t* pf_qkv = nullptr;  // [rows, qkv_rows]
+  uint16_t* pf_q = nullptr;    // rotated queries [rows, Hq * 64]
+  uint16_t* pf_att = nullptr;  // attention output [rows, Hq * 64]
+  uint16_t* pf_act = nullptr;  // SwiGLU output [rows, I]
+  int32_t* pf_tokens = nullptr;
 };
 
 namespace {
@@ -319,9 +330,11 @@ int set_ctrl(hk_engine* e, int32_t token, int32_t position, int32_t advance) {
 void free_engine(hk_engine* e) {
   for (auto& g : e->graph)
     if (g) (void)hipGraphExecDestroy(g);
-  void* bufs[] = {e->h,       e->h1,       e->qkv,      e->attn,     e->act,
-                  e->normed,  e->logits,   e->kcache,   e->vcache,   e->partial,
-                  e->counters, e->keys,      e->ctrl,     e->out_tokens, e->result};
+  void* bufs[] = {e->h,       e->h1,       e->qkv,      e->attn,       e->act,
+                  e->normed,  e->logits,   e->kcache,   e->vcache,     e->partial,
+                  e->counters, e->keys,    e->ctrl,     e->out_tokens, e->result,
+                  e->pf_x,    e->pf_h1,    e->pf_xn,    e->pf_qkv,     e->pf_q,
+                  e->pf_att,  e->pf_act,   e->pf_tokens};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -331,6 +344,103 @@ void free_engine(hk_engine* e) {
 template <typename T>
 int dalloc(T** p, size_t count) {
   HK_CHECK(hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T)));
+  return 0;
+}
+
+constexpr int kPrefillRows = 512;  // tokens per prefill chunk
+
+int prefill_workspace(hk_engine* e) {
+  if (e->pf_rows) return 0;
+  const hk_model_desc& d = e->d;
+  const size_t r = kPrefillRows;
+  HK_TRY(dalloc(&e->pf_x, r * d.hidden));
+  HK_TRY(dalloc(&e->pf_h1, r * d.hidden));
+  HK_TRY(dalloc(&e->pf_xn, r * d.hidden));
+  HK_TRY(dalloc(&e->pf_qkv, r * e->qkv_rows));
+  HK_TRY(dalloc(&e->pf_q, r * d.q_heads * kHeadDim));
+  HK_TRY(dalloc(&e->pf_att, r * d.q_heads * kHeadDim));
+  HK_TRY(dalloc(&e->pf_act, r * d.intermediate));
+  HK_TRY(dalloc(&e->pf_tokens, r));
+  e->pf_rows = kPrefillRows;
+  return 0;
+}
+
+// All layers for tokens[0..n) (already on the device) at slots start..start+n-1.
+int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
+  const hk_model_desc& d = e->d;
+  const hipStream_t s = e->stream;
+  const int H = d.hidden, I = d.intermediate, QD = d.q_heads * kHeadDim;
+  HK_TRY(launch_embed_rows(tokens_dev, n, d.vocab, e->w.token_embedding, H, e->pf_x, s));
+  for (int l = 0; l < d.layers; ++l) {
+    const hk_layer_weights& lw = e->layers[l];
+    HK_TRY(launch_rmsnorm_rows(e->pf_x, H, lw.input_norm, d.rms_eps, e->pf_xn, H, n, H, s));
+    PrefillGemmArgs q = {};
+    q.A = e->pf_xn;
+    q.lda = H;
+    q.W = static_cast<const uint16_t*>(lw.qkv);
+    q.bias = lw.qkv_bias;
+    q.Y = e->pf_qkv;
+    q.ldy = e->qkv_rows;
+    q.M = n;
+    q.N = e->qkv_rows;
+    q.K = H;
+    q.epi = lw.qkv_bias ? EPI_BIAS : EPI_BF16;
+    HK_TRY(launch_prefill_gemm(q, s));
+    PrefillAttnArgs at = {};
+    at.qkv = e->pf_qkv;
+    at.ld_qkv = e->qkv_rows;
+    at.cos_tab = e->w.rope_cos;
+    at.sin_tab = e->w.rope_sin;
+    at.qrot = e->pf_q;
+    at.kcache = e->kcache + (size_t)l * kv_layer_elems(e);
+    at.vcache = e->vcache + (size_t)l * kv_layer_elems(e);
+    at.out = e->pf_att;
+    at.ld_out = QD;
+    at.n = n;
+    at.start = start;
+    at.q_heads = d.q_heads;
+    at.kv_heads = d.kv_heads;
+    at.max_ctx = d.max_context;
+    HK_TRY(launch_prefill_attention(at, s));
+    PrefillGemmArgs o = {};
+    o.A = e->pf_att;
+    o.lda = QD;
+    o.W = static_cast<const uint16_t*>(lw.o_proj);
+    o.resid = e->pf_x;
+    o.ldr = H;
+    o.Y = e->pf_h1;
+    o.ldy = H;
+    o.M = n;
+    o.N = H;
+    o.K = QD;
+    o.epi = EPI_RESID;
+    HK_TRY(launch_prefill_gemm(o, s));
+    HK_TRY(launch_rmsnorm_rows(e->pf_h1, H, lw.post_attn_norm, d.rms_eps, e->pf_xn, H, n, H, s));
+    PrefillGemmArgs g = {};
+    g.A = e->pf_xn;
+    g.lda = H;
+    g.W = static_cast<const uint16_t*>(lw.gate_up);
+    g.Y = e->pf_act;
+    g.ldy = I;
+    g.M = n;
+    g.N = I;
+    g.K = H;
+    g.epi = EPI_SWIGLU;
+    HK_TRY(launch_prefill_gemm(g, s));
+    PrefillGemmArgs dn = {};
+    dn.A = e->pf_act;
+    dn.lda = I;
+    dn.W = static_cast<const uint16_t*>(lw.down_proj);
+    dn.resid = e->pf_h1;
+    dn.ldr = H;
+    dn.Y = e->pf_x;
+    dn.ldy = H;
+    dn.M = n;
+    dn.N = H;
+    dn.K = I;
+    dn.epi = EPI_RESID;
+    HK_TRY(launch_prefill_gemm(dn, s));
+  }
   return 0;
 }
 
@@ -486,6 +596,50 @@ int hk_engine_generate(hk_engine* e, int32_t token, int32_t position, int32_t n_
   return 0;
 }
 
+int hk_engine_prefill(hk_engine* e, const int32_t* tokens_host, int32_t n, int32_t start,
+                      float* logits_host, int32_t* next_token_host) {
+  if (!e || !tokens_host) return fail("hk_engine_prefill: null argument");
+  std::lock_guard<std::mutex> lock(e->mu);
+  if (n <= 0) return fail("hk_engine_prefill: n must be positive");
+  if (start < 0 || (int64_t)start + n > e->d.max_context)
+    return fail("position outside the " + std::to_string(e->d.max_context) + "-token context");
+  for (int i = 0; i < n; ++i)
+    if (tokens_host[i] < 0 || tokens_host[i] >= e->d.vocab) return fail("token id outside the vocabulary");
+  HK_CHECK(hipSetDevice(e->device));
+  const bool want = logits_host != nullptr || next_token_host != nullptr;
+  if (e->w8 || (e->d.hidden % 32) || (e->d.intermediate % 32) || ((e->d.q_heads * kHeadDim) % 32)) {
+    // int8 weights and shapes off the MFMA tile use the decode step per position
+    for (int i = 0; i < n; ++i) {
+      const bool last = want && i == n - 1;
+      HK_TRY(set_ctrl(e, tokens_host[i], start + i, 0));
+      HK_TRY(run_step(e, last));
+    }
+  } else {
+    HK_TRY(prefill_workspace(e));
+    for (int c0 = 0; c0 < n; c0 += e->pf_rows) {
+      const int m = std::min(e->pf_rows, n - c0);
+      HK_CHECK(hipMemcpyAsync(e->pf_tokens, tokens_host + c0, m * sizeof(int32_t),
+                              hipMemcpyHostToDevice, e->stream));
+      HK_TRY(prefill_chunk(e, e->pf_tokens, m, start + c0));
+      if (c0 + m == n && want) {
+        HK_CHECK(hipMemcpyAsync(e->h, e->pf_x + (size_t)(m - 1) * e->d.hidden,
+                                e->d.hidden * sizeof(uint16_t), hipMemcpyDeviceToDevice, e->stream));
+        HK_TRY(set_ctrl(e, -1, start + n - 1, 0));
+        HK_TRY(launch_part(e, HK_PART_HEAD, 0));
+      }
+      HK_CHECK(hipStreamSynchronize(e->stream));  // pf_tokens is reused by the next chunk
+    }
+  }
+  if (logits_host)
+    HK_CHECK(hipMemcpyAsync(logits_host, e->logits, (size_t)e->d.vocab * sizeof(float),
+                            hipMemcpyDeviceToHost, e->stream));
+  if (next_token_host)
+    HK_CHECK(hipMemcpyAsync(next_token_host, e->result, sizeof(int32_t), hipMemcpyDeviceToHost,
+                            e->stream));
+  HK_CHECK(hipStreamSynchronize(e->stream));
+  return 0;
+}
+
 int hk_engine_final_hidden(hk_engine* e, uint16_t* hidden_host) {
   if (!e || !hidden_host) return fail("hk_engine_final_hidden: null argument");
   std::lock_guard<std::mutex> lock(e->mu);
@@ -557,6 +711,28 @@ int hk_gemv_w8(const int8_t* Wq, const float* scale, const uint16_t* x, const fl
                const uint16_t* residual, uint16_t* y, float* y_f32, int32_t M, int32_t K,
                void* stream) {
   return gemv_common(Wq, scale, x, bias, residual, y, y_f32, M, K, true, stream);
+}
+
+int hk_gemm_bf16(const uint16_t* A, int32_t lda, const uint16_t* W, const float* bias,
+                 const uint16_t* residual, uint16_t* Y, int32_t M, int32_t N, int32_t K,
+                 void* stream) {
+  if (!A || !W || !Y) return fail("hk_gemm_bf16: null pointer");
+  if (bias && residual) return fail("hk_gemm_bf16: give bias or residual, not both");
+  if (lda < K) return fail("hk_gemm_bf16: lda below K");
+  PrefillGemmArgs a = {};
+  a.A = A;
+  a.lda = lda;
+  a.W = W;
+  a.bias = bias;
+  a.resid = residual;
+  a.ldr = N;
+  a.Y = Y;
+  a.ldy = N;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.epi = bias ? EPI_BIAS : residual ? EPI_RESID : EPI_BF16;
+  return launch_prefill_gemm(a, static_cast<hipStream_t>(stream));
 }
 
 int hk_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* out, int32_t n,

@@ -97,6 +97,40 @@ inline int attention_splits(int max_ctx) { return (max_ctx + kAttnChunk - 1) / k
 
 int launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 
+// ---- batched prefill (prefill.hip) ----
+
+struct PrefillGemmArgs {
+  const uint16_t* A;      // [M, lda] bf16 activations (tokens x K)
+  const uint16_t* W;      // [N, K] bf16 weights (SwiGLU: [2N, K], gate rows then up rows)
+  const float* bias;      // [N] (EPI_BIAS)
+  const uint16_t* resid;  // [M, ldr] (EPI_RESID)
+  uint16_t* Y;            // [M, ldy] bf16 output
+  int M, N, K, lda, ldr, ldy;
+  int epi;                // EPI_BF16, EPI_BIAS, EPI_RESID or EPI_SWIGLU
+};
+
+int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream);
+
+struct PrefillAttnArgs {
+  const uint16_t* qkv;      // [n, ld_qkv] bf16 rows: q heads, k heads, v heads
+  int ld_qkv;
+  const float* cos_tab;     // [max_ctx, 32]
+  const float* sin_tab;
+  uint16_t* qrot;           // [n, q_heads * 64] rotated queries (written)
+  uint16_t* kcache;         // this layer: [Hkv, max_ctx, 64]
+  uint16_t* vcache;
+  uint16_t* out;            // [n, ld_out] bf16 attention output
+  int ld_out;
+  int n, start, q_heads, kv_heads, max_ctx;
+};
+
+// rope_append then causal attention for tokens start..start+n-1.
+int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream);
+int launch_embed_rows(const int32_t* tokens, int n, int vocab, const uint16_t* table, int H,
+                      uint16_t* X, hipStream_t stream);
+int launch_rmsnorm_rows(const uint16_t* X, int ldx, const uint16_t* gamma, float eps, uint16_t* out,
+                        int ldo, int rows, int H, hipStream_t stream);
+
 // Standalone RMSNorm: out = bf16((v * inv_rms) * gamma).
 int launch_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* out,
                    int n, hipStream_t stream);

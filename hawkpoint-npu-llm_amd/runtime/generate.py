@@ -156,9 +156,9 @@ class NPUDecoder:
         return result
 
     def generate_ids(self, prompt_ids, max_new_tokens):
-        """Greedy generation from token ids with prefix reuse: per-position
-        prefill (logits only at the last prompt position), then the engine's
-        device-driven greedy loop.  Returns ``(token_ids, stats)`` with the
+        """Greedy generation from token ids with prefix reuse: batched prefill
+        of the uncached prompt tail (logits only at the last prompt position),
+        then the engine's device-driven greedy loop.  Returns ``(token_ids, stats)`` with the
         reference's TTFT / decode-rate definitions (generate.py:1110-1188)."""
         if not prompt_ids:
             raise ValueError("prompt must not be empty")
@@ -166,10 +166,11 @@ class NPUDecoder:
             raise ValueError("prompt plus generated tokens exceed the context")
         reused = self._reusable_prefix(prompt_ids)
         t0 = time.perf_counter()
-        last = len(prompt_ids) - 1
-        for i in range(reused, last):
-            self._decode_step(prompt_ids[i], i, compute_logits=False)
-        first, _ = self._decode_step(prompt_ids[last], last)
+        # the un-cached prompt tail in one batched pass (logits at its end only)
+        del self._cached_prefix[reused:]
+        first, _ = self._engine.prefill(prompt_ids[reused:], start=reused, logits=True,
+                                        want_logits_array=False)
+        self._cached_prefix = [int(t) for t in prompt_ids]
         ttft = time.perf_counter() - t0
         tokens = [first]
         t1 = time.perf_counter()

@@ -90,6 +90,7 @@ _SIGNATURES = {
     ),
     "hk_engine_step": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "hk_engine_generate": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp]),
+    "hk_engine_prefill": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "hk_engine_final_hidden": (ctypes.c_int, [_vp, _vp]),
     "hk_engine_read_kv": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp]),
     "hk_engine_launch_part": (ctypes.c_int, [_vp, _i32, _i32]),
@@ -98,6 +99,7 @@ _SIGNATURES = {
     "hk_engine_destroy": (None, [_vp]),
     "hk_gemv_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "hk_gemv_w8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
+    "hk_gemm_bf16": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "hk_rmsnorm": (ctypes.c_int, [_vp, _vp, _f32, _vp, _i32, _vp]),
     "hk_swiglu": (ctypes.c_int, [_vp, _vp, _i32, _vp]),
     "hk_argmax_f32": (ctypes.c_int, [_vp, _i32, _vp, _vp]),

@@ -195,6 +195,26 @@ class QwenDecoderEngine:
         )
         return int(self._token.value), (np.array(out, copy=True) if out is not None else None)
 
+    def prefill(self, token_ids, start=0, logits=True, want_logits_array=True):
+        """All prompt tokens at slots start..start+n-1 in one batched pass
+        (MFMA GEMMs, causal attention).  Returns ``(next_token, logits)`` for
+        the last token, or ``(None, None)`` with ``logits=False``."""
+        ids = np.ascontiguousarray(np.asarray(token_ids, dtype=np.int32))
+        if ids.ndim != 1 or ids.size == 0:
+            raise ValueError("prefill needs a non-empty 1-D list of token ids")
+        out = self._logits if (logits and want_logits_array) else None
+        hip.check(
+            self._lib.hk_engine_prefill(
+                self._live(), ids.ctypes.data, int(ids.size), int(start),
+                out.ctypes.data if out is not None else None,
+                ctypes.byref(self._token) if logits else None,
+            ),
+            "hk_engine_prefill",
+        )
+        if not logits:
+            return None, None
+        return int(self._token.value), (np.array(out, copy=True) if out is not None else None)
+
     def generate(self, token_id, position, n_steps):
         """Greedy decode: ``n_steps`` tokens starting from ``token_id`` at
         ``position`` (the token fed at step i is the argmax of step i-1)."""

@@ -112,6 +112,18 @@ int hk_engine_step(hk_engine* engine, int32_t token, int32_t position, int32_t w
 int hk_engine_generate(hk_engine* engine, int32_t token, int32_t position, int32_t n_steps,
                        int32_t* tokens_host);
 
+/* Batched prefill of `n` prompt tokens at slots start..start+n-1: every layer
+ * runs on all tokens at once (MFMA bf16 GEMMs, causal GQA attention), the KV
+ * cache gets all n slots, and, when `logits_host` or `next_token_host` is
+ * non-NULL, the final norm + LM head + argmax run for the last token.  The
+ * result equals n hk_engine_step calls (logits at the last one only) up to
+ * float32 summation order.  Replaces the reference's per-position prefill
+ * loop (npu_llm/runtime/generate.py:1110-1125) and the engine's lm_head=False
+ * dispatches (npu_llm/designs/qwen_engine.py:213-219).  Prompts longer than
+ * 512 tokens run in 512-token chunks. */
+int hk_engine_prefill(hk_engine* engine, const int32_t* tokens_host, int32_t n, int32_t start,
+                      float* logits_host, int32_t* next_token_host);
+
 /* Final-RMSNorm output ([H] bf16) of the hidden state left by the last step:
  * the value DecoderEngine.step returns (npu_llm/runtime/engine.py:65-82). */
 int hk_engine_final_hidden(hk_engine* engine, uint16_t* hidden_host);
@@ -164,6 +176,16 @@ int hk_gemv_bf16(const uint16_t* W, const uint16_t* x, const float* bias,
 int hk_gemv_w8(const int8_t* Wq, const float* scale, const uint16_t* x, const float* bias,
                const uint16_t* residual, uint16_t* y, float* y_f32, int32_t M, int32_t K,
                void* stream);
+
+/* Y[m, n] = epilogue(sum_k A[m, k] * W[n, k]) for bf16 A [M, K] (row stride
+ * lda) and W [N, K]; float32 accumulation on the matrix cores; the epilogue
+ * is bf16(acc), or bf16(f32(bf16(acc)) + bias[n]) / + residual[m, n] (row
+ * stride N) when given.  The batched form of hk_gemv_bf16 used by prefill
+ * (the reference has no batched projection: it prefills position by
+ * position, npu_llm/runtime/generate.py:1110-1125).  K must be a multiple of 32. */
+int hk_gemm_bf16(const uint16_t* A, int32_t lda, const uint16_t* W, const float* bias,
+                 const uint16_t* residual, uint16_t* Y, int32_t M, int32_t N, int32_t K,
+                 void* stream);
 
 /* out = bf16((v * inv_rms) * gamma) (cpu_backend.py:71-76; designs/rmsnorm.py). */
 int hk_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* out, int32_t n,

@@ -34,3 +34,26 @@ def bf16_ulp_diff(a_bits, b_bits):
         b = np.asarray(bits, dtype=np.uint16).astype(np.int32)
         return np.where(b & 0x8000, -(b & 0x7FFF), b)
     return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+def fwd_bound(w64, x64):
+    """Forward error bound of a float32 dot product of length K (rows of w64)."""
+    k = w64.shape[-1]
+    gamma = k * 2.0**-24 / (1 - k * 2.0**-24)
+    return 1.01 * gamma * (np.abs(w64) @ np.abs(x64)) + 1e-30
+
+
+def ulp_bf16(x):
+    x = np.abs(np.asarray(x, np.float64))
+    return 2.0 ** (np.floor(np.log2(np.maximum(x, 2.0**-126))) - 7)
+
+
+def check_bf16(y_bits, ref_bits, sum_bound, exact_frac=0.97):
+    """Two float32 sums, each within `sum_bound` of exact, rounded to bf16 may
+    differ by both errors plus one bf16 step; most should agree exactly."""
+    from oracle import bf16
+
+    y = bf16.from_bits(y_bits).astype(np.float64)
+    ref = bf16.from_bits(ref_bits).astype(np.float64)
+    assert np.all(np.abs(y - ref) <= ulp_bf16(ref) + 2 * sum_bound)
+    assert (np.asarray(y_bits) == np.asarray(ref_bits)).mean() >= exact_frac

@@ -1,0 +1,154 @@
+"""Batched prefill on the GPU: the MFMA GEMM against the oracle's projection
+arithmetic, and whole-model prefill against the oracle's per-position prefill
+(the reference's own prefill, npu_llm/runtime/generate.py:1110-1125)."""
+
+import numpy as np
+import pytest
+
+from _util import announce, check_bf16, fwd_bound, near_tie, rel_l2
+from oracle import bf16
+from oracle.cpu_backend import OracleDecoder
+from runtime.synthetic import QWEN25_05B, SMOLLM2_135M, SyntheticModel
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(array):
+    from runtime import hip
+
+    return hip.DeviceBuffer.from_array(np.ascontiguousarray(array))
+
+
+@pytest.mark.parametrize(
+    "m,n,k,epi",
+    [(40, 1152, 896, "bias"), (40, 896, 896, "resid"), (100, 4864, 896, "none"),
+     (40, 896, 4864, "resid"), (1, 576, 576, "none"), (513, 64, 32, "none"), (70, 960, 576, "bias")],
+)
+def test_gemm_bf16_matches_oracle(hk_lib, m, n, k, epi):
+    from runtime import hip
+
+    announce(f"gemm M={m} N={n} K={k} {epi}")
+    rng = np.random.default_rng(m * 7 + n + k)
+    a_bits = bf16.to_bits(rng.normal(0, 1, (m, k)).astype(np.float32))
+    w_bits = bf16.to_bits(rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    bias = rng.normal(0, 0.02, n).astype(np.float32) if epi == "bias" else None
+    resid = bf16.to_bits(rng.normal(0, 1, (m, n)).astype(np.float32)) if epi == "resid" else None
+    A, W, Y = _dev(a_bits), _dev(w_bits), hip.DeviceBuffer(2 * m * n)
+    B = _dev(bias) if bias is not None else None
+    R = _dev(resid) if resid is not None else None
+    hip.check(hk_lib.hk_gemm_bf16(A.ptr, k, W.ptr, B.ptr if B else None, R.ptr if R else None,
+                                  Y.ptr, m, n, k, None), "gemm")
+    hip.check(hk_lib.hk_stream_sync(None), "sync")
+    y = Y.read(np.uint16, m * n).reshape(m, n)
+    a64 = bf16.from_bits(a_bits).astype(np.float64)
+    w64 = bf16.from_bits(w_bits).astype(np.float64)
+    proj = bf16.round_f32(bf16.from_bits(a_bits) @ bf16.from_bits(w_bits).T)
+    bound = fwd_bound(a64, w64.T)  # [m, n]
+    if epi == "bias":
+        ref = bf16.to_bits(proj + bias)
+    elif epi == "resid":
+        ref = bf16.to_bits(proj + bf16.from_bits(resid))
+        bound = bound + 2.0 ** (np.floor(np.log2(np.maximum(np.abs(proj), 2.0**-126))) - 7)
+    else:
+        ref = bf16.to_bits(proj)
+    check_bf16(y, ref, bound)
+
+
+def _prefill_case(model, prompt, new_tokens, context, tol, label):
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce(f"prefill parity {label}: prompt {len(prompt)} ctx {context}")
+    oracle = OracleDecoder(model, context)
+    ref_tokens, ref_logits = oracle.generate_greedy(prompt, new_tokens)
+    engine = QwenDecoderEngine(model, context_length=context)
+    try:
+        tok, logits = engine.prefill(prompt, 0)
+        err = rel_l2(logits, ref_logits[0])
+        announce(f"  prefill logits rel-L2 {err:.3e}, token {tok} oracle {ref_tokens[0]}")
+        assert err <= tol
+        assert tok == ref_tokens[0] or near_tie(ref_logits[0])
+        # KV slots of the prompt against the oracle's caches
+        for layer in (0, model.metadata["layers"] - 1):
+            for slot in (0, len(prompt) - 1):
+                k, v = engine.read_kv(layer, slot)
+                rk = bf16.from_bits(oracle.stage.key_cache[layer][:, slot])
+                rv = bf16.from_bits(oracle.stage.value_cache[layer][:, slot])
+                assert np.abs(bf16.from_bits(k) - rk).max() <= 0.05 * np.abs(rk).max() + 1e-3
+                assert np.abs(bf16.from_bits(v) - rv).max() <= 0.05 * np.abs(rv).max() + 1e-3
+        if tok == ref_tokens[0] and new_tokens > 1:
+            gen = engine.generate(tok, len(prompt), new_tokens - 1)
+            for i, (a, b) in enumerate(zip(gen, ref_tokens[1:])):
+                if a != b:
+                    assert near_tie(ref_logits[i + 1]), f"token {i + 1}: gpu {a} oracle {b}"
+                    break
+    finally:
+        engine.close()
+
+
+def _prompt(vocab, n, seed):
+    rng = np.random.default_rng(seed)
+    return [int(t) for t in rng.integers(0, vocab, n)]
+
+
+def test_prefill_qwen_4_layer():
+    model = SyntheticModel(QWEN25_05B, seed=0, layers=4)
+    _prefill_case(model, _prompt(151936, 40, 12), 8, 72, 1e-2, "qwen2.5-0.5b-4L")
+
+
+def test_prefill_smollm_4_layer():
+    model = SyntheticModel(SMOLLM2_135M, seed=0, layers=4)
+    _prefill_case(model, _prompt(49152, 35, 11), 8, 64, 1e-2, "smollm2-135m-4L")
+
+
+def test_prefill_qwen_full_depth():
+    model = SyntheticModel(QWEN25_05B, seed=0)
+    _prefill_case(model, _prompt(151936, 40, 12), 4, 72, 2.5e-2, "qwen2.5-0.5b")
+
+
+def test_prefill_chunked_long_prompt():
+    """600 tokens: a 512-token chunk then an 88-token chunk that attends to it
+    (multi-chunk causal attention past 256 slots)."""
+    model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
+    _prefill_case(model, _prompt(151936, 600, 14), 4, 1024, 1e-2, "qwen-2L-600")
+
+
+def test_prefill_continues_from_cached_prefix():
+    """Prefill at start > 0 after earlier steps equals a prefill from 0."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("prefill at an offset")
+    model = SyntheticModel(QWEN25_05B, seed=2, layers=2)
+    prompt = _prompt(151936, 30, 15)
+    engine = QwenDecoderEngine(model, context_length=64)
+    try:
+        t_full, l_full = engine.prefill(prompt, 0)
+        engine.reset()
+        engine.prefill(prompt[:10], 0, logits=False)
+        t_part, l_part = engine.prefill(prompt[10:], 10)
+        assert t_part == t_full
+        assert rel_l2(l_part, l_full) <= 1e-3
+        with pytest.raises(ValueError):
+            engine.prefill(prompt, 50)
+        with pytest.raises(ValueError):
+            engine.prefill([151936], 0)
+    finally:
+        engine.close()
+
+
+def test_prefill_w8_uses_step_path():
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("prefill W8 (per-position path)")
+    model = SyntheticModel(QWEN25_05B, seed=3, layers=2)
+    prompt = _prompt(151936, 12, 16)
+    engine = QwenDecoderEngine(model, context_length=32, w8=True)
+    try:
+        t1, l1 = engine.prefill(prompt, 0)
+        engine.reset()
+        for pos, tok in enumerate(prompt[:-1]):
+            engine.step_token(tok, pos, logits=False)
+        t2, l2 = engine.step_token(prompt[-1], len(prompt) - 1)
+        assert t1 == t2
+        np.testing.assert_array_equal(l1, l2)
+    finally:
+        engine.close()
