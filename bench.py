@@ -33,6 +33,7 @@ for p in (str(ROOT), str(ROOT / "hawkpoint-npu-llm_amd")):
 
 METRIC = "decode tok/s @batch1 + HBM GB/s (% peak), Qwen2.5-0.5B-shape bf16"
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK = 2.5e15  # MI355X dense bf16 matrix peak, FLOP/s
 PROMPT = 40
 RUN = 31  # decode steps per run after the prefill token (positions 40..70)
 REFERENCE_TOKS = 28.83  # XDNA1 Qwen2.5-0.5B engine decode (reference README.md:92)
@@ -53,6 +54,13 @@ def step_bytes(meta, position):
     head = 2 * meta["vocab_size"] * h + 2 * h
     kv_slot = meta["layers"] * 2 * nkv * d * 2
     return meta["layers"] * per_layer + head + 2 * h + kv_slot * (position + 1) + kv_slot
+
+
+def layer_params(meta):
+    """Projection weights that every token multiplies (all layers, no head)."""
+    h, i = meta["hidden_size"], meta["intermediate_size"]
+    nq, nkv, d = meta["attention_heads"], meta["kv_heads"], meta["head_dim"]
+    return meta["layers"] * ((nq + 2 * nkv) * d * h + h * nq * d + 2 * i * h + h * i)
 
 
 def part_bytes(meta, part):
@@ -144,20 +152,31 @@ def main():
     engine = QwenDecoderEngine(model, context_length=4096)
     lib = hip.lib()
 
-    def prefill():
+    def prefill_per_position():
         for pos, tok in enumerate(prompt[:-1]):
             engine.step_token(tok, pos, logits=False)
         first, _ = engine.step_token(prompt[-1], PROMPT - 1, logits=True, want_logits_array=False)
         return first
 
-    first = prefill()  # captures both graphs
+    def timed(fn, reps=5):
+        times, out = [], None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            out = fn()
+            times.append(time.perf_counter() - t0)
+        return out, sorted(times)[len(times) // 2]
+
+    first = prefill_per_position()  # captures both graphs
     if args.probe:
         probe(engine, meta, args.kernel_launches)
         return
-    t0 = time.perf_counter()
-    first = prefill()
-    ttft = time.perf_counter() - t0
-    log(f"prefill {PROMPT} positions: TTFT {ttft * 1e3:.2f} ms, first token {first}")
+    first_pp, ttft_pp = timed(prefill_per_position, 3)
+    first, ttft = timed(lambda: engine.prefill(prompt, 0, want_logits_array=False)[0])
+    if first != first_pp:
+        log(f"note: batched and per-position prefill pick {first} / {first_pp} (near-tie)")
+    prefill_flops = 2.0 * PROMPT * layer_params(meta)
+    log(f"prefill {PROMPT} tokens: TTFT batched {ttft * 1e3:.2f} ms, per position "
+        f"{ttft_pp * 1e3:.2f} ms, first token {first}")
 
     def decode(n):
         tokens = []
@@ -198,6 +217,20 @@ def main():
     dom_bytes = part_bytes(meta, dominant)
     achieved = dom_bytes / (parts[dominant] * 1e-6) / 1e9
     log("kernel us/launch: " + ", ".join(f"{k} {v:.2f}" for k, v in parts.items()))
+
+    # context 4096: a 4064-token prompt in one batched prefill, then 31 greedy
+    # decode steps at positions 4064..4094
+    long_n = 4064
+    long_prompt = [int(t) for t in rng.integers(0, meta["vocab_size"], long_n)]
+    tok_long, t_long = timed(lambda: engine.prefill(long_prompt, 0, want_logits_array=False)[0], 2)
+    attn_flops = 4.0 * meta["attention_heads"] * meta["head_dim"] * meta["layers"] * long_n * (long_n + 1) / 2
+    long_flops = 2.0 * long_n * layer_params(meta) + attn_flops
+    hip.check(lib.hk_stream_sync(engine.stream), "sync")
+    t0 = time.perf_counter()
+    engine.generate(tok_long, long_n, RUN)
+    long_decode = RUN / (time.perf_counter() - t0)
+    log(f"ctx 4096: prefill {long_n} tokens {t_long * 1e3:.1f} ms "
+        f"({long_flops / t_long / 1e12:.1f} TFLOP/s), decode {long_decode:.1f} tok/s")
     engine.close()
     traffic = None
     tfile = ROOT / "profiles" / f"traffic_{dominant}_qwen05b.json"
@@ -228,6 +261,21 @@ def main():
             "kv_slots_allocated": 4096,
         },
         "ttft_ms": round(ttft * 1e3, 3),
+        "prefill": {
+            "tokens": PROMPT,
+            "batched_ms": round(ttft * 1e3, 3),
+            "per_position_ms": round(ttft_pp * 1e3, 3),
+            "mfma_tflops": round(prefill_flops / ttft / 1e12, 3),
+            "mfma_frac_of_bf16_dense": round(prefill_flops / ttft / BF16_PEAK, 5),
+        },
+        "long_context": {
+            "prompt_tokens": long_n,
+            "prefill_ms": round(t_long * 1e3, 2),
+            "prefill_tflops": round(long_flops / t_long / 1e12, 2),
+            "prefill_mfma_frac_of_bf16_dense": round(long_flops / t_long / BF16_PEAK, 4),
+            "decode_tok_s": round(long_decode, 1),
+            "decode_positions": [long_n, long_n + RUN - 1],
+        },
         "step_hbm_gbs": round(step_gbs, 1),
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "step_bytes": int(step_bytes(meta, mean_pos)),

@@ -107,6 +107,19 @@ struct PrefillGemmArgs {
   uint16_t* Y;            // [M, ldy] bf16 output
   int M, N, K, lda, ldr, ldy;
   int epi;                // EPI_BF16, EPI_BIAS, EPI_RESID or EPI_SWIGLU
+  // Grouped mode (routed experts), on when grp_count is set: workgroup z of
+  // the third grid dimension computes group z < *n_groups with weights
+  // W + grp_expert[z] * w_stride, grp_count[z] rows whose output rows are
+  // grp_offset[z] + m and whose A rows are a_rows[grp_offset[z] + m] (or
+  // grp_offset[z] + m when a_rows is null).
+  const int32_t* a_rows;
+  const int32_t* grp_expert;
+  const int32_t* grp_count;
+  const int32_t* grp_offset;
+  const int32_t* n_groups;
+  long long w_stride;
+  int max_groups;         // grid size in z
+  int max_rows;           // rows per group bound (grid size in y = ceil / 64)
 };
 
 int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream);

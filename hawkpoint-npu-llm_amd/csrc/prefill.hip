@@ -50,14 +50,30 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
   const int wm = (wave >> 1) * 32;  // wave's token offset in the tile
   const int wn = (wave & 1) * 32;   // wave's output offset in the tile
 
+  // Grouped mode: this workgroup's expert, row count and row offset.
+  const uint16_t* Wb = a.W;
+  int M = a.M;
+  int row_off = 0;
+  const bool grouped = a.grp_count != nullptr;
+  if (grouped) {
+    const int z = blockIdx.z;
+    if (z >= *a.n_groups) return;
+    M = a.grp_count[z];
+    if (m0 >= M) return;
+    row_off = a.grp_offset[z];
+    Wb = a.W + (size_t)a.grp_expert[z] * (size_t)a.w_stride;
+  }
+
   // one 16-byte piece of each tile per thread: row = tid / 4, k8 = (tid % 4) * 8
   const int lr = tid >> 2;
   const int lk = (tid & 3) * 8;
-  const bool a_ok = (m0 + lr) < a.M;
+  const bool a_ok = (m0 + lr) < M;
   const bool w_ok = (n0 + lr) < a.N;
-  const uint16_t* a_src = a.A + (size_t)(a_ok ? m0 + lr : 0) * a.lda + lk;
-  const uint16_t* w_src = a.W + (size_t)(w_ok ? n0 + lr : 0) * a.K + lk;
-  const uint16_t* u_src = a.W + (size_t)(w_ok ? n0 + lr + a.N : 0) * a.K + lk;
+  int arow = a_ok ? m0 + lr : 0;
+  if (grouped) arow = a.a_rows ? a.a_rows[row_off + (a_ok ? m0 + lr : 0)] : row_off + arow;
+  const uint16_t* a_src = a.A + (size_t)arow * a.lda + lk;
+  const uint16_t* w_src = Wb + (size_t)(w_ok ? n0 + lr : 0) * a.K + lk;
+  const uint16_t* u_src = Wb + (size_t)(w_ok ? n0 + lr + a.N : 0) * a.K + lk;
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
   f32x4 acc[2][2], accu[2][2];
@@ -107,9 +123,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
+        const int mt = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
         const int n = n0 + wn + j * 16 + (lane & 15);
-        if (m >= a.M || n >= a.N) continue;
+        if (mt >= M || n >= a.N) continue;
+        const int m = row_off + mt;
         const float v = acc[i][j][r];
         uint16_t* y = a.Y + (size_t)m * a.ldy + n;
         switch (a.epi) {
@@ -338,7 +355,14 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0) return fail("prefill gemm: sizes must be positive");
   if (a.K % kTK != 0) return fail("prefill gemm: K must be a multiple of 32");
   if (a.lda % 8 != 0) return fail("prefill gemm: lda must be a multiple of 8");
-  const dim3 grid((a.N + kTN - 1) / kTN, (a.M + kTM - 1) / kTM);
+  dim3 grid((a.N + kTN - 1) / kTN, (a.M + kTM - 1) / kTM);
+  if (a.grp_count != nullptr) {
+    if (a.max_groups <= 0 || a.max_rows <= 0 || a.n_groups == nullptr || a.grp_expert == nullptr ||
+        a.grp_offset == nullptr)
+      return fail("grouped gemm: group description incomplete");
+    grid.y = (a.max_rows + kTM - 1) / kTM;
+    grid.z = a.max_groups;
+  }
   if (a.epi == EPI_SWIGLU)
     hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a);
   else

@@ -108,6 +108,10 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     ),
     "hk_stream_sync": (ctypes.c_int, [_vp]),
+    "hk_moe_create": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp)]),
+    "hk_moe_forward": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "hk_moe_experts": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "hk_moe_destroy": (None, [_vp]),
     "hk_malloc": (ctypes.c_int, [ctypes.c_uint64, ctypes.POINTER(_vp)]),
     "hk_free": (ctypes.c_int, [_vp]),
     "hk_memcpy_h2d": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64]),

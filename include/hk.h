@@ -209,6 +209,45 @@ int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float*
 /* Wait for all work on `stream`. */
 int hk_stream_sync(void* stream);
 
+/* ---- routed-expert (MoE) block ----
+ * Expert weights (device, bf16, caller-owned): router [E, H]; gate_up
+ * [E + S, 2 I, H] (gate rows then up rows); down [E + S, H, I].  Routed experts
+ * are 0..E-1, the S shared experts follow.  Per token: r = router @ x (f32),
+ * p = softmax(r), the top_k experts by p (ties to the lower id) weighted by p,
+ * each expert bf16(down @ bf16(silu(bf16(gate @ x)) * bf16(up @ x))), and
+ * y = bf16(sum_k p_k e_k + sum_s e_s). */
+typedef struct hk_moe hk_moe;
+
+typedef struct hk_moe_desc {
+  int32_t hidden;       /* H, multiple of 32 */
+  int32_t intermediate; /* I, multiple of 32 */
+  int32_t experts;      /* routed experts E, at most 64 */
+  int32_t shared;       /* shared experts S, at most 8 */
+  int32_t top_k;        /* at most 16 */
+  int32_t max_tokens;   /* largest batch, at most 256 */
+} hk_moe_desc;
+
+int hk_moe_create(const hk_moe_desc* desc, const uint16_t* router, const uint16_t* gate_up,
+                  const uint16_t* down, hk_moe** out);
+
+/* Router + top-k + experts + combine for x [tokens, H] -> y [tokens, H]
+ * (device pointers).  ids_out [tokens, top_k] int32 and weights_out float32
+ * (device, optional) receive the routing.  No reference counterpart for the
+ * router (the reference routes in upstream ggml/Colibri); the expert part
+ * replaces compute_experts (ollama-xdna/backend/ggml-xdna.cpp:1301-1441). */
+int hk_moe_forward(hk_moe* moe, const uint16_t* x, int32_t tokens, uint16_t* y, int32_t* ids_out,
+                   float* weights_out, void* stream);
+
+/* Experts + combine with caller routing (device ids [tokens, top_k], weights
+ * [tokens, top_k]): the GGML MUL_MAT_ID contract
+ * (ollama-xdna/backend/ggml-xdna.cpp:1681-1716, 1301-1441) and Colibri's
+ * expert group (colibri-xdna/backend/backend_xdna.cpp:316-348).  Ids outside
+ * [0, experts) are rejected. */
+int hk_moe_experts(hk_moe* moe, const uint16_t* x, int32_t tokens, const int32_t* ids,
+                   const float* weights, uint16_t* y, void* stream);
+
+void hk_moe_destroy(hk_moe* moe);
+
 /* ---- device memory, streams and events (the engine's buffer plumbing) ----
  * They stand in for the reference's XRT buffer objects (iron.tensor /
  * iron.zeros, npu_llm/runtime/qwen_engine.py:52-59) so a host needs no other
