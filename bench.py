@@ -99,6 +99,67 @@ def cpu_baseline(model, prompt, decode_steps):
 
 
 COPY_BYTES = 256 << 20
+GEMV_SHAPES = [  # (name, M, K): Qwen2.5-0.5B projections
+    ("qkv", 1152, 896), ("o_proj", 896, 896), ("gate_up", 9728, 896), ("down_proj", 896, 4864),
+    ("lm_head", 151936, 896)]
+ROTATE_BYTES = 512 << 20
+
+
+def gemv_microbench(launches=200):
+    """Isolated batch-1 GEMVs at the Qwen2.5-0.5B projection shapes, bf16 and
+    W8 (int8 + per-row scale) weights, float32 output.  Each shape rotates
+    through enough distinct weight copies to exceed 512 MiB, so the 256 MB
+    Infinity Cache cannot serve them; timed with HIP events around the
+    enqueued launches.  Bytes per launch = weights (+ scales) + x + y."""
+    import ctypes
+
+    import numpy as np
+
+    from runtime import hip
+    from runtime.bf16 import to_bits
+    from runtime.synthetic import quantize_rows
+
+    lib = hip.lib()
+    rng = np.random.default_rng(2)
+    out = {}
+    for name, m, k in GEMV_SHAPES:
+        w = rng.standard_normal((m, k), dtype=np.float32) * np.float32(0.02)
+        x = hip.DeviceBuffer.from_array(to_bits(rng.standard_normal(k, dtype=np.float32)))
+        y = hip.DeviceBuffer(4 * m)
+        for dtype in ("bf16", "w8"):
+            if dtype == "bf16":
+                data, scale = to_bits(w), None
+            else:
+                data, scale = quantize_rows(from_bf16(to_bits(w)))
+            wbytes = data.nbytes
+            copies = max(2, -(-ROTATE_BYTES // wbytes))
+            first = hip.DeviceBuffer.from_array(data)
+            bufs = [first] + [hip.DeviceBuffer(wbytes) for _ in range(copies - 1)]
+            for b in bufs[1:]:
+                hip.check(lib.hk_memcpy_d2d(b.ptr, first.ptr, wbytes), "copy")
+            ptrs = (ctypes.c_void_p * copies)(*[b.ptr for b in bufs])
+            sbuf = hip.DeviceBuffer.from_array(scale) if scale is not None else None
+            sptrs = (ctypes.c_void_p * copies)(*([sbuf.ptr] * copies)) if sbuf else None
+            ev0, ev1 = hip.Event(), hip.Event()
+            hip.check(lib.hk_gemv_repeat(ptrs, sptrs, copies, x.ptr, y.ptr, m, k, copies, None), "warm")
+            ev0.record(None)
+            hip.check(lib.hk_gemv_repeat(ptrs, sptrs, copies, x.ptr, y.ptr, m, k, launches, None), "gemv")
+            ev1.record(None)
+            us = ev0.elapsed_ms(ev1) * 1e3 / launches
+            nbytes = wbytes + (4 * m if scale is not None else 0) + 2 * k + 4 * m
+            out[f"{name}_{dtype}"] = {"M": m, "K": k, "us": round(us, 3), "bytes": nbytes,
+                                      "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                      "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "rotated_copies": copies}
+            for b in bufs:
+                b.free()
+    return out
+
+
+def from_bf16(bits):
+    from runtime.bf16 import from_bits
+
+    return from_bits(bits)
 
 
 def probe(engine, meta, launches):
@@ -128,6 +189,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=310)
     ap.add_argument("--kernel-launches", type=int, default=240)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-microbench", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--probe", action="store_true",
                     help="only the counter-calibration workload: launches of the gate/up "
@@ -205,11 +267,10 @@ def main():
     for name, part in hip.PARTS.items():
         n = args.kernel_launches
         ev0, ev1 = hip.Event(), hip.Event()
-        for i in range(8):
-            hip.check(lib.hk_engine_launch_part(engine._engine, part, i % layers), "launch_part")
+        # one captured graph of n launches (layer i % 24), replayed once to warm
+        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, part, n), "launch_part_repeat")
         ev0.record(stream)
-        for i in range(n):
-            hip.check(lib.hk_engine_launch_part(engine._engine, part, i % layers), "launch_part")
+        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, part, n), "launch_part_repeat")
         ev1.record(stream)
         parts[name] = ev0.elapsed_ms(ev1) * 1e3 / n
     per_step = {k: v * (1 if k == "lm_head" else layers) for k, v in parts.items()}
@@ -291,6 +352,10 @@ def main():
         },
         "baseline_source": "28.83 tok/s, XDNA1 NPU Qwen2.5-0.5B engine (reference README.md:92)",
     }
+    if not args.no_microbench:
+        log("GEMV microbench (512 MiB rotation)")
+        result["gemv_microbench"] = gemv_microbench()
+        log(" ".join(f"{k}:{v['gbs']:.0f}GB/s" for k, v in result["gemv_microbench"].items()))
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
         result["cpu_baseline"] = cpu_baseline(model, prompt[:8], args.cpu_steps)

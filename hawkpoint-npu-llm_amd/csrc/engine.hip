@@ -12,6 +12,7 @@
 // one captured hipGraph per variant (with / without the head) serves every
 // position; the host only rewrites the control block between replays.
 #include <algorithm>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -154,6 +155,7 @@ struct hk_engine {
   int32_t* out_tokens = nullptr;  // [max_ctx]
   int32_t* result = nullptr;
   hipGraphExec_t graph[2] = {nullptr, nullptr};
+  std::map<long long, hipGraphExec_t> repeat_graphs;  // timing graphs by (part, count)
   bool use_graph = true;
   // batched-prefill workspace, allocated on first use for kPrefillRows tokens
   int pf_rows = 0;
@@ -330,6 +332,7 @@ int set_ctrl(hk_engine* e, int32_t token, int32_t position, int32_t advance) {
 void free_engine(hk_engine* e) {
   for (auto& g : e->graph)
     if (g) (void)hipGraphExecDestroy(g);
+  for (auto& kv : e->repeat_graphs) (void)hipGraphExecDestroy(kv.second);
   void* bufs[] = {e->h,       e->h1,       e->qkv,      e->attn,       e->act,
                   e->normed,  e->logits,   e->kcache,   e->vcache,     e->partial,
                   e->counters, e->keys,    e->ctrl,     e->out_tokens, e->result,
@@ -659,6 +662,50 @@ int hk_engine_launch_part(hk_engine* e, int32_t part, int32_t layer) {
   HK_CHECK(hipSetDevice(e->device));
   if (part == HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
   return launch_part(e, part, layer);
+}
+
+int hk_engine_launch_part_repeat(hk_engine* e, int32_t part, int32_t count) {
+  if (!e) return fail("hk_engine_launch_part_repeat: null engine");
+  std::lock_guard<std::mutex> lock(e->mu);
+  if (part < HK_PART_QKV || part > HK_PART_HEAD) return fail("hk_engine_launch_part_repeat: unknown part");
+  if (count <= 0 || count > 100000) return fail("hk_engine_launch_part_repeat: count out of range");
+  HK_CHECK(hipSetDevice(e->device));
+  if (part == HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
+  const long long key = (long long)part << 32 | (unsigned)count;
+  auto it = e->repeat_graphs.find(key);
+  if (it == e->repeat_graphs.end()) {
+    hipGraph_t graph = nullptr;
+    HK_CHECK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    int rc = 0;
+    for (int i = 0; i < count && rc == 0; ++i) rc = launch_part(e, part, i % e->d.layers);
+    const hipError_t end = hipStreamEndCapture(e->stream, &graph);
+    if (rc != 0) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return rc;
+    }
+    if (end != hipSuccess) return hip_fail(end, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (inst != hipSuccess) return hip_fail(inst, "hipGraphInstantiate");
+    it = e->repeat_graphs.emplace(key, exec).first;
+  }
+  HK_CHECK(hipGraphLaunch(it->second, e->stream));
+  return 0;
+}
+
+int hk_gemv_repeat(const void* const* weights, const float* const* scales, int32_t n_weights,
+                   const uint16_t* x, float* y_f32, int32_t M, int32_t K, int32_t count,
+                   void* stream) {
+  if (!weights || !x || !y_f32 || n_weights <= 0 || count <= 0)
+    return fail("hk_gemv_repeat: bad argument");
+  for (int i = 0; i < count; ++i) {
+    const int j = i % n_weights;
+    const int rc = gemv_common(weights[j], scales ? scales[j] : nullptr, x, nullptr, nullptr,
+                               nullptr, y_f32, M, K, scales != nullptr, stream);
+    if (rc != 0) return rc;
+  }
+  return 0;
 }
 
 int hk_engine_read_kv(hk_engine* e, int32_t layer, int32_t slot, uint16_t* k_host,

@@ -249,6 +249,159 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// bf16 GEMV with x in registers: every lane loads the x chunks that match its
+// weight chunks straight from memory (L2-resident), and for RMSNorm each wave
+// reduces the sum of squares over the whole x itself, so the kernel needs no
+// LDS staging and no workgroup barrier before the first FMA.  Used when each
+// wave owns about one row group (all projections but the LM head); measured
+// 20-25% faster than the LDS-staged form on the 896- and 4864-wide rows.
+template <int LPR, int NJ, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(GemvArgs a) {
+  __shared__ unsigned long long wave_keys[kWaves];
+  constexpr int RPW = 64 / LPR;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l = lane % LPR;
+  const int sub = lane / LPR;
+  const int K = a.K;
+  const int CH = K >> 3;
+  const size_t row_bytes = (size_t)K * 2;
+  const size_t pair_off = (size_t)a.M * row_bytes;
+  const int groups = (a.M + RPW - 1) / RPW;
+  const int stride = gridDim.x * kWaves;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  const uint16_t* x = a.x;
+  if (a.x_index != nullptr) {
+    int t = *a.x_index;
+    if (t >= 0) {
+      if (t >= a.vocab_limit) t = a.vocab_limit - 1;
+      x = a.x_table + (size_t)t * (size_t)K;
+      if (a.x_copy != nullptr && blockIdx.x == 0) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(x);
+        for (int i = tid; i < K / 2; i += kThreads) reinterpret_cast<uint32_t*>(a.x_copy)[i] = src[i];
+      }
+    }
+  }
+
+  u32x4 wa[NJ], wb[NJ];
+  u32x4 ua[PAIR ? NJ : 1], ub[PAIR ? NJ : 1];
+  auto load = [&](int g, u32x4 (&w)[NJ], u32x4 (&u)[PAIR ? NJ : 1]) {
+    const int row = g * RPW + sub;
+    const bool live = g < groups && row < a.M;
+    const char* wrow = static_cast<const char*>(a.W) + (size_t)(live ? row : 0) * row_bytes;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = l + j * LPR;
+      const bool ok = live && c < CH;
+      w[j] = ok ? load_stream16(wrow + (size_t)c * 16) : zero;
+      if constexpr (PAIR) u[j] = ok ? load_stream16(wrow + pair_off + (size_t)c * 16) : zero;
+    }
+  };
+
+  int g = blockIdx.x * kWaves + wave;
+  load(g, wa, ua);
+
+  // RMSNorm scale, reduced by each wave over the whole vector (cpu_backend.py:71-76)
+  float inv = 1.0f;
+  if (a.pro == PRO_NORM) {
+    float ss = 0.0f;
+    for (int c = lane; c < CH; c += 64) {
+      const u32x4 v = load16(x + c * 8);
+      const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = bf_lo(words[q]), hi = bf_hi(words[q]);
+        ss += lo * lo;
+        ss += hi * hi;
+      }
+    }
+    ss = group_sum<64>(ss);
+    inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+  }
+  // this lane's x chunks (normalised when asked), kept for every row group
+  float xv[NJ][8];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = l + j * LPR;
+    if (c < CH) {
+      const u32x4 v = load16(x + c * 8);
+      const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+      if (a.pro == PRO_NORM) {
+        const u32x4 gm = load16(a.gamma + c * 8);
+        const uint32_t gw[4] = {gm.x, gm.y, gm.z, gm.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xv[j][2 * q] = round_bf16((bf_lo(words[q]) * inv) * bf_lo(gw[q]));
+          xv[j][2 * q + 1] = round_bf16((bf_hi(words[q]) * inv) * bf_hi(gw[q]));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xv[j][2 * q] = bf_lo(words[q]);
+          xv[j][2 * q + 1] = bf_hi(words[q]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xv[j][q] = 0.0f;
+    }
+  }
+
+  auto dot = [&](const u32x4 (&w)[NJ], const u32x4 (&u)[PAIR ? NJ : 1], float& a0, float& a1,
+                 float& b0, float& b1) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t ww[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a0 = fmaf(bf_lo(ww[q]), xv[j][2 * q], a0);
+        a1 = fmaf(bf_hi(ww[q]), xv[j][2 * q + 1], a1);
+      }
+      if constexpr (PAIR) {
+        const uint32_t uu[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          b0 = fmaf(bf_lo(uu[q]), xv[j][2 * q], b0);
+          b1 = fmaf(bf_hi(uu[q]), xv[j][2 * q + 1], b1);
+        }
+      }
+    }
+  };
+
+  unsigned long long best = 0ull;
+  for (;;) {
+    if (g >= groups) break;
+    const int gn = g + stride;
+    if (gn < groups) load(gn, wb, ub);
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+    dot(wa, ua, a0, a1, b0, b1);
+    finish_row<LPR, false, PAIR>(a, g * RPW + sub, g * RPW + sub < a.M, l, a0, a1, b0, b1, best);
+    g = gn;
+    if (g >= groups) break;
+    const int gn2 = g + stride;
+    if (gn2 < groups) load(gn2, wa, ua);
+    a0 = a1 = b0 = b1 = 0.f;
+    dot(wb, ub, a0, a1, b0, b1);
+    finish_row<LPR, false, PAIR>(a, g * RPW + sub, g * RPW + sub < a.M, l, a0, a1, b0, b1, best);
+    g = gn2;
+  }
+
+  if (a.epi == EPI_F32_ARGMAX) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) best = umax64(best, shfl_xor_u64(best, m));
+    if (lane == 0) wave_keys[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long k = wave_keys[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; ++i) k = umax64(k, wave_keys[i]);
+      a.keys[blockIdx.x] = k;
+    }
+  }
+}
+
 int g_cu_count = 0;
 
 int cu_count() {
@@ -315,9 +468,88 @@ int launch_shape(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
   }
 }
 
+// Register-x plan: 32 or 64 lanes per row (whichever pads the row's chunks
+// less; 32 for short paired rows), at most kXregMaxNJ chunks per lane (8 when
+// paired), and only when every wave owns at most one row group.  Returns
+// false when the LDS-staged kernel should run instead.
+constexpr int kXregMaxNJ = 12;
+
+struct XregPlan {
+  int lpr = 0;
+  int nj = 0;
+};
+
+bool xreg_plan(const GemvArgs& a, bool w8, XregPlan* plan) {
+  if (w8) return false;
+  // x and gamma are read in 16-byte chunks here (the LDS form reads 4 bytes)
+  const uintptr_t align = reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.gamma) |
+                          reinterpret_cast<uintptr_t>(a.x_table);
+  if (align & 15) return false;
+  const bool pair = a.epi == EPI_SWIGLU;
+  const int CH = a.K / 8;
+  const int nj64 = (CH + 63) / 64, nj32 = (CH + 31) / 32;
+  const int max_nj = pair ? 8 : kXregMaxNJ;
+  int lpr;
+  if (nj32 * 32 < nj64 * 64 || (pair && nj32 * 32 == nj64 * 64 && CH <= 128))
+    lpr = nj32 <= max_nj ? 32 : 64;
+  else
+    lpr = 64;
+  const int nj = lpr == 32 ? nj32 : nj64;
+  if (nj > max_nj) return false;
+  const int rpw = 64 / lpr;
+  const int groups = (a.M + rpw - 1) / rpw;
+  int cap = cu_count() * 4;
+  if (cap > kMaxPartialKeys) cap = kMaxPartialKeys;
+  if ((groups + kWaves - 1) / kWaves > cap) return false;
+  plan->lpr = lpr;
+  plan->nj = nj;
+  return true;
+}
+
+template <int LPR, int NJ, bool PAIR>
+int launch_xreg_cfg(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  constexpr int RPW = 64 / LPR;
+  const int blocks = blocks_for((a.M + RPW - 1) / RPW);
+  if (blocks_out) *blocks_out = blocks;
+  hipLaunchKernelGGL((gemv_xreg_kernel<LPR, NJ, PAIR>), dim3(blocks), dim3(kThreads), 0, stream, a);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "gemv launch");
+}
+
+template <int LPR, bool PAIR>
+int launch_xreg_nj(int nj, const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  switch (nj) {
+    case 1: return launch_xreg_cfg<LPR, 1, PAIR>(a, stream, blocks_out);
+    case 2: return launch_xreg_cfg<LPR, 2, PAIR>(a, stream, blocks_out);
+    case 3: return launch_xreg_cfg<LPR, 3, PAIR>(a, stream, blocks_out);
+    case 4: return launch_xreg_cfg<LPR, 4, PAIR>(a, stream, blocks_out);
+    case 5: return launch_xreg_cfg<LPR, 5, PAIR>(a, stream, blocks_out);
+    case 6: return launch_xreg_cfg<LPR, 6, PAIR>(a, stream, blocks_out);
+    case 7:
+    case 8: return launch_xreg_cfg<LPR, 8, PAIR>(a, stream, blocks_out);
+    default:
+      if constexpr (!PAIR) {
+        if (nj <= 10) return launch_xreg_cfg<LPR, 10, PAIR>(a, stream, blocks_out);
+        return launch_xreg_cfg<LPR, 12, PAIR>(a, stream, blocks_out);
+      }
+      return fail("gemv: no register-x configuration for this row length");
+  }
+}
+
+template <bool PAIR>
+int launch_xreg(const XregPlan& p, const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  if (p.lpr == 32) return launch_xreg_nj<32, PAIR>(p.nj, a, stream, blocks_out);
+  return launch_xreg_nj<64, PAIR>(p.nj, a, stream, blocks_out);
+}
+
 }  // namespace
 
 int gemv_blocks(const GemvArgs& a, bool w8) {
+  XregPlan plan;
+  if (xreg_plan(a, w8, &plan)) {
+    const int rpw = 64 / plan.lpr;
+    return blocks_for((a.M + rpw - 1) / rpw);
+  }
   const int CH = w8 ? a.K / 16 : a.K / 8;
   const int rpw = 64 / pick_lpr(CH);
   return blocks_for((a.M + rpw - 1) / rpw);
@@ -339,6 +571,10 @@ int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out)
   if (a.epi == EPI_BIAS && a.bias == nullptr) return fail("gemv: bias missing");
   if (a.epi == EPI_RESID && a.resid == nullptr) return fail("gemv: residual missing");
   if (a.epi == EPI_F32_ARGMAX && a.keys == nullptr) return fail("gemv: argmax key buffer missing");
+  XregPlan plan;
+  if (xreg_plan(a, w8, &plan))
+    return pair ? launch_xreg<true>(plan, a, stream, blocks_out)
+                : launch_xreg<false>(plan, a, stream, blocks_out);
   if (w8)
     return pair ? launch_shape<true, true>(a, stream, blocks_out)
                 : launch_shape<true, false>(a, stream, blocks_out);

@@ -94,6 +94,8 @@ _SIGNATURES = {
     "hk_engine_final_hidden": (ctypes.c_int, [_vp, _vp]),
     "hk_engine_read_kv": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp]),
     "hk_engine_launch_part": (ctypes.c_int, [_vp, _i32, _i32]),
+    "hk_engine_launch_part_repeat": (ctypes.c_int, [_vp, _i32, _i32]),
+    "hk_gemv_repeat": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "hk_engine_reset": (ctypes.c_int, [_vp]),
     "hk_engine_stream": (_vp, [_vp]),
     "hk_engine_destroy": (None, [_vp]),

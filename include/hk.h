@@ -149,6 +149,19 @@ int hk_engine_read_kv(hk_engine* engine, int32_t layer, int32_t slot, uint16_t* 
  * one opaque dispatch (designs/qwen_engine.py:72-341). */
 int hk_engine_launch_part(hk_engine* engine, int32_t part, int32_t layer);
 
+/* Enqueue `count` launches of one part, layer i % layers for launch i, as one
+ * hipGraph (captured on first use per (part, count)), so host launch cost does
+ * not pace the GPU when the launches are timed with events. */
+int hk_engine_launch_part_repeat(hk_engine* engine, int32_t part, int32_t count);
+
+/* Enqueue `count` GEMVs y = W_i @ x, W_i = weights[i % n_weights] (bf16, or
+ * int8 with scales[i % n_weights] when `scales` is non-NULL), float32 output,
+ * on `stream` -- a microbenchmark that rotates through distinct weight copies
+ * so a cache cannot serve them. */
+int hk_gemv_repeat(const void* const* weights, const float* const* scales, int32_t n_weights,
+                   const uint16_t* x, float* y_f32, int32_t M, int32_t K, int32_t count,
+                   void* stream);
+
 /* Zero the KV cache (QwenDecoderEngine.reset, qwen_engine.py:65-66). */
 int hk_engine_reset(hk_engine* engine);
 
