@@ -9,14 +9,16 @@
 //   scores   (q . k) * head_dim**-0.5, minus the row max, exp, / sum   :110-125
 //   output   bf16(P @ V)                                          :126-129
 //
-// Work split: one workgroup per (KV head, chunk of 256 slots), so positions
-// below 256 use one workgroup per KV head and no merge.  With a single chunk
-// the workgroup normalises P = p / sum first and then forms P @ V, as NumPy
-// does.  With
-// several chunks each workgroup publishes (max, sum, p @ V) for its chunk and
-// the last one to finish (a per-head ticket) merges them with log-sum-exp
-// rescaling.  The KV cache layout is [kv head][slot][64] BF16 per layer, so
-// one slot of one head is a contiguous 128-byte row.
+// Work split: one workgroup per (query head, chunk of 256 slots), so
+// positions below 256 use one workgroup per query head and no merge; the K/V
+// rows of a KV head are shared by its query heads through L2.  Thread t of a
+// chunk scores slot t; the P @ V sum is split over 8 slot groups of 32 lanes
+// (one dimension pair per lane) and the groups are added in LDS.  With a single
+// chunk the workgroup normalises P = p / sum first and then forms P @ V, as
+// NumPy does.  With several chunks each workgroup publishes (max, sum, p @ V)
+// for its chunk and the last one to finish (a per-head ticket) merges them
+// with log-sum-exp rescaling.  The KV cache layout is [kv head][slot][64] BF16
+// per layer, so one slot of one head is a contiguous 128-byte row.
 #include "hk_common.h"
 #include "hk_internal.h"
 
@@ -27,24 +29,16 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kPartStride = kHeadDim + 2;  // acc[64], max, sum
+constexpr int kGroups = kThreads / kHalf;  // slot groups of the P @ V loop
+static_assert(kThreads == kAttnChunk, "one thread per slot of a chunk");
+static_assert(kHeadDim == 64, "the merge runs on wave 0 alone");
 
-__device__ __forceinline__ void unpack_row(const uint16_t* src, float (&dst)[kHeadDim]) {
-#pragma unroll
-  for (int c = 0; c < kHeadDim / 8; ++c) {
-    const u32x4 w = load16(src + c * 8);
-    dst[c * 8 + 0] = bf_lo(w.x);
-    dst[c * 8 + 1] = bf_hi(w.x);
-    dst[c * 8 + 2] = bf_lo(w.y);
-    dst[c * 8 + 3] = bf_hi(w.y);
-    dst[c * 8 + 4] = bf_lo(w.z);
-    dst[c * 8 + 5] = bf_hi(w.z);
-    dst[c * 8 + 6] = bf_lo(w.w);
-    dst[c * 8 + 7] = bf_hi(w.w);
-  }
-}
-
+// One workgroup per (query head, chunk of 256 slots).  Every load whose
+// address does not depend on a reduction (the K row of the thread's slot, the
+// V words of its slot group, q, the new k/v) is issued before the first
+// barrier, so a launch costs about one memory latency plus the reductions.
 __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) {
-  const int g = blockIdx.x;
+  const int h = blockIdx.x;
   const int s = blockIdx.y;
   const int p = *a.position;
   const int t0 = s * kAttnChunk;
@@ -54,160 +48,157 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
   const int nsplit = p / kAttnChunk + 1;
   const bool holds_new = (s == nsplit - 1);
   const int qpk = a.q_heads / a.kv_heads;
+  const int g = h / qpk;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
 
-  __shared__ float qs[kMaxQPerKV][kHeadDim];
+  __shared__ float qs[kHeadDim];
   __shared__ float knew[kHeadDim];
-  __shared__ float sc[kMaxQPerKV][kAttnChunk];
-  __shared__ float hmax[kMaxQPerKV];
-  __shared__ float hsum[kMaxQPerKV];
-  __shared__ uint32_t vs[kAttnChunk][kHalf];  // V rows of the chunk, bf16 pairs
-  __shared__ unsigned int ticket_s;
+  __shared__ float pr[kAttnChunk];
+  __shared__ float red[2][kWaves];
+  __shared__ float acc[kGroups][kHeadDim];
 
-  const float* ct = a.cos_tab + (size_t)p * kHalf;
-  const float* st = a.sin_tab + (size_t)p * kHalf;
   const size_t head_base = (size_t)g * a.max_ctx;
+  const uint16_t* vnew = a.qkv + (size_t)(a.q_heads + a.kv_heads + g) * kHeadDim;
 
-  // Rotated query heads of this group, rounded to bf16 as the reference does.
-  for (int i = tid; i < qpk * kHalf; i += kThreads) {
-    const int h = i / kHalf, j = i % kHalf;
-    const uint16_t* q = a.qkv + (size_t)(g * qpk + h) * kHeadDim;
-    const float x1 = bf16_to_f32(q[j]), x2 = bf16_to_f32(q[j + kHalf]);
-    const float c = ct[j], sn = st[j];
-    qs[h][j] = round_bf16(x1 * c - x2 * sn);
-    qs[h][j + kHalf] = round_bf16(x2 * c + x1 * sn);
+  // K row of this thread's slot (slot p comes from the rotated new key below)
+  const int slot = t0 + tid;
+  const bool has_slot = tid < n && slot != p;
+  u32x4 krow[kHeadDim / 8];
+  {
+    const uint16_t* src = a.kcache + (head_base + (has_slot ? slot : 0)) * kHeadDim;
+#pragma unroll
+    for (int c = 0; c < kHeadDim / 8; ++c) krow[c] = has_slot ? load16(src + c * 8) : u32x4{0u, 0u, 0u, 0u};
   }
-  // The new key (rotated) and value of this KV head, appended at slot p by
-  // the workgroup whose chunk holds p.
-  if (holds_new && tid < kHalf) {
-    const uint16_t* k = a.qkv + (size_t)(a.q_heads + g) * kHeadDim;
-    const uint16_t* v = a.qkv + (size_t)(a.q_heads + a.kv_heads + g) * kHeadDim;
-    const float x1 = bf16_to_f32(k[tid]), x2 = bf16_to_f32(k[tid + kHalf]);
-    const float c = ct[tid], sn = st[tid];
+  // V words for the P @ V loop: thread (group gi, dimension pair dp) takes
+  // slots gi, gi + kGroups, ... of the chunk.
+  const int dp = tid & (kHalf - 1);
+  const int gi = tid / kHalf;
+  uint32_t vw[kAttnChunk / kGroups];
+#pragma unroll
+  for (int k = 0; k < kAttnChunk / kGroups; ++k) {
+    const int t = gi + k * kGroups;
+    const int sl = t0 + t;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(
+        sl == p ? vnew : a.vcache + (head_base + (sl < p ? sl : 0)) * kHeadDim);
+    vw[k] = t < n ? src[dp] : 0u;
+  }
+
+  // Rotated query head and new key (bf16-rounded as the reference does);
+  // the first query head of the group appends k and v at slot p.
+  if (tid < 2 * kHalf) {
+    const int j = tid & (kHalf - 1);
+    const bool is_k = tid >= kHalf;
+    const uint16_t* src = is_k ? a.qkv + (size_t)(a.q_heads + g) * kHeadDim
+                               : a.qkv + (size_t)h * kHeadDim;
+    const float c = a.cos_tab[(size_t)p * kHalf + j];
+    const float sn = a.sin_tab[(size_t)p * kHalf + j];
+    const float x1 = bf16_to_f32(src[j]), x2 = bf16_to_f32(src[j + kHalf]);
     const uint32_t r1 = f32_to_bf16(x1 * c - x2 * sn);
     const uint32_t r2 = f32_to_bf16(x2 * c + x1 * sn);
-    knew[tid] = bf16_to_f32(r1);
-    knew[tid + kHalf] = bf16_to_f32(r2);
-    uint16_t* kd = a.kcache + (head_base + p) * kHeadDim;
-    uint16_t* vd = a.vcache + (head_base + p) * kHeadDim;
-    kd[tid] = (uint16_t)r1;
-    kd[tid + kHalf] = (uint16_t)r2;
-    vd[tid] = v[tid];
-    vd[tid + kHalf] = v[tid + kHalf];
-  }
-  // Stage the chunk's cached V rows (16-byte loads); slot p comes from qkv.
-  for (int i = tid; i < n * (kHeadDim / 8); i += kThreads) {
-    const int t = i / (kHeadDim / 8), c = i % (kHeadDim / 8);
-    const int slot = t0 + t;
-    const uint16_t* src = (slot == p)
-                              ? a.qkv + (size_t)(a.q_heads + a.kv_heads + g) * kHeadDim + c * 8
-                              : a.vcache + (head_base + slot) * kHeadDim + c * 8;
-    const u32x4 w = load16(src);
-    vs[t][c * 4 + 0] = w.x;
-    vs[t][c * 4 + 1] = w.y;
-    vs[t][c * 4 + 2] = w.z;
-    vs[t][c * 4 + 3] = w.w;
+    float* dst = is_k ? knew : qs;
+    dst[j] = bf16_to_f32(r1);
+    dst[j + kHalf] = bf16_to_f32(r2);
+    if (is_k && holds_new && h % qpk == 0) {
+      uint16_t* kd = a.kcache + (head_base + p) * kHeadDim;
+      uint16_t* vd = a.vcache + (head_base + p) * kHeadDim;
+      kd[j] = (uint16_t)r1;
+      kd[j + kHalf] = (uint16_t)r2;
+      vd[j] = vnew[j];
+      vd[j + kHalf] = vnew[j + kHalf];
+    }
   }
   __syncthreads();
 
-  // Scores: one (slot, head) pair per thread.
+  // score of this thread's slot
   const float scale = 1.0f / 8.0f;  // head_dim ** -0.5 for head_dim 64 (exact)
-  for (int i = tid; i < n * qpk; i += kThreads) {
-    const int t = i / qpk, h = i % qpk;
-    const int slot = t0 + t;
-    float kv[kHeadDim];
+  float sc = -INFINITY;
+  if (tid < n) {
+    float dot = 0.0f;
     if (slot == p) {
 #pragma unroll
-      for (int d = 0; d < kHeadDim; ++d) kv[d] = knew[d];
+      for (int d = 0; d < kHeadDim; ++d) dot = fmaf(qs[d], knew[d], dot);
     } else {
-      unpack_row(a.kcache + (head_base + slot) * kHeadDim, kv);
-    }
-    float dot = 0.0f;
 #pragma unroll
-    for (int d = 0; d < kHeadDim; ++d) dot = fmaf(qs[h][d], kv[d], dot);
-    sc[h][t] = dot * scale;
+      for (int c = 0; c < kHeadDim / 8; ++c) {
+        const uint32_t w[4] = {krow[c].x, krow[c].y, krow[c].z, krow[c].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          dot = fmaf(qs[c * 8 + 2 * q], bf_lo(w[q]), dot);
+          dot = fmaf(qs[c * 8 + 2 * q + 1], bf_hi(w[q]), dot);
+        }
+      }
+    }
+    sc = dot * scale;
   }
+  // chunk max and exp-sum
+  float m = group_max<64>(sc);
+  if (lane == 0) red[0][wave] = m;
+  __syncthreads();
+  m = red[0][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[0][w]);
+  const float e = tid < n ? expf(sc - m) : 0.0f;
+  float sum = group_sum<64>(e);
+  if (lane == 0) red[1][wave] = sum;
+  __syncthreads();
+  sum = red[1][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) sum += red[1][w];
+  // a single chunk normalises first (P = e / sum), as the reference does
+  if (tid < kAttnChunk) pr[tid] = nsplit == 1 ? e / sum : e;
   __syncthreads();
 
-  // Per-head max and exp-sum over this chunk (one wave per head).
-  for (int h = wave; h < qpk; h += kWaves) {
-    float m = -INFINITY;
-    for (int t = lane; t < n; t += 64) m = fmaxf(m, sc[h][t]);
-    m = group_max<64>(m);
-    float sum = 0.0f;
-    for (int t = lane; t < n; t += 64) {
-      const float e = expf(sc[h][t] - m);
-      sc[h][t] = e;
-      sum += e;
-    }
-    sum = group_sum<64>(sum);
-    if (lane == 0) {
-      hmax[h] = m;
-      hsum[h] = sum;
+  float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kAttnChunk / kGroups; ++k) {
+    const int t = gi + k * kGroups;
+    if (t < n) {
+      const float pt = pr[t];
+      o0 = fmaf(pt, bf_lo(vw[k]), o0);
+      o1 = fmaf(pt, bf_hi(vw[k]), o1);
     }
   }
+  acc[gi][2 * dp] = o0;
+  acc[gi][2 * dp + 1] = o1;
   __syncthreads();
-
+  if (tid >= kHeadDim) return;
+  float o = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kGroups; ++k) o += acc[k][tid];
   if (nsplit == 1) {
-    for (int i = tid; i < qpk * n; i += kThreads) {
-      const int h = i / n, t = i % n;
-      sc[h][t] = sc[h][t] / hsum[h];
-    }
-    __syncthreads();
+    a.out[(size_t)h * kHeadDim + tid] = (uint16_t)f32_to_bf16(o);
+    return;
   }
 
-  // Weighted sum of values from the LDS copy of this chunk's V rows:
-  // thread = (head, pair of dimensions), loop over the slots.
-  float* mine = a.partial + ((size_t)g * a.max_splits + s) * kMaxQPerKV * kPartStride;
-  for (int i = tid; i < qpk * kHalf; i += kThreads) {
-    const int h = i / kHalf, dp = i % kHalf;
-    float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll 8
-    for (int t = 0; t < n; ++t) {
-      const uint32_t v2 = vs[t][dp];
-      const float pt = sc[h][t];
-      o0 = fmaf(pt, bf_lo(v2), o0);
-      o1 = fmaf(pt, bf_hi(v2), o1);
-    }
-    if (nsplit == 1) {
-      const uint32_t packed = f32_to_bf16(o0) | (f32_to_bf16(o1) << 16);
-      reinterpret_cast<uint32_t*>(a.out + (size_t)(g * qpk + h) * kHeadDim)[dp] = packed;
-    } else {
-      mine[h * kPartStride + 2 * dp] = o0;
-      mine[h * kPartStride + 2 * dp + 1] = o1;
-    }
-  }
-  if (nsplit == 1) return;
-
-  // Split-KV: publish this chunk's max and sum, the last workgroup merges.
-  if (tid < qpk) {
-    mine[tid * kPartStride + kHeadDim] = hmax[tid];
-    mine[tid * kPartStride + kHeadDim + 1] = hsum[tid];
+  // Split-KV: publish (p @ V, max, sum) of this chunk; the last workgroup of
+  // this head (ticket) merges all chunks with log-sum-exp rescaling.
+  float* mine = a.partial + ((size_t)h * a.max_splits + s) * kPartStride;
+  mine[tid] = o;
+  if (tid == 0) {
+    mine[kHeadDim] = m;
+    mine[kHeadDim + 1] = sum;
   }
   __threadfence();
-  __syncthreads();
-  if (tid == 0) ticket_s = atomicAdd(&a.counters[g], 1u);
-  __syncthreads();
-  if (ticket_s != (unsigned int)(nsplit - 1)) return;
+  // only wave 0 (tid < 64) is left here, so a shuffle broadcasts the ticket
+  unsigned int ticket = 0;
+  if (tid == 0) ticket = atomicAdd(&a.counters[h], 1u);
+  ticket = __shfl(ticket, 0, 64);
+  if (ticket != (unsigned int)(nsplit - 1)) return;
   __threadfence();
-  const float* base = a.partial + (size_t)g * a.max_splits * kMaxQPerKV * kPartStride;
-  for (int i = tid; i < qpk * kHeadDim; i += kThreads) {
-    const int h = i / kHeadDim, d = i % kHeadDim;
-    float m = -INFINITY;
-    for (int j = 0; j < nsplit; ++j)
-      m = fmaxf(m, base[(size_t)j * kMaxQPerKV * kPartStride + h * kPartStride + kHeadDim]);
-    float l = 0.0f, o = 0.0f;
-    for (int j = 0; j < nsplit; ++j) {
-      const float* pj = base + (size_t)j * kMaxQPerKV * kPartStride + h * kPartStride;
-      const float f = expf(pj[kHeadDim] - m);
-      l = fmaf(pj[kHeadDim + 1], f, l);
-      o = fmaf(pj[d], f, o);
-    }
-    a.out[(size_t)(g * qpk + h) * kHeadDim + d] = (uint16_t)f32_to_bf16(o / l);
+  const float* base = a.partial + (size_t)h * a.max_splits * kPartStride;
+  float mx = -INFINITY;
+  for (int j = 0; j < nsplit; ++j) mx = fmaxf(mx, base[(size_t)j * kPartStride + kHeadDim]);
+  float l = 0.0f, out = 0.0f;
+  for (int j = 0; j < nsplit; ++j) {
+    const float* pj = base + (size_t)j * kPartStride;
+    const float f = expf(pj[kHeadDim] - mx);
+    l = fmaf(pj[kHeadDim + 1], f, l);
+    out = fmaf(pj[tid], f, out);
   }
-  if (tid == 0) atomicExch(&a.counters[g], 0u);
+  a.out[(size_t)h * kHeadDim + tid] = (uint16_t)f32_to_bf16(out / l);
+  if (tid == 0) atomicExch(&a.counters[h], 0u);
 }
 
 }  // namespace
@@ -218,7 +209,7 @@ int launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
   if (a.q_heads / a.kv_heads > kMaxQPerKV) return fail("attention: more than 16 q heads per kv head");
   if (a.max_ctx <= 0 || a.max_ctx > kMaxContext) return fail("attention: context out of range");
   if (a.max_splits < attention_splits(a.max_ctx)) return fail("attention: too few split-KV slots");
-  hipLaunchKernelGGL(attention_decode_kernel, dim3(a.kv_heads, a.max_splits), dim3(kThreads), 0,
+  hipLaunchKernelGGL(attention_decode_kernel, dim3(a.q_heads, a.max_splits), dim3(kThreads), 0,
                      stream, a);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "attention launch");

@@ -530,8 +530,8 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     const size_t kv = (size_t)d.layers * kv_layer_elems(e);
     HK_TRY(dalloc(&e->kcache, kv));
     HK_TRY(dalloc(&e->vcache, kv));
-    HK_TRY(dalloc(&e->partial, (size_t)d.kv_heads * e->max_splits * kMaxQPerKV * (kHeadDim + 2)));
-    HK_TRY(dalloc(&e->counters, d.kv_heads));
+    HK_TRY(dalloc(&e->partial, (size_t)d.q_heads * e->max_splits * (kHeadDim + 2)));
+    HK_TRY(dalloc(&e->counters, d.q_heads));
     HK_TRY(dalloc(&e->keys, kMaxPartialKeys));
     HK_TRY(dalloc(&e->ctrl, 1));
     HK_TRY(dalloc(&e->out_tokens, d.max_context));
@@ -539,7 +539,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     HK_CHECK(hipMemset(e->kcache, 0, kv * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->vcache, 0, kv * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->h, 0, d.hidden * sizeof(uint16_t)));
-    HK_CHECK(hipMemset(e->counters, 0, d.kv_heads * sizeof(unsigned int)));
+    HK_CHECK(hipMemset(e->counters, 0, d.q_heads * sizeof(unsigned int)));
     HK_CHECK(hipMemset(e->ctrl, 0, sizeof(StepCtrl)));
     HK_CHECK(hipDeviceSynchronize());
     return 0;
@@ -820,7 +820,7 @@ int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float*
   if (max_context > kMaxContext) return fail("hk_attention_decode: context above 65536 slots");
   const int splits = attention_splits(max_context);
   OpScratch* s = nullptr;
-  HK_TRY(op_scratch(&s, (size_t)kv_heads * splits * kMaxQPerKV * (kHeadDim + 2), kv_heads));
+  HK_TRY(op_scratch(&s, (size_t)q_heads * splits * (kHeadDim + 2), q_heads));
   hipLaunchKernelGGL(store_i32_kernel, dim3(1), dim3(1), 0, st, s->position, position);
   HK_CHECK(hipGetLastError());
   AttnArgs a = {};

@@ -82,8 +82,8 @@ struct AttnArgs {
   uint16_t* vcache;          // this layer: [Hkv, max_ctx, 64] bf16
   const int32_t* position;   // device scalar
   uint16_t* out;             // [Hq * 64] bf16
-  float* partial;            // [Hkv, max_splits, 16, 66] split-KV partials (contexts > 256)
-  unsigned int* counters;    // [Hkv] zero between launches
+  float* partial;            // [Hq, max_splits, 66] split-KV partials (contexts > 256)
+  unsigned int* counters;    // [Hq] zero between launches
   int q_heads, kv_heads, max_ctx, max_splits;
 };
 
