@@ -153,7 +153,11 @@ struct hk_engine {
   unsigned long long* keys = nullptr;  // [kMaxPartialKeys] LM-head argmax partials
   StepCtrl* ctrl = nullptr;
   int32_t* out_tokens = nullptr;  // [max_ctx]
-  int32_t* result = nullptr;
+  int32_t* result = nullptr;      // [2]: last argmax token, persistent-step error word
+  // whole step in one persistent launch (persistent.hip); -1: per-kernel graph
+  int pshape = -1;
+  PersistentLayer* players = nullptr;  // device copy of the layer pointers
+  unsigned int* psync = nullptr;       // progress and attention-head epochs
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   std::map<long long, hipGraphExec_t> repeat_graphs;  // timing graphs by (part, count)
   bool use_graph = true;
@@ -281,6 +285,60 @@ int launch_part(hk_engine* e, int part, int l) {
   }
 }
 
+int launch_persistent(hk_engine* e, bool head) {
+  const hk_model_desc& d = e->d;
+  PersistentArgs a = {};
+  a.w = e->players;
+  a.layers = d.layers;
+  a.vocab = d.vocab;
+  a.max_ctx = d.max_context;
+  a.max_splits = e->max_splits;
+  a.head = head ? 1 : 0;
+  a.eps = d.rms_eps;
+  a.embed = e->w.token_embedding;
+  a.lm_head = e->w.lm_head;
+  a.final_norm = e->w.final_norm;
+  a.cos_tab = e->w.rope_cos;
+  a.sin_tab = e->w.rope_sin;
+  a.kcache = e->kcache;
+  a.vcache = e->vcache;
+  a.h = e->h;
+  a.h1 = e->h1;
+  a.qkv = e->qkv;
+  a.attn = e->attn;
+  a.act = e->act;
+  a.logits = e->logits;
+  a.keys = e->keys;
+  a.partial = e->partial;
+  a.counters = e->counters;
+  a.ctrl = e->ctrl;
+  a.out_tokens = e->out_tokens;
+  a.result = e->result;
+  a.progress = e->psync;
+  a.headflag = e->psync + (size_t)kPersistentGrid * kFlagStride;
+  a.error = reinterpret_cast<unsigned int*>(e->result + 1);
+  return launch_persistent_step(e->pshape, a, e->stream);
+}
+
+size_t psync_words(const hk_engine* e) {
+  return (size_t)(kPersistentGrid + e->d.q_heads) * kFlagStride;
+}
+
+// After a synchronised copy of `result` (token, error word): an error means a
+// persistent launch was abandoned; clear its flags so the next step starts
+// clean, and report it.
+int check_persistent(hk_engine* e, const int32_t* result_host) {
+  if (e->pshape < 0 || result_host[1] == 0) return 0;
+  HK_CHECK(hipStreamSynchronize(e->stream));
+  HK_CHECK(hipMemset(e->psync, 0, psync_words(e) * sizeof(unsigned int)));
+  HK_CHECK(hipMemset(e->counters, 0, e->d.q_heads * sizeof(unsigned int)));
+  HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
+  HK_CHECK(hipDeviceSynchronize());
+  set_error("decode step abandoned: a workgroup of the persistent step waited too long for "
+            "another (is another kernel occupying the GPU?); its outputs and KV slot are invalid");
+  return HK_ERR_HIP;
+}
+
 int enqueue_step(hk_engine* e, bool head) {
   for (int l = 0; l < e->d.layers; ++l)
     for (int part = HK_PART_QKV; part <= HK_PART_DOWN; ++part) HK_TRY(launch_part(e, part, l));
@@ -289,6 +347,7 @@ int enqueue_step(hk_engine* e, bool head) {
 }
 
 int run_step(hk_engine* e, bool head) {
+  if (e->pshape >= 0) return launch_persistent(e, head);
   if (!e->use_graph) return enqueue_step(e, head);
   hipGraphExec_t& exec = e->graph[head ? 1 : 0];
   if (exec == nullptr) {
@@ -337,7 +396,7 @@ void free_engine(hk_engine* e) {
                   e->normed,  e->logits,   e->kcache,   e->vcache,     e->partial,
                   e->counters, e->keys,    e->ctrl,     e->out_tokens, e->result,
                   e->pf_x,    e->pf_h1,    e->pf_xn,    e->pf_qkv,     e->pf_q,
-                  e->pf_att,  e->pf_act,   e->pf_tokens};
+                  e->pf_att,  e->pf_act,   e->pf_tokens, e->players, e->psync};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -535,12 +594,30 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     HK_TRY(dalloc(&e->keys, kMaxPartialKeys));
     HK_TRY(dalloc(&e->ctrl, 1));
     HK_TRY(dalloc(&e->out_tokens, d.max_context));
-    HK_TRY(dalloc(&e->result, 1));
+    HK_TRY(dalloc(&e->result, 2));
     HK_CHECK(hipMemset(e->kcache, 0, kv * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->vcache, 0, kv * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->h, 0, d.hidden * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->counters, 0, d.q_heads * sizeof(unsigned int)));
     HK_CHECK(hipMemset(e->ctrl, 0, sizeof(StepCtrl)));
+    HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
+    const char* pers = getenv("HK_PERSISTENT");
+    if (!(pers && pers[0] == '0'))
+      e->pshape = persistent_shape(d.hidden, d.intermediate, d.q_heads, d.kv_heads, w8);
+    if (e->pshape >= 0) {
+      std::vector<PersistentLayer> pl(d.layers);
+      for (int l = 0; l < d.layers; ++l) {
+        const hk_layer_weights& lw = e->layers[l];
+        pl[l] = {static_cast<const uint16_t*>(lw.qkv),     lw.qkv_bias,
+                 static_cast<const uint16_t*>(lw.o_proj),  static_cast<const uint16_t*>(lw.gate_up),
+                 static_cast<const uint16_t*>(lw.down_proj), lw.input_norm, lw.post_attn_norm};
+      }
+      HK_TRY(dalloc(&e->players, d.layers));
+      HK_CHECK(hipMemcpy(e->players, pl.data(), d.layers * sizeof(PersistentLayer),
+                         hipMemcpyHostToDevice));
+      HK_TRY(dalloc(&e->psync, psync_words(e)));
+      HK_CHECK(hipMemset(e->psync, 0, psync_words(e) * sizeof(unsigned int)));
+    }
     HK_CHECK(hipDeviceSynchronize());
     return 0;
   };
@@ -575,10 +652,13 @@ int hk_engine_step(hk_engine* e, int32_t token, int32_t position, int32_t want_l
   if (logits_host)
     HK_CHECK(hipMemcpyAsync(logits_host, e->logits, (size_t)e->d.vocab * sizeof(float),
                             hipMemcpyDeviceToHost, e->stream));
-  if (next_token_host)
-    HK_CHECK(hipMemcpyAsync(next_token_host, e->result, sizeof(int32_t), hipMemcpyDeviceToHost,
-                            e->stream));
-  if (embedding_host || logits_host || next_token_host) HK_CHECK(hipStreamSynchronize(e->stream));
+  if (embedding_host || logits_host || next_token_host) {
+    int32_t result[2] = {0, 0};
+    HK_CHECK(hipMemcpyAsync(result, e->result, sizeof(result), hipMemcpyDeviceToHost, e->stream));
+    HK_CHECK(hipStreamSynchronize(e->stream));
+    HK_TRY(check_persistent(e, result));
+    if (next_token_host) *next_token_host = result[0];
+  }
   return 0;
 }
 
@@ -593,10 +673,12 @@ int hk_engine_generate(hk_engine* e, int32_t token, int32_t position, int32_t n_
   HK_CHECK(hipSetDevice(e->device));
   HK_TRY(set_ctrl(e, token, position, 1));
   for (int i = 0; i < n_steps; ++i) HK_TRY(run_step(e, true));
+  int32_t result[2] = {0, 0};
   HK_CHECK(hipMemcpyAsync(tokens_host, e->out_tokens, (size_t)n_steps * sizeof(int32_t),
                           hipMemcpyDeviceToHost, e->stream));
+  HK_CHECK(hipMemcpyAsync(result, e->result, sizeof(result), hipMemcpyDeviceToHost, e->stream));
   HK_CHECK(hipStreamSynchronize(e->stream));
-  return 0;
+  return check_persistent(e, result);
 }
 
 int hk_engine_prefill(hk_engine* e, const int32_t* tokens_host, int32_t n, int32_t start,

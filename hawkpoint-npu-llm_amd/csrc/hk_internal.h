@@ -97,6 +97,55 @@ inline int attention_splits(int max_ctx) { return (max_ctx + kAttnChunk - 1) / k
 
 int launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 
+// ---- whole decode step in one persistent launch (persistent.hip) ----
+constexpr int kPersistentThreads = 512;  // one workgroup per CU
+constexpr int kPersistentGrid = 256;     // workgroups (MI355X has 256 CUs)
+constexpr int kPersistentChunk = 512;    // attention slots per task
+constexpr int kFlagStride = 32;          // uint32 words between flags (one 128-byte line each)
+
+struct PersistentLayer {
+  const uint16_t* qkv;
+  const float* qkv_bias;  // null when the model has none
+  const uint16_t* o;
+  const uint16_t* gate_up;
+  const uint16_t* down;
+  const uint16_t* in_norm;
+  const uint16_t* post_norm;
+};
+
+struct PersistentArgs {
+  const PersistentLayer* w;  // device array [layers]
+  int layers, vocab, max_ctx, max_splits;
+  int head;  // 1: final norm, LM head and argmax (with token feedback when ctrl->advance)
+  float eps;
+  const uint16_t* embed;
+  const uint16_t* lm_head;
+  const uint16_t* final_norm;
+  const float* cos_tab;
+  const float* sin_tab;
+  uint16_t* kcache;  // [L][Hkv][max_ctx][64]
+  uint16_t* vcache;
+  uint16_t* h;
+  uint16_t* h1;
+  uint16_t* qkv;
+  uint16_t* attn;
+  uint16_t* act;
+  float* logits;
+  unsigned long long* keys;  // [kPersistentGrid]
+  float* partial;            // [Hq, max_splits, 66]
+  unsigned int* counters;    // [Hq], zero between launches
+  StepCtrl* ctrl;
+  int32_t* out_tokens;
+  int32_t* result;
+  unsigned int* progress;  // [kPersistentGrid * kFlagStride] epoch per workgroup
+  unsigned int* headflag;  // [Hq * kFlagStride] epoch per attention head
+  unsigned int* error;     // nonzero: a wait timed out; the launch was abandoned
+};
+
+// Model shapes the persistent step is compiled for (-1: use the per-kernel step).
+int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bool w8);
+int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream);
+
 // ---- batched prefill (prefill.hip) ----
 
 struct PrefillGemmArgs {
