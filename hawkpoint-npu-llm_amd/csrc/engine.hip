@@ -157,7 +157,8 @@ struct hk_engine {
   // whole step in one persistent launch (persistent.hip); -1: per-kernel graph
   int pshape = -1;
   PersistentLayer* players = nullptr;  // device copy of the layer pointers
-  unsigned int* psync = nullptr;       // progress and attention-head epochs
+  unsigned int* psync = nullptr;       // per-workgroup epochs
+  uint32_t* ptag = nullptr;            // tagged activations: h, h1, qkv, attn, act
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   std::map<long long, hipGraphExec_t> repeat_graphs;  // timing graphs by (part, count)
   bool use_graph = true;
@@ -303,10 +304,12 @@ int launch_persistent(hk_engine* e, bool head) {
   a.kcache = e->kcache;
   a.vcache = e->vcache;
   a.h = e->h;
-  a.h1 = e->h1;
-  a.qkv = e->qkv;
-  a.attn = e->attn;
-  a.act = e->act;
+  a.th = e->ptag;
+  a.th1 = a.th + d.hidden;
+  a.tqkv = a.th1 + d.hidden;
+  a.tattn = a.tqkv + e->qkv_rows;
+  a.tact = a.tattn + (size_t)d.q_heads * kHeadDim;
+  a.pad = a.tact + d.intermediate;
   a.logits = e->logits;
   a.keys = e->keys;
   a.partial = e->partial;
@@ -315,13 +318,16 @@ int launch_persistent(hk_engine* e, bool head) {
   a.out_tokens = e->out_tokens;
   a.result = e->result;
   a.progress = e->psync;
-  a.headflag = e->psync + (size_t)kPersistentGrid * kFlagStride;
   a.error = reinterpret_cast<unsigned int*>(e->result + 1);
   return launch_persistent_step(e->pshape, a, e->stream);
 }
 
-size_t psync_words(const hk_engine* e) {
-  return (size_t)(kPersistentGrid + e->d.q_heads) * kFlagStride;
+size_t psync_words(const hk_engine*) { return (size_t)kPersistentGrid * kFlagStride; }
+
+size_t ptag_words(const hk_engine* e) {
+  const hk_model_desc& d = e->d;
+  return 2 * (size_t)d.hidden + e->qkv_rows + (size_t)d.q_heads * kHeadDim + d.intermediate +
+         (size_t)kPersistentGrid * (kPersistentThreads / 64);
 }
 
 // After a synchronised copy of `result` (token, error word): an error means a
@@ -331,6 +337,7 @@ int check_persistent(hk_engine* e, const int32_t* result_host) {
   if (e->pshape < 0 || result_host[1] == 0) return 0;
   HK_CHECK(hipStreamSynchronize(e->stream));
   HK_CHECK(hipMemset(e->psync, 0, psync_words(e) * sizeof(unsigned int)));
+  HK_CHECK(hipMemset(e->ptag, 0, ptag_words(e) * sizeof(uint32_t)));
   HK_CHECK(hipMemset(e->counters, 0, e->d.q_heads * sizeof(unsigned int)));
   HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
   HK_CHECK(hipDeviceSynchronize());
@@ -396,7 +403,7 @@ void free_engine(hk_engine* e) {
                   e->normed,  e->logits,   e->kcache,   e->vcache,     e->partial,
                   e->counters, e->keys,    e->ctrl,     e->out_tokens, e->result,
                   e->pf_x,    e->pf_h1,    e->pf_xn,    e->pf_qkv,     e->pf_q,
-                  e->pf_att,  e->pf_act,   e->pf_tokens, e->players, e->psync};
+                  e->pf_att,  e->pf_act,   e->pf_tokens, e->players, e->psync, e->ptag};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -585,7 +592,8 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     HK_TRY(dalloc(&e->attn, (size_t)d.q_heads * kHeadDim));
     HK_TRY(dalloc(&e->act, d.intermediate));
     HK_TRY(dalloc(&e->normed, d.hidden));
-    HK_TRY(dalloc(&e->logits, d.vocab));
+    // the tail past vocab is the persistent step's per-wave store sink
+    HK_TRY(dalloc(&e->logits, (size_t)d.vocab + kPersistentGrid * (kPersistentThreads / 64)));
     const size_t kv = (size_t)d.layers * kv_layer_elems(e);
     HK_TRY(dalloc(&e->kcache, kv));
     HK_TRY(dalloc(&e->vcache, kv));
@@ -602,7 +610,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     HK_CHECK(hipMemset(e->ctrl, 0, sizeof(StepCtrl)));
     HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
     const char* pers = getenv("HK_PERSISTENT");
-    if (!(pers && pers[0] == '0'))
+    if (!(pers && pers[0] == '0') && d.layers <= kPersistentMaxLayers)
       e->pshape = persistent_shape(d.hidden, d.intermediate, d.q_heads, d.kv_heads, w8);
     if (e->pshape >= 0) {
       std::vector<PersistentLayer> pl(d.layers);
@@ -617,6 +625,8 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
                          hipMemcpyHostToDevice));
       HK_TRY(dalloc(&e->psync, psync_words(e)));
       HK_CHECK(hipMemset(e->psync, 0, psync_words(e) * sizeof(unsigned int)));
+      HK_TRY(dalloc(&e->ptag, ptag_words(e)));
+      HK_CHECK(hipMemset(e->ptag, 0, ptag_words(e) * sizeof(uint32_t)));
     }
     HK_CHECK(hipDeviceSynchronize());
     return 0;

@@ -50,7 +50,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, float* xs, float* red
   const uint32_t* x2 = reinterpret_cast<const uint32_t*>(x);
   float ss = 0.0f;
   for (int i = tid; i < K / 2; i += kThreads) {
-    const uint32_t w = x2[i];
+    const uint32_t w = ldg(x2 + i);
     const float v0 = bf_lo(w), v1 = bf_hi(w);
     xs[2 * i] = v0;
     xs[2 * i + 1] = v1;
@@ -69,7 +69,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, float* xs, float* red
   const float inv = 1.0f / sqrtf(mean + a.eps);
   const uint32_t* g2 = reinterpret_cast<const uint32_t*>(a.gamma);
   for (int i = tid; i < K / 2; i += kThreads) {
-    const uint32_t g = g2[i];
+    const uint32_t g = ldg(g2 + i);
     xs[2 * i] = round_bf16((xs[2 * i] * inv) * bf_lo(g));
     xs[2 * i + 1] = round_bf16((xs[2 * i + 1] * inv) * bf_hi(g));
   }
@@ -119,28 +119,28 @@ __device__ __forceinline__ void finish_row(const GemvArgs& a, int row, bool live
   float accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
   if (!live || l != 0) return;
   if constexpr (W8) {
-    acc = acc * a.scale[row];
-    if constexpr (PAIR) accu = accu * a.scale[row + a.M];
+    acc = acc * ldg(a.scale + row);
+    if constexpr (PAIR) accu = accu * ldg(a.scale + row + a.M);
   }
   switch (a.epi) {
     case EPI_BF16:
-      a.y[row] = (uint16_t)f32_to_bf16(acc);
+      stg(a.y + row, (uint16_t)f32_to_bf16(acc));
       break;
     case EPI_BIAS:
-      a.y[row] = (uint16_t)f32_to_bf16(round_bf16(acc) + a.bias[row]);
+      stg(a.y + row, (uint16_t)f32_to_bf16(round_bf16(acc) + ldg(a.bias + row)));
       break;
     case EPI_RESID:
-      a.y[row] = (uint16_t)f32_to_bf16(round_bf16(acc) + bf16_to_f32(a.resid[row]));
+      stg(a.y + row, (uint16_t)f32_to_bf16(round_bf16(acc) + bf16_to_f32(ldg(a.resid + row))));
       break;
     case EPI_F32:
-      a.yf[row] = acc;
+      stg(a.yf + row, acc);
       break;
     case EPI_F32_ARGMAX:
-      a.yf[row] = acc;
+      stg(a.yf + row, acc);
       best = umax64(best, argmax_key(acc, (uint32_t)row));
       break;
     case EPI_SWIGLU:
-      a.y[row] = (uint16_t)f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu)));
+      stg(a.y + row, (uint16_t)f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))));
       break;
     default:
       break;

@@ -36,15 +36,36 @@ __device__ __forceinline__ float round_bf16(float f) {
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Global-memory accesses go through address-space-1 pointers.  Through a
+// generic pointer the compiler emits flat instructions, which count in both
+// the vector-memory and the LDS counter, so every later LDS access would wait
+// for all outstanding global loads and stores.
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+
+// (scalar and ext_vector types)
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+
+template <typename T>
+__device__ __forceinline__ void stg(T* p, T v) {
+  *(__attribute__((address_space(1))) T*)p = v;
+}
+
+// 8 bytes as two 32-bit words (ldg takes scalar types only).
+__device__ __forceinline__ uint2 ldg_u2(const void* p) {
+  const unsigned long long v = ldg(reinterpret_cast<const unsigned long long*>(p));
+  return make_uint2((unsigned int)v, (unsigned int)(v >> 32));
+}
+
 // Streaming 16-byte load that does not allocate in the caches: every weight
 // byte is read exactly once per decode step.
 __device__ __forceinline__ u32x4 load_stream16(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return __builtin_nontemporal_load((global_u32x4*)p);
 }
 
-__device__ __forceinline__ u32x4 load16(const void* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
+__device__ __forceinline__ u32x4 load16(const void* p) { return *(global_u32x4*)p; }
 
 // Butterfly sum over groups of `width` adjacent lanes (width a power of two).
 template <int width>

@@ -100,8 +100,9 @@ int launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 // ---- whole decode step in one persistent launch (persistent.hip) ----
 constexpr int kPersistentThreads = 512;  // one workgroup per CU
 constexpr int kPersistentGrid = 256;     // workgroups (MI355X has 256 CUs)
-constexpr int kPersistentChunk = 512;    // attention slots per task
+constexpr int kPersistentChunk = 256;    // attention slots per task
 constexpr int kFlagStride = 32;          // uint32 words between flags (one 128-byte line each)
+constexpr int kPersistentMaxLayers = 128;
 
 struct PersistentLayer {
   const uint16_t* qkv;
@@ -125,20 +126,22 @@ struct PersistentArgs {
   const float* sin_tab;
   uint16_t* kcache;  // [L][Hkv][max_ctx][64]
   uint16_t* vcache;
-  uint16_t* h;
-  uint16_t* h1;
-  uint16_t* qkv;
-  uint16_t* attn;
-  uint16_t* act;
-  float* logits;
+  uint16_t* h;  // plain bf16 hidden: layer-0 input when ctrl->token < 0; final hidden out
+  // tagged activations, (tag << 16) | bf16 per element
+  uint32_t* th;     // [H] layer output
+  uint32_t* th1;    // [H] after attention + residual
+  uint32_t* tqkv;   // [(Hq + 2 Hkv) * 64]
+  uint32_t* tattn;  // [Hq * 64]
+  uint32_t* tact;   // [I]
+  uint32_t* pad;    // [kPersistentGrid * 8] per-wave sink for stores of rows a wave does not own
+  float* logits;             // [vocab + kPersistentGrid * 8]: the tail is a per-wave sink
   unsigned long long* keys;  // [kPersistentGrid]
   float* partial;            // [Hq, max_splits, 66]
   unsigned int* counters;    // [Hq], zero between launches
   StepCtrl* ctrl;
   int32_t* out_tokens;
   int32_t* result;
-  unsigned int* progress;  // [kPersistentGrid * kFlagStride] epoch per workgroup
-  unsigned int* headflag;  // [Hq * kFlagStride] epoch per attention head
+  unsigned int* progress;  // [kPersistentGrid * kFlagStride] last epoch per workgroup
   unsigned int* error;     // nonzero: a wait timed out; the launch was abandoned
 };
 

@@ -4,8 +4,8 @@
 // dependent GEMVs (QKV, O, gate/up, down per layer, then the LM head).  As
 // separate kernels each one pays a launch and a full HBM latency before its
 // first byte arrives, so at batch 1 they run at 1-3 TB/s.  Here one
-// workgroup per CU stays resident for the whole step and the phases are
-// linked by flags instead of kernel boundaries:
+// workgroup per CU stays resident for the whole step and hands results
+// from phase to phase through memory:
 //
 //   Q  qkv = bf16(W_qkv @ rmsnorm(h) [+ bias])           cpu_backend.py:134-143
 //   A  RoPE, KV append at slot p, GQA attention          :95-129
@@ -14,25 +14,31 @@
 //   D  h = bf16(bf16(W_d @ act) + h1)                    :166-171
 //   H  logits = W_lm @ rmsnorm(h) (f32), argmax           :173-181
 //
-// * Every wave owns at most one row group per GEMV phase, and issues the
-//   loads of that group's weights as soon as it has finished the previous
-//   phase -- before it waits for the previous phase's results -- so weight
-//   streaming overlaps the dependency wait.  The LM head streams its rows
-//   with a double buffer.
-// * Dependencies: each workgroup publishes an epoch number after its outputs
-//   of a phase are stored (progress[wg]); attention publishes one per query
-//   head (headflag[h]).  A consumer waits only for the producers of what it
-//   reads.  Epochs only grow (base + phase index, base = the epoch the
-//   previous launch ended on), so flags are never reset between steps.
-// * Cross-workgroup data (activations, split-KV partials, argmax keys) is
-//   written and read with device-coherent (sc1) accesses: the eight XCDs have
-//   separate L2 caches, and sc1 accesses bypass their incoherent state
-//   without whole-cache write-back or invalidate fences.  Each producer waits
-//   for its stores (s_waitcnt) before its flag is stored.
+// * Activations travel as tagged 32-bit words, (tag << 16) | bf16, where the
+//   tag names the phase instance that wrote them.  A consumer polls the words
+//   it needs until every one carries the expected tag; a single 32-bit store
+//   is seen whole or not at all, so no separate flag (and no wait for store
+//   completion before one) is needed.  Tags come from an epoch that only
+//   grows: base + phase index, base = the epoch the previous launch ended on,
+//   so buffers are never cleared between steps.  Tags are 1..65535, so
+//   zeroed memory never matches.
+// * In a GEMV phase, wave 7 of each workgroup is the stager: it polls the
+//   input vector, applies RMSNorm, and writes it to one of two LDS buffers
+//   (plus the raw values the residual add needs).  It issues no other global
+//   loads and no stores, so its polls return at the bare memory latency: a
+//   wave's loads complete in order, and on gfx9 its stores count in the same
+//   counter.  Waves 0-6 own at most one row group each and hold its weights in
+//   registers, loaded two phases ahead (O with gate/up right after Q, down with
+//   the next layer's QKV right after gate/up), so weight streaming overlaps
+//   attention and the waits.  The LM head streams rows on all eight waves with
+//   a double buffer.
+// * Cross-workgroup data is written and read with device-coherent (sc1)
+//   accesses: the eight XCDs have separate L2 caches, and sc1 accesses bypass
+//   their incoherent state without whole-cache write-back or invalidate fences.
 // * Every wait is bounded: after kSpinLimit polls, or once another workgroup
 //   has flagged an error, the workgroup records the error and leaves; all
 //   later waits then end at once, so the launch always drains.  The host
-//   reports the error and resets the flags.
+//   reports the error and clears the tags and flags.
 //
 // Rounding points are those of the separate kernels (gemv.hip, attention.hip).
 #include "hk_common.h"
@@ -44,14 +50,16 @@ namespace {
 constexpr int kPT = kPersistentThreads;  // threads per workgroup (one workgroup per CU)
 constexpr int kPW = kPT / 64;             // waves per workgroup
 constexpr int kPf = 16;                   // 16-byte weight chunks a lane holds across a wait
-constexpr int kXMax = 8192;               // floats of x staged in LDS
+constexpr int kXMax = 5120;               // floats per LDS staging buffer
+constexpr int kHMax = 1024;               // raw residual values kept in LDS
+constexpr int kCW = kPW - 1;              // compute waves; wave kCW is the stager
 constexpr int kChunk = kPersistentChunk;  // attention slots per task
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kGroupsPV = kPT / kHalf;    // slot groups of the P @ V loop
 constexpr int kPartStride = kHeadDim + 2;
-constexpr unsigned kSpinLimit = 1u << 21;
+constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait is abandoned
 constexpr int kSc1 = 16;                  // buffer-load cache policy: device scope (sc1)
-static_assert(kChunk == kPT, "one thread per attention slot");
+static_assert(2 * kChunk == kPT, "two threads per attention slot");
 
 // ---- device-coherent accesses ----
 __device__ __forceinline__ void st_c16(uint16_t* p, uint32_t v) {
@@ -79,16 +87,25 @@ __device__ __forceinline__ unsigned long long ld_c64(const unsigned long long* p
   return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
 }
-// 16 bytes at base + off, device-coherent; reads past `bytes` return zero.
-__device__ __forceinline__ u32x4 ld_c128(const void* base, int bytes, int off) {
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1);
+// Buffer resource over [base, base + bytes): loads through it take a 32-bit
+// byte offset, and offsets past `bytes` read zero instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
+// 16 bytes at base + off, device-coherent.
+__device__ __forceinline__ u32x4 ld_c128(const void* base, int bytes, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base, bytes), off, 0, kSc1);
+}
+
 
 __device__ __forceinline__ bool reached(unsigned v, unsigned target) {
   return (int)(v - target) >= 0;
 }
+
+// Tag of epoch e: 1..65535 (never 0, the value of cleared memory).
+__device__ __forceinline__ unsigned tag_of(unsigned e) { return e % 65535u + 1u; }
+
+__device__ __forceinline__ uint32_t tagged(uint32_t bf16, unsigned tag) { return (tag << 16) | bf16; }
 
 // ---- phase shapes ----
 struct PhaseCfg {
@@ -97,15 +114,20 @@ struct PhaseCfg {
 
 // Lanes per row (64, 32, 16 or 8) so that a wave owns at most one row group of
 // the phase at `waves` waves in the grid, with the group's chunks fitting in
-// the kPf prefetch registers.
-constexpr PhaseCfg pick_cfg(int M, int K, bool pair, int waves) {
+// `budget` prefetch registers.
+constexpr PhaseCfg pick_cfg(int M, int K, bool pair, int waves, int budget) {
   for (int lpr = 64; lpr >= 8; lpr /= 2) {
     const int rpw = 64 / lpr;
     const int groups = (M + rpw - 1) / rpw;
     const int nj = (K / 8 + lpr - 1) / lpr;
-    if (groups <= waves && nj * (pair ? 2 : 1) <= kPf) return {lpr, nj};
+    if (groups <= waves && nj * (pair ? 2 : 1) <= budget) return {lpr, nj};
   }
   return {0, 0};
+}
+
+// producers of a phase: workgroups whose compute waves own row groups
+constexpr int producers(PhaseCfg c, int M) {
+  return ((M + 64 / c.lpr - 1) / (64 / c.lpr) + kCW - 1) / kCW;
 }
 
 template <int H_, int I_, int HQ_, int HKV_>
@@ -114,26 +136,39 @@ struct Shape {
   static constexpr int QPK = HQ / HKV;
   static constexpr int QKV = (HQ + 2 * HKV) * kHeadDim;
   static constexpr int AO = HQ * kHeadDim;
-  static constexpr int kWaves = kPersistentGrid * kPW;
-  static constexpr PhaseCfg q = pick_cfg(QKV, H, false, kWaves);
-  static constexpr PhaseCfg o = pick_cfg(H, AO, false, kWaves);
-  static constexpr PhaseCfg g = pick_cfg(I, H, true, kWaves);
-  static constexpr PhaseCfg d = pick_cfg(H, I, false, kWaves);
+  static constexpr int kWaves = kPersistentGrid * kCW;
+  static constexpr PhaseCfg q = pick_cfg(QKV, H, false, kWaves, 4);
+  static constexpr PhaseCfg o = pick_cfg(H, AO, false, kWaves, 4);
+  static constexpr PhaseCfg g = pick_cfg(I, H, true, kWaves, kPf - o.nj);
+  static constexpr PhaseCfg d = pick_cfg(H, I, false, kWaves, kPf - q.nj);
+  // register slots: O and gate/up are held together, then down and next QKV
+  static constexpr int off_o = 0, off_g = o.nj, off_d = 0, off_q = d.nj;
   static constexpr int head_lpr = 16;
   static constexpr int head_nj = (H / 8 + head_lpr - 1) / head_lpr;
+  static constexpr int nq = producers(q, QKV), no = producers(o, H);
+  static constexpr int ng = producers(g, I), nd = producers(d, H);
   static_assert(q.lpr && o.lpr && g.lpr && d.lpr, "no register plan for this shape");
   static_assert(head_nj <= kPf / 2, "LM head rows too long for the double buffer");
-  static_assert(H <= kXMax && I <= kXMax && AO <= kXMax, "x staging too small");
-  static_assert(H % 8 == 0 && I % 8 == 0, "rows are read in 16-byte chunks");
+  static_assert(H <= kXMax && I <= kXMax && AO <= kXMax && H <= kHMax, "x staging too small");
+  static_assert((I / 4 + 63) / 64 <= 32 && (H / 4 + 63) / 64 <= 32 && (AO / 4 + 63) / 64 <= 32,
+                "stager chunk mask is 32 bits");
+  static_assert(H % 8 == 0 && I % 8 == 0 && AO % 8 == 0, "rows are read in 16-byte chunks");
+  // residual rows are fetched by workgroups that have just seen the whole
+  // source vector: O rows by Q producers, down rows by gate/up producers
+  // the stager of an O-row workgroup saw all of h (Q phase), of a down-row
+  // workgroup all of h1 (gate/up phase); each such workgroup also takes part
+  // in every phase between the write of its raw residual copy and its use
+  static_assert(no <= nq && nd <= ng && no <= ng && nd <= nq && nd <= no,
+                "residual copies need nested producer sets");
 };
 
-// producers of a phase: workgroups whose waves own row groups
-__host__ __device__ constexpr int producers(PhaseCfg c, int M) {
-  return ((M + 64 / c.lpr - 1) / (64 / c.lpr) + kPW - 1) / kPW;
-}
-
 struct PShared {
-  float xs[kXMax];
+  // layer table: read from LDS, since a global read of it would make the
+  // wave wait for all its outstanding loads and stores first
+  PersistentLayer layers[kPersistentMaxLayers];
+  float xs[2][kXMax];   // staged GEMV inputs (alternating); attention scratch in xs[0]
+  float raw_h[kHMax];   // layer input h before RMSNorm: residual of the O rows
+  float raw_h1[kHMax];  // h1 before RMSNorm: residual of the down rows
   float red[2][kPW];
   unsigned long long keys[kPW];
   int abort;
@@ -143,33 +178,53 @@ struct PShared {
 struct Ctx {
   const PersistentArgs* a;
   PShared* sm;
-  int wg, wave, lane, gw;
+  int wg, wave, lane;
+  int gw;  // compute-wave index wg * kCW + wave (wave < kCW)
 };
 
-// Wave 0 waits until flags[i * kFlagStride] has reached `target` for every i
-// in the given ranges; the other waves wait at the workgroup barrier.
-// Returns false when the launch is being abandoned.
-__device__ bool wait_flags(Ctx& c, const unsigned* flags, int lo0, int hi0, int lo1, int hi1,
-                           int lo2, int hi2, unsigned target) {
+// Record an abandoned launch (first failing wait) for the host.
+__device__ __forceinline__ bool give_up(const PersistentArgs& a) {
+  st_c32(a.error, 1u);
+  return false;
+}
+
+// Poll one tagged word until it carries `tag`; false when the launch is abandoned.
+__device__ bool poll_word(const PersistentArgs& a, const uint32_t* p, unsigned tag, uint32_t& out) {
+  for (unsigned spins = 1;; ++spins) {
+    const uint32_t w = ld_c32(p);
+    if ((w >> 16) == tag) {
+      out = w;
+      return true;
+    }
+    if ((spins & 63u) == 0u && (ld_c32(a.error) != 0u || spins > kSpinLimit)) return give_up(a);
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Poll the 16-byte chunk at byte `off` of a tagged buffer of `bytes` bytes.
+__device__ bool poll_chunk(const PersistentArgs& a, const uint32_t* base, int bytes, int off,
+                           unsigned tag, u32x4& v) {
+  for (unsigned spins = 1;; ++spins) {
+    v = ld_c128(base, bytes, off);
+    if ((v.x >> 16) == tag && (v.y >> 16) == tag && (v.z >> 16) == tag && (v.w >> 16) == tag)
+      return true;
+    if ((spins & 63u) == 0u && (ld_c32(a.error) != 0u || spins > kSpinLimit)) return give_up(a);
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Wave 0 waits until flags[i * kFlagStride] has reached `target` for i < n;
+// the other waves wait at the workgroup barrier.  False when abandoned.
+__device__ bool wait_all(Ctx& c, const unsigned* flags, int n, unsigned target) {
   if (c.wave == 0) {
-    const int n0 = hi0 - lo0, n1 = hi1 - lo1, n2 = hi2 - lo2;
-    const int total = n0 + n1 + n2;
-    unsigned spins = 0;
     int abort = 0;
-    for (;;) {
+    for (unsigned spins = 1;; ++spins) {
       bool ok = true;
-      for (int i = c.lane; i < total; i += 64) {
-        const int f = i < n0 ? lo0 + i : i < n0 + n1 ? lo1 + (i - n0) : lo2 + (i - n0 - n1);
-        ok = ok && reached(ld_c32(flags + (size_t)f * kFlagStride), target);
-      }
+      for (int i = c.lane; i < n; i += 64) ok = ok && reached(ld_c32(flags + (size_t)i * kFlagStride), target);
       if (__all(ok)) break;
-      if (ld_c32(c.a->error) != 0u) {
+      if ((spins & 63u) == 0u && (ld_c32(c.a->error) != 0u || spins > kSpinLimit)) {
         abort = 1;
-        break;
-      }
-      if (++spins > kSpinLimit) {
-        abort = 1;
-        if (c.lane == 0) st_c32(c.a->error, 1u);
+        if (c.lane == 0) give_up(*c.a);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -180,10 +235,6 @@ __device__ bool wait_flags(Ctx& c, const unsigned* flags, int lo0, int hi0, int 
   return c.sm->abort == 0;
 }
 
-__device__ __forceinline__ bool wait_all(Ctx& c, const unsigned* flags, int n, unsigned target) {
-  return wait_flags(c, flags, 0, n, 0, 0, 0, 0, target);
-}
-
 // Publish this workgroup's epoch once every thread's stores have completed.
 __device__ __forceinline__ void publish(Ctx& c, unsigned* flag, unsigned epoch) {
   __builtin_amdgcn_s_waitcnt(0);
@@ -191,67 +242,127 @@ __device__ __forceinline__ void publish(Ctx& c, unsigned* flag, unsigned epoch) 
   if (threadIdx.x == 0) st_c32(flag, epoch);
 }
 
-// Stage K bf16 values into LDS as f32 (coherent loads when another workgroup
-// wrote them), RMS-normalised with gamma when given (cpu_backend.py:71-76).
+// Stager: poll the K tagged words at src until all carry `tag` (a lane keeps
+// up to kBatch chunks in flight at once), then write them to xs as f32 --
+// RMS-normalised with gamma when given (cpu_backend.py:71-76) -- and the raw
+// values to `raw` when given.  Runs on one wave; false when abandoned.
+constexpr int kBatch = 10;
+
 template <int K>
-__device__ void stage_x(Ctx& c, const uint16_t* src, bool coherent, const uint16_t* gamma,
-                        float eps) {
-  constexpr int CH = K / 8;
-  float* xs = c.sm->xs;
+__device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigned tag,
+                           const uint16_t* gamma, float eps, float* xs, float* raw) {
+  constexpr int CH = K / 4;  // 16-byte chunks of four tagged words
+  constexpr int PER = (CH + 63) / 64;
+  const int lane = threadIdx.x & 63;
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < CH; i += kPT) {
-    const u32x4 v = coherent ? ld_c128(src, K * 2, i * 16) : load16(src + i * 8);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float lo = bf_lo(w[q]), hi = bf_hi(w[q]);
-      xs[i * 8 + 2 * q] = lo;
-      xs[i * 8 + 2 * q + 1] = hi;
-      ss += lo * lo;
-      ss += hi * hi;
+  for (int j0 = 0; j0 < PER; j0 += kBatch) {
+    constexpr int B = PER < kBatch ? PER : kBatch;
+    unsigned pending = 0;
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int ch = lane + 64 * (j0 + j);
+      if (j0 + j < PER && ch < CH) pending |= 1u << j;
+    }
+    u32x4 v[B];
+    for (unsigned spins = 1;; ++spins) {
+#pragma unroll
+      for (int j = 0; j < B; ++j)
+        if ((pending >> j) & 1u)
+          v[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src, K * 4), lane * 16, (j0 + j) * 1024, kSc1);
+#pragma unroll
+      for (int j = 0; j < B; ++j)
+        if (((pending >> j) & 1u) && (v[j].x >> 16) == tag && (v[j].y >> 16) == tag &&
+            (v[j].z >> 16) == tag && (v[j].w >> 16) == tag)
+          pending &= ~(1u << j);
+      if (!__any(pending != 0u)) break;
+      if ((spins & 63u) == 0u && (ld_c32(a.error) != 0u || spins > kSpinLimit)) return give_up(a);
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int ch = lane + 64 * (j0 + j);
+      if (j0 + j < PER && ch < CH) {
+        const float f[4] = {bf_lo(v[j].x), bf_lo(v[j].y), bf_lo(v[j].z), bf_lo(v[j].w)};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          ss += f[q] * f[q];
+          xs[ch * 4 + q] = f[q];
+          if (raw != nullptr) raw[ch * 4 + q] = f[q];
+        }
+      }
     }
   }
   if (gamma != nullptr) {
     ss = group_sum<64>(ss);
-    if (c.lane == 0) c.sm->red[0][c.wave] = ss;
-    __syncthreads();
-    float total = c.sm->red[0][0];
-#pragma unroll
-    for (int w = 1; w < kPW; ++w) total += c.sm->red[0][w];
-    const float inv = 1.0f / sqrtf(total / (float)K + eps);
-    for (int i = threadIdx.x; i < CH; i += kPT) {
-      const u32x4 gv = load16(gamma + i * 8);
-      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        xs[i * 8 + 2 * q] = round_bf16((xs[i * 8 + 2 * q] * inv) * bf_lo(gw[q]));
-        xs[i * 8 + 2 * q + 1] = round_bf16((xs[i * 8 + 2 * q + 1] * inv) * bf_hi(gw[q]));
-      }
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    for (int ch = lane; ch < CH; ch += 64) {
+      const uint2 g = ldg_u2(gamma + ch * 4);
+      xs[ch * 4 + 0] = round_bf16((xs[ch * 4 + 0] * inv) * bf_lo(g.x));
+      xs[ch * 4 + 1] = round_bf16((xs[ch * 4 + 1] * inv) * bf_hi(g.x));
+      xs[ch * 4 + 2] = round_bf16((xs[ch * 4 + 2] * inv) * bf_lo(g.y));
+      xs[ch * 4 + 3] = round_bf16((xs[ch * 4 + 3] * inv) * bf_hi(g.y));
     }
   }
-  __syncthreads();
+  return true;
 }
 
-// Issue the loads of this wave's row group (rows gw*RPW + sub) of W [M, K]
-// (plus the paired rows M.. for gate/up) into pf.
-template <int LPR, int NJ, bool PAIR>
+// Stager for plain bf16 input written before the launch (layer 0).
+template <int K>
+__device__ void stage_wave_plain(const uint16_t* src, const uint16_t* gamma, float eps, float* xs,
+                                 float* raw) {
+  constexpr int CH = K / 4;
+  const int lane = threadIdx.x & 63;
+  float ss = 0.0f;
+  for (int ch = lane; ch < CH; ch += 64) {
+    const uint2 w = ldg_u2(src + ch * 4);
+    const float f[4] = {bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y)};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ss += f[q] * f[q];
+      raw[ch * 4 + q] = f[q];
+      xs[ch * 4 + q] = f[q];
+    }
+  }
+  if (gamma == nullptr) return;
+  ss = group_sum<64>(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+  for (int ch = lane; ch < CH; ch += 64) {
+    const uint2 g = ldg_u2(gamma + ch * 4);
+    xs[ch * 4 + 0] = round_bf16((xs[ch * 4 + 0] * inv) * bf_lo(g.x));
+    xs[ch * 4 + 1] = round_bf16((xs[ch * 4 + 1] * inv) * bf_hi(g.x));
+    xs[ch * 4 + 2] = round_bf16((xs[ch * 4 + 2] * inv) * bf_lo(g.y));
+    xs[ch * 4 + 3] = round_bf16((xs[ch * 4 + 3] * inv) * bf_hi(g.y));
+  }
+}
+
+// Issue the loads of this wave's row group (rows group*RPW + sub) of W [M, K]
+// (plus the paired rows M.. for gate/up) into pf[OFF ...].  The loads are
+// unconditional buffer loads -- a row outside [0, M), a chunk past the row
+// or a workgroup that is not `live` reads zero through an offset past the
+// resource -- so every compute wave issues the same memory instructions in
+// every phase and the compiler can wait for exactly the loads it needs.
+constexpr unsigned kOutside = 0x7ffffff0u;  // byte offset beyond every resource
+constexpr int kNT = 2;                      // buffer-load cache policy: non-temporal
+
+template <int LPR, int NJ, bool PAIR, int OFF>
 __device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const uint16_t* W, int M, int K,
-                                         int group) {
+                                         int group, bool live_wg) {
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
   const int l = lane % LPR, sub = lane / LPR;
   const int row = group * RPW + sub;
-  const bool live = row < M;
-  const int CH = K / 8;
-  const char* wrow = reinterpret_cast<const char*>(W) + (size_t)(live ? row : 0) * K * 2;
-  const size_t pair_off = (size_t)M * K * 2;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
+  const bool live = live_wg && row < M;
+  const __amdgpu_buffer_rsrc_t r = rsrc(W, (PAIR ? 2 : 1) * M * K * 2);
+  // one VGPR per lane: the chunk stride and the gate/up distance go in the
+  // scalar offset.  Chunks past the row end read the next row (ignored by
+  // dot_group) or, past the matrix, zero.
+  const unsigned voff = live ? (unsigned)row * (unsigned)K * 2u + (unsigned)l * 16u : kOutside;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int ch = l + j * LPR;
-    const bool ok = live && ch < CH;
-    pf[j] = ok ? load_stream16(wrow + (size_t)ch * 16) : zero;
-    if constexpr (PAIR) pf[NJ + j] = ok ? load_stream16(wrow + pair_off + (size_t)ch * 16) : zero;
+    pf[OFF + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, j * LPR * 16, kNT);
+    if constexpr (PAIR)
+      pf[OFF + NJ + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, M * K * 2 + j * LPR * 16, kNT);
   }
 }
 
@@ -270,7 +381,7 @@ __device__ __forceinline__ void fma8(const u32x4 w, const float* xs, int ch, flo
 
 // Dot products of the prefetched row group with the staged x; every lane of
 // the row's LPR lanes ends with the sums.
-template <int LPR, int NJ, bool PAIR>
+template <int LPR, int NJ, bool PAIR, int OFF>
 __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const float* xs, int K,
                                           float& acc, float& accu) {
   const int l = (threadIdx.x & 63) % LPR;
@@ -280,8 +391,8 @@ __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const float* x
   for (int j = 0; j < NJ; ++j) {
     const int ch = l + j * LPR;
     if (ch < CH) {
-      fma8(pf[j], xs, ch, a0, a1);
-      if constexpr (PAIR) fma8(pf[NJ + j], xs, ch, b0, b1);
+      fma8(pf[OFF + j], xs, ch, a0, a1);
+      if constexpr (PAIR) fma8(pf[OFF + NJ + j], xs, ch, b0, b1);
     }
   }
   acc = group_sum<LPR>(a0 + a1);
@@ -296,7 +407,8 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 // ---- attention task: query head h, slots [s * kChunk, ...] of layer l ----
 template <class S>
-__device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned ep_q, unsigned ep_a) {
+__device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_q,
+                               unsigned tag_a) {
   const PersistentArgs& a = *c.a;
   const int g = h / S::QPK;
   const int t0 = s * kChunk;
@@ -304,108 +416,118 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned ep_q
   const int nsplit = p / kChunk + 1;
   const bool holds_new = (s == nsplit - 1);
   const int tid = threadIdx.x;
-  float* qs = c.sm->xs;                 // [64]
+  float* qs = c.sm->xs[0];              // [64]
   float* knew = qs + kHeadDim;          // [64]
   float* pr = knew + kHeadDim;          // [kChunk]
   float* acc = pr + kChunk;             // [kGroupsPV][64]
   const size_t head_base = ((size_t)l * S::HKV + g) * a.max_ctx;
-  const uint16_t* kc = a.kcache + head_base * kHeadDim;
-  const uint16_t* vc = a.vcache + head_base * kHeadDim;
+  // this head's cache rows [0, p): slots p and beyond read as zero
+  const __amdgpu_buffer_rsrc_t kc = rsrc(a.kcache + head_base * kHeadDim, p * kHeadDim * 2);
+  const __amdgpu_buffer_rsrc_t vc = rsrc(a.vcache + head_base * kHeadDim, p * kHeadDim * 2);
 
-  // K row of this thread's slot: cache rows were written by earlier launches,
-  // so these loads go out before the wait.
-  const int slot = t0 + tid;
-  const bool has_slot = tid < n && slot != p;
-  u32x4 krow[kHeadDim / 8];
-  {
-    const uint16_t* src = kc + (size_t)(has_slot ? slot : 0) * kHeadDim;
+  // Cached K half-row of this thread's slot (two threads per slot, one per
+  // 32 dimensions) and V words of its slot group (rows written by earlier
+  // launches) go out before the new q/k/v are polled.
+  const int si = tid >> 1, half = tid & 1;
+  const int slot = t0 + si;
+  u32x4 krow[kHeadDim / 16];
 #pragma unroll
-    for (int ch = 0; ch < kHeadDim / 8; ++ch)
-      krow[ch] = has_slot ? load16(src + ch * 8) : u32x4{0u, 0u, 0u, 0u};
-  }
-
-  // rows of q head h, k head g, v head g come from Q-phase producers
-  constexpr int rows_per_wg = kPW * (64 / S::q.lpr);
-  const int qr = h * kHeadDim, kr = (S::HQ + g) * kHeadDim, vr = (S::HQ + S::HKV + g) * kHeadDim;
-  if (!wait_flags(c, a.progress, qr / rows_per_wg, (qr + kHeadDim - 1) / rows_per_wg + 1,
-                  kr / rows_per_wg, (kr + kHeadDim - 1) / rows_per_wg + 1, vr / rows_per_wg,
-                  (vr + kHeadDim - 1) / rows_per_wg + 1, ep_q))
-    return false;
-
-  const uint16_t* qkv = a.qkv;
-  const uint16_t* vnew = qkv + vr;
-  // V words of this thread's slot group for the P @ V loop (slot p from
-  // qkv); they arrive while the scores and the softmax are formed
+  for (int ch = 0; ch < kHeadDim / 16; ++ch)
+    krow[ch] = __builtin_amdgcn_raw_buffer_load_b128(kc, slot * kHeadDim * 2 + half * kHeadDim,
+                                                     ch * 16, 0);
   const int dp = tid & (kHalf - 1);
   const int gi = tid / kHalf;
   uint32_t vw[kChunk / kGroupsPV];
+  const int voff = (t0 + gi) * kHeadDim * 2 + dp * 4;
 #pragma unroll
-  for (int k = 0; k < kChunk / kGroupsPV; ++k) {
-    const int sl = t0 + gi + k * kGroupsPV;
-    vw[k] = sl < p ? reinterpret_cast<const uint32_t*>(vc + (size_t)sl * kHeadDim)[dp]
-            : sl == p ? ld_c16(vnew + 2 * dp) | (ld_c16(vnew + 2 * dp + 1) << 16)
-                      : 0u;
-  }
+  for (int k = 0; k < kChunk / kGroupsPV; ++k)
+    vw[k] = __builtin_amdgcn_raw_buffer_load_b32(vc, voff, k * kGroupsPV * kHeadDim * 2, 0);
 
+  const int qr = h * kHeadDim, kr = (S::HQ + g) * kHeadDim, vr = (S::HQ + S::HKV + g) * kHeadDim;
+  const uint32_t* tq = a.tqkv;
+  bool ok = true;
+  // the slot-p value word of the P @ V loop, for the group holding slot p
+  if ((p - t0 - gi) % kGroupsPV == 0 && p - t0 - gi >= 0) {
+    const int kp = (p - t0 - gi) / kGroupsPV;
+    uint32_t lo = 0, hi = 0;
+    ok = poll_word(a, tq + vr + 2 * dp, tag_q, lo) && poll_word(a, tq + vr + 2 * dp + 1, tag_q, hi);
+    const uint32_t word = (lo & 0xffffu) | (hi << 16);
+#pragma unroll
+    for (int k = 0; k < kChunk / kGroupsPV; ++k)
+      if (k == kp) vw[k] = word;
+  }
   // rotated q head and new key (bf16-rounded); the group's first query head
   // appends k and v at slot p
-  if (tid < 2 * kHalf) {
+  if (tid < 2 * kHalf && ok) {
     const int j = tid & (kHalf - 1);
     const bool is_k = tid >= kHalf;
-    const uint16_t* src = qkv + (is_k ? kr : qr);
-    const float cs = a.cos_tab[(size_t)p * kHalf + j];
-    const float sn = a.sin_tab[(size_t)p * kHalf + j];
-    const float x1 = bf16_to_f32(ld_c16(src + j)), x2 = bf16_to_f32(ld_c16(src + j + kHalf));
+    const uint32_t* src = tq + (is_k ? kr : qr);
+    const float cs = ldg(a.cos_tab + (size_t)p * kHalf + j);
+    const float sn = ldg(a.sin_tab + (size_t)p * kHalf + j);
+    uint32_t w1 = 0, w2 = 0;
+    ok = poll_word(a, src + j, tag_q, w1) && poll_word(a, src + j + kHalf, tag_q, w2);
+    const float x1 = bf_lo(w1), x2 = bf_lo(w2);
     const uint32_t r1 = f32_to_bf16(x1 * cs - x2 * sn);
     const uint32_t r2 = f32_to_bf16(x2 * cs + x1 * sn);
     float* dst = is_k ? knew : qs;
     dst[j] = bf16_to_f32(r1);
     dst[j + kHalf] = bf16_to_f32(r2);
-    if (is_k && holds_new && h % S::QPK == 0) {
+    if (is_k && holds_new && h % S::QPK == 0 && ok) {
+      uint32_t v1 = 0, v2 = 0;
+      ok = poll_word(a, tq + vr + j, tag_q, v1) && poll_word(a, tq + vr + j + kHalf, tag_q, v2);
       uint16_t* kd = a.kcache + (head_base + p) * kHeadDim;
       uint16_t* vd = a.vcache + (head_base + p) * kHeadDim;
-      kd[j] = (uint16_t)r1;
-      kd[j + kHalf] = (uint16_t)r2;
-      vd[j] = (uint16_t)ld_c16(vnew + j);
-      vd[j + kHalf] = (uint16_t)ld_c16(vnew + j + kHalf);
+      stg(kd + j, (uint16_t)r1);
+      stg(kd + j + kHalf, (uint16_t)r2);
+      stg(vd + j, (uint16_t)v1);
+      stg(vd + j + kHalf, (uint16_t)v2);
     }
   }
-  __syncthreads();
+  if (__syncthreads_or(!ok)) return false;
 
   const float scale = 1.0f / 8.0f;  // head_dim ** -0.5 for head_dim 64 (exact)
-  float sc = -INFINITY;
-  if (tid < n) {
-    float dot = 0.0f;
+  float dot = 0.0f;
+  {
+    const float* qh = qs + half * kHalf;
     if (slot == p) {
-#pragma unroll
-      for (int d = 0; d < kHeadDim; ++d) dot = fmaf(qs[d], knew[d], dot);
+      const float* kh = knew + half * kHalf;
+      for (int d = 0; d < kHalf; ++d) dot = fmaf(qh[d], kh[d], dot);
     } else {
 #pragma unroll
-      for (int ch = 0; ch < kHeadDim / 8; ++ch) {
-        const uint32_t w[4] = {krow[ch].x, krow[ch].y, krow[ch].z, krow[ch].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          dot = fmaf(qs[ch * 8 + 2 * q], bf_lo(w[q]), dot);
-          dot = fmaf(qs[ch * 8 + 2 * q + 1], bf_hi(w[q]), dot);
-        }
+      for (int ch = 0; ch < kHeadDim / 16; ++ch) {
+        // eight q values per step: keeps the LDS reads from being hoisted
+        // into many live registers
+        const float4 q0 = reinterpret_cast<const float4*>(qh)[2 * ch];
+        const float4 q1 = reinterpret_cast<const float4*>(qh)[2 * ch + 1];
+        dot = fmaf(q0.x, bf_lo(krow[ch].x), dot);
+        dot = fmaf(q0.y, bf_hi(krow[ch].x), dot);
+        dot = fmaf(q0.z, bf_lo(krow[ch].y), dot);
+        dot = fmaf(q0.w, bf_hi(krow[ch].y), dot);
+        dot = fmaf(q1.x, bf_lo(krow[ch].z), dot);
+        dot = fmaf(q1.y, bf_hi(krow[ch].z), dot);
+        dot = fmaf(q1.z, bf_lo(krow[ch].w), dot);
+        dot = fmaf(q1.w, bf_hi(krow[ch].w), dot);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    sc = dot * scale;
   }
+  dot += __shfl_xor(dot, 1, 64);  // the two halves of the slot
+  const bool live = si < n;
+  const float sc = live ? dot * scale : -INFINITY;
   float m = group_max<64>(sc);
   if (c.lane == 0) c.sm->red[0][c.wave] = m;
   __syncthreads();
   m = c.sm->red[0][0];
 #pragma unroll
   for (int w = 1; w < kPW; ++w) m = fmaxf(m, c.sm->red[0][w]);
-  const float e = tid < n ? expf(sc - m) : 0.0f;
-  float sum = group_sum<64>(e);
+  const float e = live ? expf(sc - m) : 0.0f;
+  float sum = group_sum<64>(half == 0 ? e : 0.0f);  // each slot once
   if (c.lane == 0) c.sm->red[1][c.wave] = sum;
   __syncthreads();
   sum = c.sm->red[1][0];
 #pragma unroll
   for (int w = 1; w < kPW; ++w) sum += c.sm->red[1][w];
-  pr[tid] = nsplit == 1 ? e / sum : e;  // a single chunk normalises first, as NumPy does
+  if (half == 0) pr[si] = nsplit == 1 ? e / sum : e;  // a single chunk normalises first, as NumPy does
   __syncthreads();
 
   float o0 = 0.0f, o1 = 0.0f;
@@ -417,6 +539,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned ep_q
       o0 = fmaf(pt, bf_lo(vw[k]), o0);
       o1 = fmaf(pt, bf_hi(vw[k]), o1);
     }
+    if (k % 8 == 7) __builtin_amdgcn_sched_barrier(0);
   }
   acc[gi * kHeadDim + 2 * dp] = o0;
   acc[gi * kHeadDim + 2 * dp + 1] = o1;
@@ -426,10 +549,9 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned ep_q
 #pragma unroll
     for (int k = 0; k < kGroupsPV; ++k) o += acc[k * kHeadDim + tid];
   }
-  uint16_t* out = a.attn + (size_t)h * kHeadDim;
+  uint32_t* out = a.tattn + (size_t)h * kHeadDim;
   if (nsplit == 1) {
-    if (tid < kHeadDim) st_c16(out + tid, f32_to_bf16(o));
-    publish(c, a.headflag + (size_t)h * kFlagStride, ep_a);
+    if (tid < kHeadDim) st_c32(out + tid, tagged(f32_to_bf16(o), tag_a));
     return true;
   }
 
@@ -459,11 +581,10 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned ep_q
       lsum = fmaf(ld_cf(pj + kHeadDim + 1), f, lsum);
       r = fmaf(ld_cf(pj + tid), f, r);
     }
-    st_c16(out + tid, f32_to_bf16(r / lsum));
+    st_c32(out + tid, tagged(f32_to_bf16(r / lsum), tag_a));
   }
   if (tid == 0)
     (void)__hip_atomic_exchange(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  publish(c, a.headflag + (size_t)h * kFlagStride, ep_a);
   return true;
 }
 
@@ -477,88 +598,134 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   c.wg = blockIdx.x;
   c.wave = threadIdx.x >> 6;
   c.lane = threadIdx.x & 63;
-  c.gw = c.wg * kPW + c.wave;
+  c.gw = c.wg * kCW + c.wave;
+  const bool stager = c.wave == kCW;
   if (threadIdx.x == 0) sm.abort = 0;
 
   const PersistentArgs& a = args;
   const int L = a.layers;
-  const unsigned base = ld_c32(a.progress + (size_t)c.wg * kFlagStride);  // this workgroup's last epoch
-  const int token = a.ctrl->token;
-  const int p = a.ctrl->position;
-  const uint16_t* embed_row =
-      token >= 0 ? a.embed + (size_t)min(token, a.vocab - 1) * S::H : nullptr;
+  static_assert(sizeof(PersistentLayer) % 8 == 0, "layer table is copied in 8-byte words");
+  {
+    constexpr int kWords = sizeof(PersistentLayer) / 8;
+    const unsigned long long* src = reinterpret_cast<const unsigned long long*>(a.w);
+    unsigned long long* dst = reinterpret_cast<unsigned long long*>(sm.layers);
+    for (int i = threadIdx.x; i < L * kWords; i += kPT) dst[i] = ldg(src + i);
+  }
+  __syncthreads();
   unsigned* my_flag = a.progress + (size_t)c.wg * kFlagStride;
+  const unsigned base = ld_c32(my_flag);  // the epoch this workgroup ended the last launch on
+  const int token = ldg(&a.ctrl->token);
+  const int p = ldg(&a.ctrl->position);
+  // layer 0 reads the embedding row, or the hidden state the host preloaded
+  const uint16_t* x0 = token >= 0 ? a.embed + (size_t)min(token, a.vocab - 1) * S::H : a.h;
+  const bool is_q = c.wg < S::nq, is_o = c.wg < S::no, is_g = c.wg < S::ng, is_d = c.wg < S::nd;
+  const int tasks = S::HQ * (p / kChunk + 1);
 
-  constexpr int nq = producers(S::q, S::QKV), no = producers(S::o, S::H);
-  constexpr int ng = producers(S::g, S::I), nd = producers(S::d, S::H);
-  const bool is_q = c.wg < nq, is_o = c.wg < no, is_g = c.wg < ng, is_d = c.wg < nd;
-  const int nsplit = p / kChunk + 1;
-  const int tasks = S::HQ * nsplit;
+  // Row of this lane in each GEMV phase.  Every compute wave stores once per
+  // phase: a row it does not own (or a phase its workgroup sits out) goes to
+  // the wave's own pad word, so all compute waves issue the same stores.
+  uint32_t* pad = a.pad + c.wg * kPW + c.wave;
+  const int row_q = c.gw * (64 / S::q.lpr) + c.lane / S::q.lpr;
+  const int row_o = c.gw * (64 / S::o.lpr) + c.lane / S::o.lpr;
+  const int row_g = c.gw * (64 / S::g.lpr) + c.lane / S::g.lpr;
+  const int row_d = c.gw * (64 / S::d.lpr) + c.lane / S::d.lpr;
+  uint32_t* const dst_q = is_q && row_q < S::QKV ? a.tqkv + row_q : pad;
+  uint32_t* const dst_o = is_o && row_o < S::H ? a.th1 + row_o : pad;
+  uint32_t* const dst_g = is_g && row_g < S::I ? a.tact + row_g : pad;
+  uint32_t* const dst_d = is_d && row_d < S::H ? a.th + row_d : pad;
+  uint16_t* const dst_h = is_d && row_d < S::H ? a.h + row_d : reinterpret_cast<uint16_t*>(pad);
+  const int res_o = min(row_o, S::H - 1), res_d = min(row_d, S::H - 1);
+  const unsigned bias_off = is_q && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
 
   u32x4 pf[kPf];
-  float acc, accu;
-  if (is_q) prefetch<S::q.lpr, S::q.nj, false>(pf, a.w[0].qkv, S::QKV, S::H, c.gw);
-  __syncthreads();
+  float acc, accu, bias_q = 0.0f;
+  int buf = 0;  // LDS staging buffer of the next GEMV phase
+  if (!stager) {
+    prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, is_q);
+    bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           rsrc(sm.layers[0].qkv_bias, S::QKV * 4), bias_off, 0, 0));
+  }
+
+  // The stager fills xs[buf]; the barrier hands it to the compute waves.
+  // Returns false (in every wave) when the launch is abandoned.
+  auto handoff = [&](bool ok) -> bool {
+    if (stager && c.lane == 0 && !ok) sm.abort = 1;
+    __syncthreads();
+    return sm.abort == 0;
+  };
 
   for (int l = 0; l < L; ++l) {
-    const PersistentLayer& lw = a.w[l];
-    const unsigned ep = base + 5u * (unsigned)l;
+    const PersistentLayer& lw = sm.layers[l];
+    const unsigned ep = base + 5u * (unsigned)l;  // epoch of the previous layer's down phase
     // ---- Q ----
     if (is_q) {
-      const uint16_t* xsrc = (l == 0 && embed_row) ? embed_row : a.h;
-      if (l > 0 && !wait_all(c, a.progress, nd, ep)) return;
-      stage_x<S::H>(c, xsrc, xsrc == a.h, lw.in_norm, a.eps);
-      dot_group<S::q.lpr, S::q.nj, false>(pf, sm.xs, S::H, acc, accu);
-      const int row = c.gw * (64 / S::q.lpr) + c.lane / S::q.lpr;
-      if (c.lane % S::q.lpr == 0 && row < S::QKV) {
-        const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + lw.qkv_bias[row])
-                                       : f32_to_bf16(acc);
-        st_c16(a.qkv + row, y);
+      bool ok = true;
+      if (stager) {
+        if (l == 0)
+          stage_wave_plain<S::H>(x0, lw.in_norm, a.eps, sm.xs[buf], sm.raw_h);
+        else
+          ok = stage_wave<S::H>(a, a.th, tag_of(ep), lw.in_norm, a.eps, sm.xs[buf], sm.raw_h);
       }
-      publish(c, my_flag, ep + 1);
+      if (!handoff(ok)) return;
     }
-    // ---- A ---- (tasks go to the highest workgroups, which own no Q rows)
+    if (!stager) {
+      dot_group<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.xs[buf], S::H, acc, accu);
+      const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
+      st_c32(dst_q, tagged(y, tag_of(ep + 1)));
+    }
+    if (is_q) buf ^= 1;
+    // ---- A ---- (tasks go to the highest workgroups, which own no Q rows;
+    // the O and gate/up weights are requested after it, so that registers
+    // are not held across attention)
     for (int t = kPersistentGrid - 1 - c.wg; t < tasks; t += kPersistentGrid) {
       __syncthreads();  // LDS reuse
-      if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, ep + 1, ep + 2)) return;
+      if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2))) return;
     }
-    if (is_o) prefetch<S::o.lpr, S::o.nj, false>(pf, lw.o, S::H, S::AO, c.gw);
+    if (!stager) {
+      prefetch<S::o.lpr, S::o.nj, false, S::off_o>(pf, lw.o, S::H, S::AO, c.gw, is_o);
+      prefetch<S::g.lpr, S::g.nj, true, S::off_g>(pf, lw.gate_up, S::I, S::H, c.gw, is_g);
+    }
     // ---- O ----
     if (is_o) {
-      if (!wait_all(c, a.headflag, S::HQ, ep + 2)) return;
-      stage_x<S::AO>(c, a.attn, true, nullptr, 0.0f);
-      dot_group<S::o.lpr, S::o.nj, false>(pf, sm.xs, S::AO, acc, accu);
-      const int row = c.gw * (64 / S::o.lpr) + c.lane / S::o.lpr;
-      if (c.lane % S::o.lpr == 0 && row < S::H) {
-        const float r = (l == 0 && embed_row) ? bf16_to_f32(embed_row[row])
-                                               : bf16_to_f32(ld_c16(a.h + row));
-        st_c16(a.h1 + row, f32_to_bf16(round_bf16(acc) + r));
-      }
-      publish(c, my_flag, ep + 3);
+      bool ok = true;
+      if (stager) ok = stage_wave<S::AO>(a, a.tattn, tag_of(ep + 2), nullptr, 0.0f, sm.xs[buf], nullptr);
+      if (!handoff(ok)) return;
     }
-    if (is_g) prefetch<S::g.lpr, S::g.nj, true>(pf, lw.gate_up, S::I, S::H, c.gw);
+    if (!stager) {
+      dot_group<S::o.lpr, S::o.nj, false, S::off_o>(pf, sm.xs[buf], S::AO, acc, accu);
+      st_c32(dst_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)));
+    }
+    if (is_o) buf ^= 1;
     // ---- G ----
     if (is_g) {
-      if (!wait_all(c, a.progress, no, ep + 3)) return;
-      stage_x<S::H>(c, a.h1, true, lw.post_norm, a.eps);
-      dot_group<S::g.lpr, S::g.nj, true>(pf, sm.xs, S::H, acc, accu);
-      const int row = c.gw * (64 / S::g.lpr) + c.lane / S::g.lpr;
-      if (c.lane % S::g.lpr == 0 && row < S::I)
-        st_c16(a.act + row, f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))));
-      publish(c, my_flag, ep + 4);
+      bool ok = true;
+      if (stager) ok = stage_wave<S::H>(a, a.th1, tag_of(ep + 3), lw.post_norm, a.eps, sm.xs[buf], sm.raw_h1);
+      if (!handoff(ok)) return;
     }
-    if (is_d) prefetch<S::d.lpr, S::d.nj, false>(pf, lw.down, S::H, S::I, c.gw);
+    if (!stager) {
+      dot_group<S::g.lpr, S::g.nj, true, S::off_g>(pf, sm.xs[buf], S::H, acc, accu);
+      st_c32(dst_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)));
+      prefetch<S::d.lpr, S::d.nj, false, S::off_d>(pf, lw.down, S::H, S::I, c.gw, is_d);
+      const bool more = l + 1 < L;
+      const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
+      prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, nx.qkv, S::QKV, S::H, c.gw, is_q && more);
+      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             rsrc(nx.qkv_bias, S::QKV * 4), bias_off, 0, 0));
+    }
+    if (is_g) buf ^= 1;
     // ---- D ----
     if (is_d) {
-      if (!wait_all(c, a.progress, ng, ep + 4)) return;
-      stage_x<S::I>(c, a.act, true, nullptr, 0.0f);
-      dot_group<S::d.lpr, S::d.nj, false>(pf, sm.xs, S::I, acc, accu);
-      const int row = c.gw * (64 / S::d.lpr) + c.lane / S::d.lpr;
-      if (c.lane % S::d.lpr == 0 && row < S::H)
-        st_c16(a.h + row, f32_to_bf16(round_bf16(acc) + bf16_to_f32(ld_c16(a.h1 + row))));
-      publish(c, my_flag, ep + 5);
+      bool ok = true;
+      if (stager) ok = stage_wave<S::I>(a, a.tact, tag_of(ep + 4), nullptr, 0.0f, sm.xs[buf], nullptr);
+      if (!handoff(ok)) return;
     }
-    if (l + 1 < L && is_q) prefetch<S::q.lpr, S::q.nj, false>(pf, a.w[l + 1].qkv, S::QKV, S::H, c.gw);
+    if (!stager) {
+      dot_group<S::d.lpr, S::d.nj, false, S::off_d>(pf, sm.xs[buf], S::I, acc, accu);
+      const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
+      st_c32(dst_d, tagged(y, tag_of(ep + 5)));
+      stg(dst_h, (uint16_t)y);  // plain copy: the final hidden for hk_engine_final_hidden
+    }
+    if (is_d) buf ^= 1;
   }
   const unsigned ep_layers = base + 5u * (unsigned)L;
   if (!a.head) {
@@ -566,39 +733,41 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     return;
   }
 
-  // ---- H: LM head over all waves, double-buffered row groups ----
+  // ---- H: LM head over all eight waves, double-buffered row groups; every
+  // wave runs the same (even) number of iterations, past-the-end groups read
+  // zero and store to the pad ----
   constexpr int HL = S::head_lpr, HNJ = S::head_nj, HRPW = 64 / HL;
   const int groups = (a.vocab + HRPW - 1) / HRPW;
   const int stride = kPersistentGrid * kPW;
+  const int iters = (groups + stride - 1) / stride;
+  float* const lpad = a.logits + a.vocab + c.wg * kPW + c.wave;
   u32x4 wb[kPf];
-  int grp = c.gw;
-  if (grp < groups) prefetch<HL, HNJ, false>(pf, a.lm_head, a.vocab, S::H, grp);
-  if (!wait_all(c, a.progress, nd, ep_layers)) return;
-  stage_x<S::H>(c, a.h, true, a.final_norm, a.eps);
+  int grp = c.wg * kPW + c.wave;
+  if (!stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
+  {
+    bool ok = true;
+    if (stager) ok = stage_wave<S::H>(a, a.th, tag_of(ep_layers), a.final_norm, a.eps, sm.xs[buf], nullptr);
+    if (!handoff(ok)) return;
+  }
+  if (stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
+  const float* xh = sm.xs[buf];
   unsigned long long best = 0ull;
   const int sub = c.lane / HL;
-  const bool lead = c.lane % HL == 0;
-  for (;;) {
-    if (grp >= groups) break;
-    int nxt = grp + stride;
-    if (nxt < groups) prefetch<HL, HNJ, false>(wb, a.lm_head, a.vocab, S::H, nxt);
-    dot_group<HL, HNJ, false>(pf, sm.xs, S::H, acc, accu);
-    int row = grp * HRPW + sub;
-    if (lead && row < a.vocab) {
-      a.logits[row] = acc;
-      best = umax64(best, argmax_key(acc, (uint32_t)row));
-    }
-    grp = nxt;
-    if (grp >= groups) break;
-    nxt = grp + stride;
-    if (nxt < groups) prefetch<HL, HNJ, false>(pf, a.lm_head, a.vocab, S::H, nxt);
-    dot_group<HL, HNJ, false>(wb, sm.xs, S::H, acc, accu);
-    row = grp * HRPW + sub;
-    if (lead && row < a.vocab) {
-      a.logits[row] = acc;
-      best = umax64(best, argmax_key(acc, (uint32_t)row));
-    }
-    grp = nxt;
+  auto finish = [&](int g) {
+    const int row = g * HRPW + sub;
+    const bool valid = row < a.vocab;
+    stg(valid ? a.logits + row : lpad, acc);
+    best = umax64(best, valid ? argmax_key(acc, (uint32_t)row) : 0ull);
+  };
+  for (int it = 0; it < iters; it += 2) {
+    prefetch<HL, HNJ, false, 0>(wb, a.lm_head, a.vocab, S::H, grp + stride, true);
+    dot_group<HL, HNJ, false, 0>(pf, xh, S::H, acc, accu);
+    finish(grp);
+    grp += stride;
+    prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp + stride, true);
+    dot_group<HL, HNJ, false, 0>(wb, xh, S::H, acc, accu);
+    finish(grp);
+    grp += stride;
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) best = umax64(best, shfl_xor_u64(best, m));
@@ -681,6 +850,7 @@ int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bo
 }
 
 int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream) {
+  if (a.layers <= 0 || a.layers > kPersistentMaxLayers) return fail("persistent step: layer count out of range");
   if (a.max_splits < (a.max_ctx + kChunk - 1) / kChunk) return fail("persistent step: partials too small");
   switch (shape) {
     case 0: return launch_shape<SmolShape>(a, stream);
