@@ -171,6 +171,9 @@ struct PShared {
   float raw_h1[kHMax];  // h1 before RMSNorm: residual of the down rows
   float red[2][kPW];
   unsigned long long keys[kPW];
+  uint32_t out_val[kCW * 16];  // a phase's tagged outputs, gathered for one store
+  unsigned out_count;          // compute-wave arrivals (7 per gathered phase)
+  unsigned out_stored;         // out_count value once the gathered store is issued
   int abort;
   int ticket;
 };
@@ -253,7 +256,17 @@ __device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigne
                            const uint16_t* gamma, float eps, float* xs, float* raw) {
   constexpr int CH = K / 4;  // 16-byte chunks of four tagged words
   constexpr int PER = (CH + 63) / 64;
+  constexpr int GPER = PER <= kBatch ? PER : 1;  // gamma words held across the poll
   const int lane = threadIdx.x & 63;
+  // gamma is constant: fetch it before polling so its latency overlaps the wait
+  uint2 gv[GPER];
+  if (gamma != nullptr && PER <= kBatch) {
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      const int ch = lane + 64 * j;
+      gv[j] = ch < CH ? ldg_u2(gamma + ch * 4) : make_uint2(0u, 0u);
+    }
+  }
   float ss = 0.0f;
 #pragma unroll
   for (int j0 = 0; j0 < PER; j0 += kBatch) {
@@ -296,12 +309,16 @@ __device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigne
   if (gamma != nullptr) {
     ss = group_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)K + eps);
-    for (int ch = lane; ch < CH; ch += 64) {
-      const uint2 g = ldg_u2(gamma + ch * 4);
-      xs[ch * 4 + 0] = round_bf16((xs[ch * 4 + 0] * inv) * bf_lo(g.x));
-      xs[ch * 4 + 1] = round_bf16((xs[ch * 4 + 1] * inv) * bf_hi(g.x));
-      xs[ch * 4 + 2] = round_bf16((xs[ch * 4 + 2] * inv) * bf_lo(g.y));
-      xs[ch * 4 + 3] = round_bf16((xs[ch * 4 + 3] * inv) * bf_hi(g.y));
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int ch = lane + 64 * j;
+      if (ch < CH) {
+        const uint2 g = PER <= kBatch ? gv[j < GPER ? j : 0] : ldg_u2(gamma + ch * 4);
+        xs[ch * 4 + 0] = round_bf16((xs[ch * 4 + 0] * inv) * bf_lo(g.x));
+        xs[ch * 4 + 1] = round_bf16((xs[ch * 4 + 1] * inv) * bf_hi(g.x));
+        xs[ch * 4 + 2] = round_bf16((xs[ch * 4 + 2] * inv) * bf_lo(g.y));
+        xs[ch * 4 + 3] = round_bf16((xs[ch * 4 + 3] * inv) * bf_hi(g.y));
+      }
     }
   }
   return true;
@@ -588,6 +605,50 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   return true;
 }
 
+// Publish one GEMV phase's outputs.  Each compute wave parks its rows'
+// tagged words in LDS; the last of the seven to arrive stores the workgroup's
+// rows (contiguous: kCW * RPW of them from `first`) with one instruction, so a
+// cache line of outputs has a few writers instead of one per wave -- that is
+// what makes it visible to the pollers quickly.  Every compute wave issues
+// exactly one global store here (the others to their pad word), which keeps
+// the compiler's wait counts exact.
+// With `then_load`, every wave of a producer workgroup then waits until the
+// gathered store has been issued before it goes on to issue weight loads:
+// the CU's memory pipeline is in order, so the store must not queue behind
+// tens of kilobytes of prefetch.
+template <int RPW>
+__device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t word, bool row_lead,
+                                             uint32_t* first, int valid_rows, uint32_t* pad,
+                                             bool then_load) {
+  static_assert(kCW * RPW <= kCW * 16, "gather buffer too small");
+  uint32_t* dst = pad;
+  uint32_t v = 0;
+  unsigned old = 0;
+  if (producer) {
+    const int sub = c.lane / (64 / RPW);
+    if (row_lead) c.sm->out_val[c.wave * RPW + sub] = word;
+    if (c.lane == 0) old = atomicAdd(&c.sm->out_count, 1u);
+    old = __shfl(old, 0, 64);
+    if (old % kCW == kCW - 1 && c.lane < kCW * RPW && c.lane < valid_rows) {
+      v = c.sm->out_val[c.lane];
+      dst = first + c.lane;
+    }
+  }
+  st_c32(dst, v);
+  if (!producer) return;
+  const unsigned done = old - old % kCW + kCW;
+  if (old % kCW == kCW - 1) {
+    if (c.lane == 0) __hip_atomic_store(&c.sm->out_stored, done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  } else if (then_load) {
+    // the last wave is at most a few hundred cycles behind; the bound only
+    // guards against an unforeseen schedule (ordering is a performance matter)
+    for (unsigned spins = 0; spins < (1u << 16); ++spins) {
+      if (__hip_atomic_load(&c.sm->out_stored, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == done) break;
+      __builtin_amdgcn_s_sleep(0);
+    }
+  }
+}
+
 // ---- the step kernel ----
 template <class S>
 __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
@@ -600,7 +661,11 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   c.lane = threadIdx.x & 63;
   c.gw = c.wg * kCW + c.wave;
   const bool stager = c.wave == kCW;
-  if (threadIdx.x == 0) sm.abort = 0;
+  if (threadIdx.x == 0) {
+    sm.abort = 0;
+    sm.out_count = 0;
+    sm.out_stored = 0;
+  }
 
   const PersistentArgs& a = args;
   const int L = a.layers;
@@ -629,10 +694,12 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   const int row_o = c.gw * (64 / S::o.lpr) + c.lane / S::o.lpr;
   const int row_g = c.gw * (64 / S::g.lpr) + c.lane / S::g.lpr;
   const int row_d = c.gw * (64 / S::d.lpr) + c.lane / S::d.lpr;
-  uint32_t* const dst_q = is_q && row_q < S::QKV ? a.tqkv + row_q : pad;
-  uint32_t* const dst_o = is_o && row_o < S::H ? a.th1 + row_o : pad;
-  uint32_t* const dst_g = is_g && row_g < S::I ? a.tact + row_g : pad;
-  uint32_t* const dst_d = is_d && row_d < S::H ? a.th + row_d : pad;
+  // first row of this workgroup in each phase and how many of its rows exist
+  constexpr int RQ = 64 / S::q.lpr, RO = 64 / S::o.lpr, RG = 64 / S::g.lpr, RD = 64 / S::d.lpr;
+  const int fq = c.wg * kCW * RQ, fo = c.wg * kCW * RO, fg = c.wg * kCW * RG, fd = c.wg * kCW * RD;
+  const int nvq = S::QKV - fq, nvo = S::H - fo, nvg = S::I - fg, nvd = S::H - fd;
+  const bool lq = c.lane % S::q.lpr == 0, lo = c.lane % S::o.lpr == 0;
+  const bool lg = c.lane % S::g.lpr == 0, ld = c.lane % S::d.lpr == 0;
   uint16_t* const dst_h = is_d && row_d < S::H ? a.h + row_d : reinterpret_cast<uint16_t*>(pad);
   const int res_o = min(row_o, S::H - 1), res_d = min(row_d, S::H - 1);
   const unsigned bias_off = is_q && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
@@ -671,7 +738,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     if (!stager) {
       dot_group<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.xs[buf], S::H, acc, accu);
       const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
-      st_c32(dst_q, tagged(y, tag_of(ep + 1)));
+      publish_rows<RQ>(c, is_q, tagged(y, tag_of(ep + 1)), lq, a.tqkv + fq, nvq, pad, true);
     }
     if (is_q) buf ^= 1;
     // ---- A ---- (tasks go to the highest workgroups, which own no Q rows;
@@ -693,7 +760,8 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     }
     if (!stager) {
       dot_group<S::o.lpr, S::o.nj, false, S::off_o>(pf, sm.xs[buf], S::AO, acc, accu);
-      st_c32(dst_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)));
+      publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
+                       lo, a.th1 + fo, nvo, pad, false);
     }
     if (is_o) buf ^= 1;
     // ---- G ----
@@ -704,7 +772,8 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     }
     if (!stager) {
       dot_group<S::g.lpr, S::g.nj, true, S::off_g>(pf, sm.xs[buf], S::H, acc, accu);
-      st_c32(dst_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)));
+      publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
+                       lg, a.tact + fg, nvg, pad, true);
       prefetch<S::d.lpr, S::d.nj, false, S::off_d>(pf, lw.down, S::H, S::I, c.gw, is_d);
       const bool more = l + 1 < L;
       const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
@@ -722,7 +791,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     if (!stager) {
       dot_group<S::d.lpr, S::d.nj, false, S::off_d>(pf, sm.xs[buf], S::I, acc, accu);
       const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
-      st_c32(dst_d, tagged(y, tag_of(ep + 5)));
+      publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, a.th + fd, nvd, pad, false);
       stg(dst_h, (uint16_t)y);  // plain copy: the final hidden for hk_engine_final_hidden
     }
     if (is_d) buf ^= 1;
