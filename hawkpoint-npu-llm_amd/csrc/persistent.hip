@@ -107,6 +107,46 @@ __device__ __forceinline__ unsigned tag_of(unsigned e) { return e % 65535u + 1u;
 
 __device__ __forceinline__ uint32_t tagged(uint32_t bf16, unsigned tag) { return (tag << 16) | bf16; }
 
+// ---- cross-lane sums with DPP ----
+// Within a 16-lane row DPP moves take a few cycles, against an LDS round trip
+// for ds_bpermute (what __shfl_xor compiles to).  Steps: swap neighbours
+// (quad_perm 1,0,3,2), swap pairs (2,3,0,1), then pair quads (half-row mirror)
+// and halves (row mirror); each step adds lanes holding equal partial sums,
+// so every lane of the group ends with the same total.  Rows are joined with
+// two shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_plus(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+  return v + __builtin_bit_cast(float, moved);
+}
+
+template <int W>
+__device__ __forceinline__ float wave_sum(float v) {
+  static_assert(W == 16 || W == 32 || W == 64, "row-multiple widths only");
+  v = dpp_plus<0xb1>(v);   // quad_perm 1,0,3,2
+  v = dpp_plus<0x4e>(v);   // quad_perm 2,3,0,1
+  v = dpp_plus<0x141>(v);  // row_half_mirror
+  v = dpp_plus<0x140>(v);  // row_mirror
+  if (W >= 32) v += __shfl_xor(v, 16, 64);
+  if (W >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+  return fmaxf(v, __builtin_bit_cast(float, moved));
+}
+
+__device__ __forceinline__ float wave_max64(float v) {
+  v = dpp_max<0xb1>(v);
+  v = dpp_max<0x4e>(v);
+  v = dpp_max<0x141>(v);
+  v = dpp_max<0x140>(v);
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
 // ---- phase shapes ----
 struct PhaseCfg {
   int lpr, nj;
@@ -166,7 +206,10 @@ struct PShared {
   // layer table: read from LDS, since a global read of it would make the
   // wave wait for all its outstanding loads and stores first
   PersistentLayer layers[kPersistentMaxLayers];
-  float xs[2][kXMax];   // staged GEMV inputs (alternating); attention scratch in xs[0]
+  // staged GEMV inputs as bf16 (alternating buffers); attention scratch in xs[0].
+  // Every staged x is bf16-exact (activations, or RMSNorm output rounded to
+  // bf16), so a 16-byte LDS read carries 8 of them.
+  uint16_t xs[2][kXMax];
   float raw_h[kHMax];   // layer input h before RMSNorm: residual of the O rows
   float raw_h1[kHMax];  // h1 before RMSNorm: residual of the down rows
   float red[2][kPW];
@@ -251,16 +294,18 @@ __device__ __forceinline__ void publish(Ctx& c, unsigned* flag, unsigned epoch) 
 // values to `raw` when given.  Runs on one wave; false when abandoned.
 constexpr int kBatch = 10;
 
-template <int K>
+template <int K, bool NORM>
 __device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigned tag,
-                           const uint16_t* gamma, float eps, float* xs, float* raw) {
+                           const uint16_t* gamma, float eps, uint16_t* xs, float* raw) {
   constexpr int CH = K / 4;  // 16-byte chunks of four tagged words
   constexpr int PER = (CH + 63) / 64;
   constexpr int GPER = PER <= kBatch ? PER : 1;  // gamma words held across the poll
   const int lane = threadIdx.x & 63;
+  // normalised inputs are staged in one batch, so their words stay in registers
+  static_assert(!NORM || PER <= kBatch, "RMSNorm input longer than one stager batch");
   // gamma is constant: fetch it before polling so its latency overlaps the wait
   uint2 gv[GPER];
-  if (gamma != nullptr && PER <= kBatch) {
+  if (NORM) {
 #pragma unroll
     for (int j = 0; j < GPER; ++j) {
       const int ch = lane + 64 * j;
@@ -300,24 +345,27 @@ __device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigne
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           ss += f[q] * f[q];
-          xs[ch * 4 + q] = f[q];
           if (raw != nullptr) raw[ch * 4 + q] = f[q];
         }
+        if (!NORM)
+          *reinterpret_cast<uint2*>(xs + ch * 4) =
+              make_uint2((v[j].x & 0xffffu) | (v[j].y << 16), (v[j].z & 0xffffu) | (v[j].w << 16));
       }
     }
-  }
-  if (gamma != nullptr) {
-    ss = group_sum<64>(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    if constexpr (NORM) {
+      ss = wave_sum<64>(ss);
+      const float inv = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int ch = lane + 64 * j;
-      if (ch < CH) {
-        const uint2 g = PER <= kBatch ? gv[j < GPER ? j : 0] : ldg_u2(gamma + ch * 4);
-        xs[ch * 4 + 0] = round_bf16((xs[ch * 4 + 0] * inv) * bf_lo(g.x));
-        xs[ch * 4 + 1] = round_bf16((xs[ch * 4 + 1] * inv) * bf_hi(g.x));
-        xs[ch * 4 + 2] = round_bf16((xs[ch * 4 + 2] * inv) * bf_lo(g.y));
-        xs[ch * 4 + 3] = round_bf16((xs[ch * 4 + 3] * inv) * bf_hi(g.y));
+      for (int j = 0; j < B; ++j) {
+        const int ch = lane + 64 * j;
+        if (j < PER && ch < CH) {
+          const uint2 g = gv[j < GPER ? j : 0];
+          const uint32_t n0 = f32_to_bf16((bf_lo(v[j].x) * inv) * bf_lo(g.x));
+          const uint32_t n1 = f32_to_bf16((bf_lo(v[j].y) * inv) * bf_hi(g.x));
+          const uint32_t n2 = f32_to_bf16((bf_lo(v[j].z) * inv) * bf_lo(g.y));
+          const uint32_t n3 = f32_to_bf16((bf_lo(v[j].w) * inv) * bf_hi(g.y));
+          *reinterpret_cast<uint2*>(xs + ch * 4) = make_uint2(n0 | (n1 << 16), n2 | (n3 << 16));
+        }
       }
     }
   }
@@ -326,8 +374,8 @@ __device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigne
 
 // Stager for plain bf16 input written before the launch (layer 0).
 template <int K>
-__device__ void stage_wave_plain(const uint16_t* src, const uint16_t* gamma, float eps, float* xs,
-                                 float* raw) {
+__device__ void stage_wave_plain(const uint16_t* src, const uint16_t* gamma, float eps,
+                                 uint16_t* xs, float* raw) {
   constexpr int CH = K / 4;
   const int lane = threadIdx.x & 63;
   float ss = 0.0f;
@@ -338,18 +386,19 @@ __device__ void stage_wave_plain(const uint16_t* src, const uint16_t* gamma, flo
     for (int q = 0; q < 4; ++q) {
       ss += f[q] * f[q];
       raw[ch * 4 + q] = f[q];
-      xs[ch * 4 + q] = f[q];
     }
+    *reinterpret_cast<uint2*>(xs + ch * 4) = w;
   }
   if (gamma == nullptr) return;
-  ss = group_sum<64>(ss);
+  ss = wave_sum<64>(ss);
   const float inv = 1.0f / sqrtf(ss / (float)K + eps);
   for (int ch = lane; ch < CH; ch += 64) {
     const uint2 g = ldg_u2(gamma + ch * 4);
-    xs[ch * 4 + 0] = round_bf16((xs[ch * 4 + 0] * inv) * bf_lo(g.x));
-    xs[ch * 4 + 1] = round_bf16((xs[ch * 4 + 1] * inv) * bf_hi(g.x));
-    xs[ch * 4 + 2] = round_bf16((xs[ch * 4 + 2] * inv) * bf_lo(g.y));
-    xs[ch * 4 + 3] = round_bf16((xs[ch * 4 + 3] * inv) * bf_hi(g.y));
+    const uint32_t n0 = f32_to_bf16((raw[ch * 4 + 0] * inv) * bf_lo(g.x));
+    const uint32_t n1 = f32_to_bf16((raw[ch * 4 + 1] * inv) * bf_hi(g.x));
+    const uint32_t n2 = f32_to_bf16((raw[ch * 4 + 2] * inv) * bf_lo(g.y));
+    const uint32_t n3 = f32_to_bf16((raw[ch * 4 + 3] * inv) * bf_hi(g.y));
+    *reinterpret_cast<uint2*>(xs + ch * 4) = make_uint2(n0 | (n1 << 16), n2 | (n3 << 16));
   }
 }
 
@@ -383,23 +432,23 @@ __device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const uint16_t* W, in
   }
 }
 
-__device__ __forceinline__ void fma8(const u32x4 w, const float* xs, int ch, float& a0, float& a1) {
-  const float4* xv = reinterpret_cast<const float4*>(xs + ch * 8);
-  const float4 p = xv[0], q = xv[1];
-  a0 = fmaf(bf_lo(w.x), p.x, a0);
-  a1 = fmaf(bf_hi(w.x), p.y, a1);
-  a0 = fmaf(bf_lo(w.y), p.z, a0);
-  a1 = fmaf(bf_hi(w.y), p.w, a1);
-  a0 = fmaf(bf_lo(w.z), q.x, a0);
-  a1 = fmaf(bf_hi(w.z), q.y, a1);
-  a0 = fmaf(bf_lo(w.w), q.z, a0);
-  a1 = fmaf(bf_hi(w.w), q.w, a1);
+__device__ __forceinline__ void fma8(const u32x4 w, const uint16_t* xs, int ch, float& a0,
+                                     float& a1) {
+  const u32x4 x = *reinterpret_cast<const u32x4*>(xs + ch * 8);
+  a0 = fmaf(bf_lo(w.x), bf_lo(x.x), a0);
+  a1 = fmaf(bf_hi(w.x), bf_hi(x.x), a1);
+  a0 = fmaf(bf_lo(w.y), bf_lo(x.y), a0);
+  a1 = fmaf(bf_hi(w.y), bf_hi(x.y), a1);
+  a0 = fmaf(bf_lo(w.z), bf_lo(x.z), a0);
+  a1 = fmaf(bf_hi(w.z), bf_hi(x.z), a1);
+  a0 = fmaf(bf_lo(w.w), bf_lo(x.w), a0);
+  a1 = fmaf(bf_hi(w.w), bf_hi(x.w), a1);
 }
 
 // Dot products of the prefetched row group with the staged x; every lane of
 // the row's LPR lanes ends with the sums.
 template <int LPR, int NJ, bool PAIR, int OFF>
-__device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const float* xs, int K,
+__device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t* xs, int K,
                                           float& acc, float& accu) {
   const int l = (threadIdx.x & 63) % LPR;
   const int CH = K / 8;
@@ -412,8 +461,13 @@ __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const float* x
       if constexpr (PAIR) fma8(pf[OFF + NJ + j], xs, ch, b0, b1);
     }
   }
-  acc = group_sum<LPR>(a0 + a1);
-  accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
+  if constexpr (LPR >= 16) {
+    acc = wave_sum<LPR>(a0 + a1);
+    accu = PAIR ? wave_sum<LPR>(b0 + b1) : 0.0f;
+  } else {
+    acc = group_sum<LPR>(a0 + a1);
+    accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
+  }
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -433,7 +487,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   const int nsplit = p / kChunk + 1;
   const bool holds_new = (s == nsplit - 1);
   const int tid = threadIdx.x;
-  float* qs = c.sm->xs[0];              // [64]
+  float* qs = reinterpret_cast<float*>(c.sm->xs[0]);  // [64]
   float* knew = qs + kHeadDim;          // [64]
   float* pr = knew + kHeadDim;          // [kChunk]
   float* acc = pr + kChunk;             // [kGroupsPV][64]
@@ -507,9 +561,18 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   {
     const float* qh = qs + half * kHalf;
     if (slot == p) {
-      const float* kh = knew + half * kHalf;
-      for (int d = 0; d < kHalf; ++d) dot = fmaf(qh[d], kh[d], dot);
-    } else {
+      // the new key (bf16 values held as f32) packed like a cached row
+      const float4* kh = reinterpret_cast<const float4*>(knew + half * kHalf);
+#pragma unroll
+      for (int ch = 0; ch < kHeadDim / 16; ++ch) {
+        const float4 a0 = kh[2 * ch], a1 = kh[2 * ch + 1];
+        krow[ch] = u32x4{(__float_as_uint(a0.x) >> 16) | (__float_as_uint(a0.y) & 0xffff0000u),
+                         (__float_as_uint(a0.z) >> 16) | (__float_as_uint(a0.w) & 0xffff0000u),
+                         (__float_as_uint(a1.x) >> 16) | (__float_as_uint(a1.y) & 0xffff0000u),
+                         (__float_as_uint(a1.z) >> 16) | (__float_as_uint(a1.w) & 0xffff0000u)};
+      }
+    }
+    {
 #pragma unroll
       for (int ch = 0; ch < kHeadDim / 16; ++ch) {
         // eight q values per step: keeps the LDS reads from being hoisted
@@ -531,14 +594,14 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   dot += __shfl_xor(dot, 1, 64);  // the two halves of the slot
   const bool live = si < n;
   const float sc = live ? dot * scale : -INFINITY;
-  float m = group_max<64>(sc);
+  float m = wave_max64(sc);
   if (c.lane == 0) c.sm->red[0][c.wave] = m;
   __syncthreads();
   m = c.sm->red[0][0];
 #pragma unroll
   for (int w = 1; w < kPW; ++w) m = fmaxf(m, c.sm->red[0][w]);
   const float e = live ? expf(sc - m) : 0.0f;
-  float sum = group_sum<64>(half == 0 ? e : 0.0f);  // each slot once
+  float sum = wave_sum<64>(half == 0 ? e : 0.0f);  // each slot once
   if (c.lane == 0) c.sm->red[1][c.wave] = sum;
   __syncthreads();
   sum = c.sm->red[1][0];
@@ -731,7 +794,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
         if (l == 0)
           stage_wave_plain<S::H>(x0, lw.in_norm, a.eps, sm.xs[buf], sm.raw_h);
         else
-          ok = stage_wave<S::H>(a, a.th, tag_of(ep), lw.in_norm, a.eps, sm.xs[buf], sm.raw_h);
+          ok = stage_wave<S::H, true>(a, a.th, tag_of(ep), lw.in_norm, a.eps, sm.xs[buf], sm.raw_h);
       }
       if (!handoff(ok)) return;
     }
@@ -755,7 +818,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     // ---- O ----
     if (is_o) {
       bool ok = true;
-      if (stager) ok = stage_wave<S::AO>(a, a.tattn, tag_of(ep + 2), nullptr, 0.0f, sm.xs[buf], nullptr);
+      if (stager) ok = stage_wave<S::AO, false>(a, a.tattn, tag_of(ep + 2), nullptr, 0.0f, sm.xs[buf], nullptr);
       if (!handoff(ok)) return;
     }
     if (!stager) {
@@ -767,7 +830,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     // ---- G ----
     if (is_g) {
       bool ok = true;
-      if (stager) ok = stage_wave<S::H>(a, a.th1, tag_of(ep + 3), lw.post_norm, a.eps, sm.xs[buf], sm.raw_h1);
+      if (stager) ok = stage_wave<S::H, true>(a, a.th1, tag_of(ep + 3), lw.post_norm, a.eps, sm.xs[buf], sm.raw_h1);
       if (!handoff(ok)) return;
     }
     if (!stager) {
@@ -785,7 +848,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     // ---- D ----
     if (is_d) {
       bool ok = true;
-      if (stager) ok = stage_wave<S::I>(a, a.tact, tag_of(ep + 4), nullptr, 0.0f, sm.xs[buf], nullptr);
+      if (stager) ok = stage_wave<S::I, false>(a, a.tact, tag_of(ep + 4), nullptr, 0.0f, sm.xs[buf], nullptr);
       if (!handoff(ok)) return;
     }
     if (!stager) {
@@ -815,11 +878,11 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   if (!stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
   {
     bool ok = true;
-    if (stager) ok = stage_wave<S::H>(a, a.th, tag_of(ep_layers), a.final_norm, a.eps, sm.xs[buf], nullptr);
+    if (stager) ok = stage_wave<S::H, true>(a, a.th, tag_of(ep_layers), a.final_norm, a.eps, sm.xs[buf], nullptr);
     if (!handoff(ok)) return;
   }
   if (stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
-  const float* xh = sm.xs[buf];
+  const uint16_t* xh = sm.xs[buf];
   unsigned long long best = 0ull;
   const int sub = c.lane / HL;
   auto finish = [&](int g) {
