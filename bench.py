@@ -11,10 +11,12 @@ tokens" protocol.  One step = one decode token: every layer, the final norm,
 the LM head and the argmax, with weights and KV resident in HBM.
 
 value = timed steps / wall seconds between two stream synchronisations.
-roofline: the kernel with the largest share of a step, timed with HIP events
-on the engine's stream over launches that rotate through all 24 layers'
-weights (419 MB for gate/up, more than the 256 MB Infinity Cache), against
-the MI355X's 8 TB/s HBM peak.
+roofline: the decode-step kernel -- one persistent launch runs the whole step
+(all 24 layers, the LM head and the argmax) -- timed with HIP events on the
+engine's stream over a graph of back-to-back step launches; achieved = the
+step's algorithmic bytes (988 MB of weights plus KV) / its duration, against
+the MI355X's 8 TB/s HBM peak.  The per-kernel path (one GEMV or attention
+kernel per part, used for int8 weights and other shapes) is timed too.
 cpu_baseline: the oracle (NumPy BF16 CPU restatement of the reference's CPU
 runtime) on a bounded sample of the same workload.
 """
@@ -162,24 +164,23 @@ def from_bf16(bits):
     return from_bits(bits)
 
 
-def probe(engine, meta, launches):
+def probe(engine, meta, launches, position):
     """Workload for the rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE): the
-    dominant kernel (gate/up GEMV, rotating through every layer's weights)
-    and, as the calibration of the counters, device-to-device copies of a
-    known size (256 MiB read + 256 MiB written per copy)."""
+    decode-step kernel, launched one step at a time at the last decode
+    position, and, as the calibration of the counters, device-to-device copies
+    of a known size (256 MiB read + 256 MiB written per copy)."""
     from runtime import hip
 
     lib = hip.lib()
-    layers = meta["layers"]
-    for i in range(launches):
-        hip.check(lib.hk_engine_launch_part(engine._engine, hip.PARTS["gate_up"], i % layers), "launch")
+    for _ in range(launches):
+        hip.check(lib.hk_engine_launch_part(engine._engine, hip.PART_STEP, 0), "launch")
     hip.check(lib.hk_stream_sync(engine.stream), "sync")
     src, dst = hip.DeviceBuffer(COPY_BYTES), hip.DeviceBuffer(COPY_BYTES)
     src.zero()
     for _ in range(4):
         hip.check(lib.hk_memcpy_d2d(dst.ptr, src.ptr, COPY_BYTES), "copy")
-    print(json.dumps({"probe": "gate_up", "launches": launches,
-                      "bytes_per_launch": part_bytes(meta, "gate_up"), "copy_bytes": COPY_BYTES}))
+    print(json.dumps({"probe": "decode_step", "launches": launches, "position": position,
+                      "bytes_per_launch": step_bytes(meta, position), "copy_bytes": COPY_BYTES}))
 
 
 def main():
@@ -190,10 +191,12 @@ def main():
     ap.add_argument("--kernel-launches", type=int, default=240)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
+    ap.add_argument("--no-parts", action="store_true",
+                    help="skip the graph-replayed step and per-part timing (for profiler runs)")
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--probe", action="store_true",
-                    help="only the counter-calibration workload: launches of the gate/up "
-                    "GEMV over all layers, then 4 device copies of 256 MiB")
+                    help="only the counter-calibration workload: decode-step launches, then "
+                    "4 device copies of 256 MiB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -230,7 +233,7 @@ def main():
 
     first = prefill_per_position()  # captures both graphs
     if args.probe:
-        probe(engine, meta, args.kernel_launches)
+        probe(engine, meta, args.kernel_launches, PROMPT - 1)
         return
     first_pp, ttft_pp = timed(prefill_per_position, 3)
     first, ttft = timed(lambda: engine.prefill(prompt, 0, want_logits_array=False)[0])
@@ -260,24 +263,36 @@ def main():
     step_gbs = step_bytes(meta, mean_pos) / (ms_step * 1e-3) / 1e9
     log(f"decode: {tok_s:.1f} tok/s, {ms_step * 1e3:.1f} us/step, {step_gbs:.0f} GB/s whole step")
 
-    # per-part kernel times (HIP events on the engine stream)
+    stream = engine.stream
+    end_pos = PROMPT + RUN  # ctrl position after the last timed run
+    # the decode-step kernel: a graph of back-to-back step launches at the
+    # last position (no token feedback), timed with HIP events on its stream
+    n = args.kernel_launches
+    if args.no_parts:  # profiler runs: no graph replays; the step's wall time stands in
+        step_kernel_us = ms_step * 1e3
+    else:
+        ev0, ev1 = hip.Event(), hip.Event()
+        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
+        ev0.record(stream)
+        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
+        ev1.record(stream)
+        step_kernel_us = ev0.elapsed_ms(ev1) * 1e3 / n
+    dom_bytes = step_bytes(meta, end_pos)
+    achieved = dom_bytes / (step_kernel_us * 1e-6) / 1e9
+    log(f"decode-step kernel: {step_kernel_us:.1f} us/launch, {achieved:.0f} GB/s")
+
+    # the per-kernel path, part by part (graph of launches over all layers)
     parts = {}
     layers = meta["layers"]
-    stream = engine.stream
-    for name, part in hip.PARTS.items():
-        n = args.kernel_launches
-        ev0, ev1 = hip.Event(), hip.Event()
-        # one captured graph of n launches (layer i % 24), replayed once to warm
-        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, part, n), "launch_part_repeat")
-        ev0.record(stream)
-        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, part, n), "launch_part_repeat")
-        ev1.record(stream)
-        parts[name] = ev0.elapsed_ms(ev1) * 1e3 / n
-    per_step = {k: v * (1 if k == "lm_head" else layers) for k, v in parts.items()}
-    dominant = max((k for k in per_step if part_bytes(meta, k)), key=per_step.get)
-    dom_bytes = part_bytes(meta, dominant)
-    achieved = dom_bytes / (parts[dominant] * 1e-6) / 1e9
-    log("kernel us/launch: " + ", ".join(f"{k} {v:.2f}" for k, v in parts.items()))
+    if not args.no_parts:
+        for name, part in hip.PARTS.items():
+            e0, e1 = hip.Event(), hip.Event()
+            hip.check(lib.hk_engine_launch_part_repeat(engine._engine, part, n), "launch_part_repeat")
+            e0.record(stream)
+            hip.check(lib.hk_engine_launch_part_repeat(engine._engine, part, n), "launch_part_repeat")
+            e1.record(stream)
+            parts[name] = e0.elapsed_ms(e1) * 1e3 / n
+        log("per-kernel path us/launch: " + ", ".join(f"{k} {v:.2f}" for k, v in parts.items()))
 
     # context 4096: a 4064-token prompt in one batched prefill, then 31 greedy
     # decode steps at positions 4064..4094
@@ -294,7 +309,7 @@ def main():
         f"({long_flops / t_long / 1e12:.1f} TFLOP/s), decode {long_decode:.1f} tok/s")
     engine.close()
     traffic = None
-    tfile = ROOT / "profiles" / f"traffic_{dominant}_qwen05b.json"
+    tfile = ROOT / "profiles" / "traffic_decode_step_qwen05b.json"
     if tfile.is_file():
         # HBM bytes per launch from the committed rocprofv3 --pmc runs
         traffic = json.loads(tfile.read_text()).get("traffic_bytes_per_launch")
@@ -340,10 +355,12 @@ def main():
         "step_hbm_gbs": round(step_gbs, 1),
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "step_bytes": int(step_bytes(meta, mean_pos)),
-        "kernel_us": {k: round(v, 3) for k, v in parts.items()},
+        "step_kernel_us": round(step_kernel_us, 2),
+        "per_kernel_path_us": {k: round(v, 3) for k, v in parts.items()},
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{dominant} GEMV (bytes/launch {dom_bytes})",
+            "kernel": f"decode_step_kernel, one launch per token (bytes/launch {dom_bytes} at "
+            f"position {end_pos})",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -157,6 +157,7 @@ struct hk_engine {
   // whole step in one persistent launch (persistent.hip); -1: per-kernel graph
   int pshape = -1;
   PersistentLayer* players = nullptr;  // device copy of the layer pointers
+  unsigned int spin_limit = kPersistentSpinLimit;
   unsigned int* psync = nullptr;       // per-workgroup epochs
   uint32_t* ptag = nullptr;            // tagged activations: h, h1, qkv, attn, act
   hipGraphExec_t graph[2] = {nullptr, nullptr};
@@ -319,6 +320,7 @@ int launch_persistent(hk_engine* e, bool head) {
   a.result = e->result;
   a.progress = e->psync;
   a.error = reinterpret_cast<unsigned int*>(e->result + 1);
+  a.spin_limit = e->spin_limit;
   return launch_persistent_step(e->pshape, a, e->stream);
 }
 
@@ -612,6 +614,10 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     const char* pers = getenv("HK_PERSISTENT");
     if (!(pers && pers[0] == '0') && d.layers <= kPersistentMaxLayers)
       e->pshape = persistent_shape(d.hidden, d.intermediate, d.q_heads, d.kv_heads, w8);
+    // polls a persistent-step wait may take before the launch is abandoned
+    // (a small value forces the abandon path, for tests of it)
+    if (const char* spin = getenv("HK_PERSISTENT_SPIN"))
+      e->spin_limit = (unsigned int)strtoul(spin, nullptr, 10);
     if (e->pshape >= 0) {
       std::vector<PersistentLayer> pl(d.layers);
       for (int l = 0; l < d.layers; ++l) {
@@ -749,27 +755,33 @@ int hk_engine_final_hidden(hk_engine* e, uint16_t* hidden_host) {
 int hk_engine_launch_part(hk_engine* e, int32_t part, int32_t layer) {
   if (!e) return fail("hk_engine_launch_part: null engine");
   std::lock_guard<std::mutex> lock(e->mu);
-  if (part < HK_PART_QKV || part > HK_PART_HEAD) return fail("hk_engine_launch_part: unknown part");
+  if (part < HK_PART_QKV || part > HK_PART_STEP) return fail("hk_engine_launch_part: unknown part");
   if (layer < 0 || layer >= e->d.layers) return fail("hk_engine_launch_part: layer out of range");
   HK_CHECK(hipSetDevice(e->device));
-  if (part == HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
+  if (part >= HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
+  if (part == HK_PART_STEP) return run_step(e, true);
   return launch_part(e, part, layer);
 }
 
 int hk_engine_launch_part_repeat(hk_engine* e, int32_t part, int32_t count) {
   if (!e) return fail("hk_engine_launch_part_repeat: null engine");
   std::lock_guard<std::mutex> lock(e->mu);
-  if (part < HK_PART_QKV || part > HK_PART_HEAD) return fail("hk_engine_launch_part_repeat: unknown part");
+  if (part < HK_PART_QKV || part > HK_PART_STEP) return fail("hk_engine_launch_part_repeat: unknown part");
   if (count <= 0 || count > 100000) return fail("hk_engine_launch_part_repeat: count out of range");
   HK_CHECK(hipSetDevice(e->device));
-  if (part == HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
+  if (part >= HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
   const long long key = (long long)part << 32 | (unsigned)count;
   auto it = e->repeat_graphs.find(key);
   if (it == e->repeat_graphs.end()) {
     hipGraph_t graph = nullptr;
     HK_CHECK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
     int rc = 0;
-    for (int i = 0; i < count && rc == 0; ++i) rc = launch_part(e, part, i % e->d.layers);
+    for (int i = 0; i < count && rc == 0; ++i) {
+      if (part != HK_PART_STEP)
+        rc = launch_part(e, part, i % e->d.layers);
+      else
+        rc = e->pshape >= 0 ? launch_persistent(e, true) : enqueue_step(e, true);
+    }
     const hipError_t end = hipStreamEndCapture(e->stream, &graph);
     if (rc != 0) {
       if (graph) (void)hipGraphDestroy(graph);

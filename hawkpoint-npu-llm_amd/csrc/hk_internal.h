@@ -143,7 +143,10 @@ struct PersistentArgs {
   int32_t* result;
   unsigned int* progress;  // [kPersistentGrid * kFlagStride] last epoch per workgroup
   unsigned int* error;     // nonzero: a wait timed out; the launch was abandoned
+  unsigned int spin_limit; // polls before a wait is abandoned
 };
+
+constexpr unsigned kPersistentSpinLimit = 1u << 20;
 
 // Model shapes the persistent step is compiled for (-1: use the per-kernel step).
 int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bool w8);

@@ -35,7 +35,7 @@
 // * Cross-workgroup data is written and read with device-coherent (sc1)
 //   accesses: the eight XCDs have separate L2 caches, and sc1 accesses bypass
 //   their incoherent state without whole-cache write-back or invalidate fences.
-// * Every wait is bounded: after kSpinLimit polls, or once another workgroup
+// * Every wait is bounded: after spin_limit polls, or once another workgroup
 //   has flagged an error, the workgroup records the error and leaves; all
 //   later waits then end at once, so the launch always drains.  The host
 //   reports the error and clears the tags and flags.
@@ -57,7 +57,6 @@ constexpr int kChunk = kPersistentChunk;  // attention slots per task
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kGroupsPV = kPT / kHalf;    // slot groups of the P @ V loop
 constexpr int kPartStride = kHeadDim + 2;
-constexpr unsigned kSpinLimit = 1u << 20;  // polls before a wait is abandoned
 constexpr int kSc1 = 16;                  // buffer-load cache policy: device scope (sc1)
 static_assert(2 * kChunk == kPT, "two threads per attention slot");
 
@@ -242,7 +241,7 @@ __device__ bool poll_word(const PersistentArgs& a, const uint32_t* p, unsigned t
       out = w;
       return true;
     }
-    if ((spins & 63u) == 0u && (ld_c32(a.error) != 0u || spins > kSpinLimit)) return give_up(a);
+    if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -254,7 +253,7 @@ __device__ bool poll_chunk(const PersistentArgs& a, const uint32_t* base, int by
     v = ld_c128(base, bytes, off);
     if ((v.x >> 16) == tag && (v.y >> 16) == tag && (v.z >> 16) == tag && (v.w >> 16) == tag)
       return true;
-    if ((spins & 63u) == 0u && (ld_c32(a.error) != 0u || spins > kSpinLimit)) return give_up(a);
+    if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -268,7 +267,7 @@ __device__ bool wait_all(Ctx& c, const unsigned* flags, int n, unsigned target) 
       bool ok = true;
       for (int i = c.lane; i < n; i += 64) ok = ok && reached(ld_c32(flags + (size_t)i * kFlagStride), target);
       if (__all(ok)) break;
-      if ((spins & 63u) == 0u && (ld_c32(c.a->error) != 0u || spins > kSpinLimit)) {
+      if (spins > c.a->spin_limit || ((spins & 63u) == 0u && ld_c32(c.a->error) != 0u)) {
         abort = 1;
         if (c.lane == 0) give_up(*c.a);
         break;
@@ -334,7 +333,7 @@ __device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigne
             (v[j].z >> 16) == tag && (v[j].w >> 16) == tag)
           pending &= ~(1u << j);
       if (!__any(pending != 0u)) break;
-      if ((spins & 63u) == 0u && (ld_c32(a.error) != 0u || spins > kSpinLimit)) return give_up(a);
+      if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
       __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
@@ -432,9 +431,7 @@ __device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const uint16_t* W, in
   }
 }
 
-__device__ __forceinline__ void fma8(const u32x4 w, const uint16_t* xs, int ch, float& a0,
-                                     float& a1) {
-  const u32x4 x = *reinterpret_cast<const u32x4*>(xs + ch * 8);
+__device__ __forceinline__ void fma8(const u32x4 w, const u32x4 x, float& a0, float& a1) {
   a0 = fmaf(bf_lo(w.x), bf_lo(x.x), a0);
   a1 = fmaf(bf_hi(w.x), bf_hi(x.x), a1);
   a0 = fmaf(bf_lo(w.y), bf_lo(x.y), a0);
@@ -446,20 +443,27 @@ __device__ __forceinline__ void fma8(const u32x4 w, const uint16_t* xs, int ch, 
 }
 
 // Dot products of the prefetched row group with the staged x; every lane of
-// the row's LPR lanes ends with the sums.
+// the row's LPR lanes ends with the sums.  All x chunks are read from LDS
+// first (a chunk past the row reads inside the staging buffer and is zeroed
+// by a select, not a branch), so the reads overlap instead of each paying
+// the LDS latency in turn.
 template <int LPR, int NJ, bool PAIR, int OFF>
 __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t* xs, int K,
                                           float& acc, float& accu) {
+  static_assert((64 + (NJ - 1) * LPR) * 8 <= kXMax, "x reads stay inside the staging buffer");
   const int l = (threadIdx.x & 63) % LPR;
   const int CH = K / 8;
+  u32x4 xv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xs + (l + j * LPR) * 8);
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) xv[j] = l + j * LPR < CH ? xv[j] : zero;
   float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int ch = l + j * LPR;
-    if (ch < CH) {
-      fma8(pf[OFF + j], xs, ch, a0, a1);
-      if constexpr (PAIR) fma8(pf[OFF + NJ + j], xs, ch, b0, b1);
-    }
+    fma8(pf[OFF + j], xv[j], a0, a1);
+    if constexpr (PAIR) fma8(pf[OFF + NJ + j], xv[j], b0, b1);
   }
   if constexpr (LPR >= 16) {
     acc = wave_sum<LPR>(a0 + a1);

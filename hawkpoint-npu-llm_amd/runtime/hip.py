@@ -31,6 +31,7 @@ HK_ERR_UNSUPPORTED = 3
 HK_MODEL_QKV_BIAS = 1
 HK_MODEL_W8 = 2
 PARTS = {"qkv": 0, "attention": 1, "o_proj": 2, "gate_up": 3, "down_proj": 4, "lm_head": 5}
+PART_STEP = 6  # the whole decode step as the engine runs it
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32

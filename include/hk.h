@@ -141,6 +141,8 @@ int hk_engine_read_kv(hk_engine* engine, int32_t layer, int32_t slot, uint16_t* 
 #define HK_PART_GATE_UP 3   /* RMSNorm + gate/up projection + SwiGLU */
 #define HK_PART_DOWN 4      /* down_proj + residual */
 #define HK_PART_HEAD 5      /* final RMSNorm + LM head + argmax */
+#define HK_PART_STEP 6      /* the whole decode step as the engine runs it (one
+                               persistent launch when the model shape has one) */
 
 /* Enqueue one part of the step for `layer` on the engine stream, without
  * waiting, using the token/position of the last step.  For timing single
@@ -151,7 +153,8 @@ int hk_engine_launch_part(hk_engine* engine, int32_t part, int32_t layer);
 
 /* Enqueue `count` launches of one part, layer i % layers for launch i, as one
  * hipGraph (captured on first use per (part, count)), so host launch cost does
- * not pace the GPU when the launches are timed with events. */
+ * not pace the GPU when the launches are timed with events.  HK_PART_STEP
+ * repeats the whole step at the last token/position, without token feedback. */
 int hk_engine_launch_part_repeat(hk_engine* engine, int32_t part, int32_t count);
 
 /* Enqueue `count` GEMVs y = W_i @ x, W_i = weights[i % n_weights] (bf16, or

@@ -166,3 +166,55 @@ def test_step_contract_errors(qwen_model):
     finally:
         engine.close()
         engine.close()  # idempotent
+
+
+def test_per_kernel_path_bf16_decode(monkeypatch):
+    """bf16 models of a shape the persistent step is compiled for run it by
+    default; HK_PERSISTENT=0 selects the per-kernel step (one GEMV or
+    attention kernel per part, replayed as a hipGraph), which must hold the
+    same bar."""
+    monkeypatch.setenv("HK_PERSISTENT", "0")
+    model = SyntheticModel(QWEN25_05B, seed=0, layers=4)
+    _check_decode(model, _prompt(151936, 40, 12), 32, 72, label="qwen-4L-per-kernel")
+
+
+def test_per_kernel_path_split_kv(monkeypatch):
+    monkeypatch.setenv("HK_PERSISTENT", "0")
+    model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
+    _check_decode(model, _prompt(151936, 600, 14), 8, 4096, label="qwen-2L-ctx4096-per-kernel")
+
+
+def test_persistent_abandon_is_reported(monkeypatch):
+    """A persistent-step wait that runs out of polls abandons the launch: every
+    workgroup leaves at its next wait, the host reports RuntimeError and clears
+    the step's flags.  A spin limit of 0 forces this from the host -- the first
+    poll that is not already satisfied gives up -- with every kernel still
+    exiting normally.  A fresh engine then decodes correctly."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("persistent step: forced abandon")
+    model = SyntheticModel(QWEN25_05B, seed=3, layers=4)
+    prompt = _prompt(151936, 6, 15)
+    monkeypatch.setenv("HK_PERSISTENT_SPIN", "0")
+    engine = QwenDecoderEngine(model, context_length=16)
+    try:
+        with pytest.raises(RuntimeError, match="abandoned"):
+            for pos, tok in enumerate(prompt):
+                engine.step_token(tok, pos, logits=True)
+        with pytest.raises(RuntimeError, match="abandoned"):
+            engine.generate(prompt[-1], len(prompt) - 1, 4)
+    finally:
+        engine.close()
+    monkeypatch.delenv("HK_PERSISTENT_SPIN")
+    oracle = OracleDecoder(model, 16)
+    ref_tokens, ref_logits = oracle.generate_greedy(prompt, 1)
+    engine = QwenDecoderEngine(model, context_length=16)
+    try:
+        for pos, tok in enumerate(prompt[:-1]):
+            engine.step_token(tok, pos, logits=False)
+        got_tok, got_logits = engine.step_token(prompt[-1], len(prompt) - 1, logits=True)
+        announce(f"  after abandon: rel-L2 {rel_l2(got_logits, ref_logits[0]):.3e}")
+        assert rel_l2(got_logits, ref_logits[0]) <= 1e-2
+        assert got_tok == ref_tokens[0] or near_tie(ref_logits[0])
+    finally:
+        engine.close()
