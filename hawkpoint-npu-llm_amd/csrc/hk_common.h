@@ -24,8 +24,11 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
 
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) & 0x8000u) | 0x7fc0u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  // both results are formed and one selected: a branch here would diverge
+  // per element and cost more than the arithmetic
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t nan = ((u >> 16) & 0x8000u) | 0x7fc0u;
+  return (u & 0x7fffffffu) > 0x7f800000u ? nan : rounded;
 }
 
 __device__ __forceinline__ float round_bf16(float f) {

@@ -22,16 +22,23 @@
 //   grows: base + phase index, base = the epoch the previous launch ended on,
 //   so buffers are never cleared between steps.  Tags are 1..65535, so
 //   zeroed memory never matches.
-// * In a GEMV phase, wave 7 of each workgroup is the stager: it polls the
-//   input vector, applies RMSNorm, and writes it to one of two LDS buffers
-//   (plus the raw values the residual add needs).  It issues no other global
-//   loads and no stores, so its polls return at the bare memory latency: a
-//   wave's loads complete in order, and on gfx9 its stores count in the same
-//   counter.  Waves 0-6 own at most one row group each and hold its weights in
-//   registers, loaded two phases ahead (O with gate/up right after Q, down with
-//   the next layer's QKV right after gate/up), so weight streaming overlaps
-//   attention and the waits.  The LM head streams rows on all eight waves with
-//   a double buffer.
+// * In a GEMV phase, waves 6 and 7 of each workgroup are the stagers: they
+//   split the input vector's 16-byte chunks between them, poll them and
+//   write them to one of two LDS buffers (plus the raw values the residual
+//   add needs).  For an RMSNorm input they also stage gamma and their partial
+//   sums of squares, and all eight waves normalise the buffer in place after
+//   the hand-off barrier (a few values per thread instead of a serial pass
+//   on the stagers).  Their only other global loads are weight prefetches aimed
+//   outside the buffer, which return zero without a memory access, and they
+//   store nothing, so their polls return at the bare memory latency: a wave's
+//   loads complete in order, and on gfx9 its stores count in the same
+//   counter.  Two pollers matter for the 4864-word down input: one wave
+//   waiting on 19 chunks per lane per round sees its hand-off about 1 us
+//   later than two waves on 10 each.  Waves 0-5 own at most one row group
+//   each and hold its weights in registers, loaded one or two phases ahead
+//   (O and gate/up right after attention, down and the next layer's QKV
+//   right after O), so weight streaming overlaps attention and the waits.  The LM
+//   head streams rows on all eight waves with a double buffer.
 // * Cross-workgroup data is written and read with device-coherent (sc1)
 //   accesses: the eight XCDs have separate L2 caches, and sc1 accesses bypass
 //   their incoherent state without whole-cache write-back or invalidate fences.
@@ -49,10 +56,11 @@ namespace {
 
 constexpr int kPT = kPersistentThreads;  // threads per workgroup (one workgroup per CU)
 constexpr int kPW = kPT / 64;             // waves per workgroup
-constexpr int kPf = 16;                   // 16-byte weight chunks a lane holds across a wait
+constexpr int kPf = 28;                   // 16-byte weight chunks a lane holds across a wait
 constexpr int kXMax = 5120;               // floats per LDS staging buffer
 constexpr int kHMax = 1024;               // raw residual values kept in LDS
-constexpr int kCW = kPW - 1;              // compute waves; wave kCW is the stager
+constexpr int kSW = 2;                    // stager waves: waves kCW .. kPW - 1
+constexpr int kCW = kPW - kSW;            // compute waves
 constexpr int kChunk = kPersistentChunk;  // attention slots per task
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kGroupsPV = kPT / kHalf;    // slot groups of the P @ V loop
@@ -178,16 +186,18 @@ struct Shape {
   static constexpr int kWaves = kPersistentGrid * kCW;
   static constexpr PhaseCfg q = pick_cfg(QKV, H, false, kWaves, 4);
   static constexpr PhaseCfg o = pick_cfg(H, AO, false, kWaves, 4);
-  static constexpr PhaseCfg g = pick_cfg(I, H, true, kWaves, kPf - o.nj);
-  static constexpr PhaseCfg d = pick_cfg(H, I, false, kWaves, kPf - q.nj);
-  // register slots: O and gate/up are held together, then down and next QKV
-  static constexpr int off_o = 0, off_g = o.nj, off_d = 0, off_q = d.nj;
+  static constexpr PhaseCfg d = pick_cfg(H, I, false, kWaves, 12);
+  static constexpr PhaseCfg g = pick_cfg(I, H, true, kWaves, kPf - o.nj - d.nj);
+  // register slots: O and gate/up are requested together after attention;
+  // down, and the next layer's QKV in the O slots, once O has been computed
+  static constexpr int off_o = 0, off_g = o.nj, off_d = o.nj + 2 * g.nj, off_q = 0;
   static constexpr int head_lpr = 16;
   static constexpr int head_nj = (H / 8 + head_lpr - 1) / head_lpr;
   static constexpr int nq = producers(q, QKV), no = producers(o, H);
   static constexpr int ng = producers(g, I), nd = producers(d, H);
   static_assert(q.lpr && o.lpr && g.lpr && d.lpr, "no register plan for this shape");
   static_assert(head_nj <= kPf / 2, "LM head rows too long for the double buffer");
+  static_assert(q.nj <= o.nj && off_d + d.nj <= kPf, "register slots overlap");
   static_assert(H <= kXMax && I <= kXMax && AO <= kXMax && H <= kHMax, "x staging too small");
   static_assert((I / 4 + 63) / 64 <= 32 && (H / 4 + 63) / 64 <= 32 && (AO / 4 + 63) / 64 <= 32,
                 "stager chunk mask is 32 bits");
@@ -208,14 +218,16 @@ struct PShared {
   // staged GEMV inputs as bf16 (alternating buffers); attention scratch in xs[0].
   // Every staged x is bf16-exact (activations, or RMSNorm output rounded to
   // bf16), so a 16-byte LDS read carries 8 of them.
-  uint16_t xs[2][kXMax];
-  float raw_h[kHMax];   // layer input h before RMSNorm: residual of the O rows
-  float raw_h1[kHMax];  // h1 before RMSNorm: residual of the down rows
+  alignas(16) uint16_t xs[2][kXMax];
+  alignas(16) float raw_h[kHMax];   // layer input h before RMSNorm: residual of the O rows
+  alignas(16) float raw_h1[kHMax];  // h1 before RMSNorm: residual of the down rows
   float red[2][kPW];
   unsigned long long keys[kPW];
   uint32_t out_val[kCW * 16];  // a phase's tagged outputs, gathered for one store
   unsigned out_count;          // compute-wave arrivals (7 per gathered phase)
   unsigned out_stored;         // out_count value once the gathered store is issued
+  alignas(16) uint16_t gs[kHMax];  // RMSNorm gamma of the staged input
+  float ssp[kSW];                  // stagers' partial sums of squares of the staged input
   int abort;
   int ticket;
 };
@@ -287,118 +299,126 @@ __device__ __forceinline__ void publish(Ctx& c, unsigned* flag, unsigned epoch) 
   if (threadIdx.x == 0) st_c32(flag, epoch);
 }
 
-// Stager: poll the K tagged words at src until all carry `tag` (a lane keeps
-// up to kBatch chunks in flight at once), then write them to xs as f32 --
-// RMS-normalised with gamma when given (cpu_backend.py:71-76) -- and the raw
-// values to `raw` when given.  Runs on one wave; false when abandoned.
+// Stagers: poll the K tagged words at src until all carry `tag` (stager
+// wave s of kSW takes the 16-byte chunks s*64 + lane + 64*kSW*j, keeping up to
+// kBatch of them in flight at once) and write them to xs as bf16, the raw
+// values to `raw` when RAW.  For an RMSNorm input (NORM) they also write gamma
+// to gs and their partial sums of squares to ssp; normalise_staged finishes
+// the job on all waves.  False when abandoned.
 constexpr int kBatch = 10;
 
-template <int K, bool NORM>
-__device__ bool stage_wave(const PersistentArgs& a, const uint32_t* src, unsigned tag,
-                           const uint16_t* gamma, float eps, uint16_t* xs, float* raw) {
+template <int K, bool NORM, bool RAW>
+__device__ bool stage_wave(Ctx& c, const uint32_t* src, unsigned tag, const uint16_t* gamma,
+                           uint16_t* xs, float* raw) {
+  const PersistentArgs& a = *c.a;
   constexpr int CH = K / 4;  // 16-byte chunks of four tagged words
-  constexpr int PER = (CH + 63) / 64;
-  constexpr int GPER = PER <= kBatch ? PER : 1;  // gamma words held across the poll
-  const int lane = threadIdx.x & 63;
-  // normalised inputs are staged in one batch, so their words stay in registers
-  static_assert(!NORM || PER <= kBatch, "RMSNorm input longer than one stager batch");
+  constexpr int STRIDE = 64 * kSW;
+  constexpr int PER = (CH + STRIDE - 1) / STRIDE;
+  constexpr int GPER = NORM ? PER : 1;
+  static_assert(!NORM || K <= kHMax, "gamma staging too small");
+  const int lane = c.lane, sw = c.wave - kCW;
+  const int first = sw * 64 + lane;  // this lane's chunk j is first + STRIDE * j
   // gamma is constant: fetch it before polling so its latency overlaps the wait
   uint2 gv[GPER];
-  if (NORM) {
+  if constexpr (NORM) {
 #pragma unroll
     for (int j = 0; j < GPER; ++j) {
-      const int ch = lane + 64 * j;
+      const int ch = first + STRIDE * j;
       gv[j] = ch < CH ? ldg_u2(gamma + ch * 4) : make_uint2(0u, 0u);
     }
   }
   float ss = 0.0f;
+  bool ok = true;
+  constexpr int B = PER < kBatch ? PER : kBatch;
 #pragma unroll
   for (int j0 = 0; j0 < PER; j0 += kBatch) {
-    constexpr int B = PER < kBatch ? PER : kBatch;
     unsigned pending = 0;
 #pragma unroll
-    for (int j = 0; j < B; ++j) {
-      const int ch = lane + 64 * (j0 + j);
-      if (j0 + j < PER && ch < CH) pending |= 1u << j;
-    }
+    for (int j = 0; j < B; ++j)
+      if (j0 + j < PER && first + STRIDE * (j0 + j) < CH) pending |= 1u << j;
     u32x4 v[B];
     for (unsigned spins = 1;; ++spins) {
 #pragma unroll
       for (int j = 0; j < B; ++j)
         if ((pending >> j) & 1u)
-          v[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src, K * 4), lane * 16, (j0 + j) * 1024, kSc1);
+          v[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src, K * 4), first * 16,
+                                                       (j0 + j) * STRIDE * 16, kSc1);
 #pragma unroll
       for (int j = 0; j < B; ++j)
         if (((pending >> j) & 1u) && (v[j].x >> 16) == tag && (v[j].y >> 16) == tag &&
             (v[j].z >> 16) == tag && (v[j].w >> 16) == tag)
           pending &= ~(1u << j);
       if (!__any(pending != 0u)) break;
-      if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
+      if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) {
+        ok = give_up(a);
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
+    if (!ok) break;
 #pragma unroll
     for (int j = 0; j < B; ++j) {
-      const int ch = lane + 64 * (j0 + j);
+      const int ch = first + STRIDE * (j0 + j);
       if (j0 + j < PER && ch < CH) {
-        const float f[4] = {bf_lo(v[j].x), bf_lo(v[j].y), bf_lo(v[j].z), bf_lo(v[j].w)};
+        if constexpr (NORM || RAW) {
+          const float f[4] = {bf_lo(v[j].x), bf_lo(v[j].y), bf_lo(v[j].z), bf_lo(v[j].w)};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          ss += f[q] * f[q];
-          if (raw != nullptr) raw[ch * 4 + q] = f[q];
+          for (int q = 0; q < 4; ++q) ss += f[q] * f[q];
+          if constexpr (RAW) *reinterpret_cast<float4*>(raw + ch * 4) = make_float4(f[0], f[1], f[2], f[3]);
         }
-        if (!NORM)
-          *reinterpret_cast<uint2*>(xs + ch * 4) =
-              make_uint2((v[j].x & 0xffffu) | (v[j].y << 16), (v[j].z & 0xffffu) | (v[j].w << 16));
-      }
-    }
-    if constexpr (NORM) {
-      ss = wave_sum<64>(ss);
-      const float inv = 1.0f / sqrtf(ss / (float)K + eps);
-#pragma unroll
-      for (int j = 0; j < B; ++j) {
-        const int ch = lane + 64 * j;
-        if (j < PER && ch < CH) {
-          const uint2 g = gv[j < GPER ? j : 0];
-          const uint32_t n0 = f32_to_bf16((bf_lo(v[j].x) * inv) * bf_lo(g.x));
-          const uint32_t n1 = f32_to_bf16((bf_lo(v[j].y) * inv) * bf_hi(g.x));
-          const uint32_t n2 = f32_to_bf16((bf_lo(v[j].z) * inv) * bf_lo(g.y));
-          const uint32_t n3 = f32_to_bf16((bf_lo(v[j].w) * inv) * bf_hi(g.y));
-          *reinterpret_cast<uint2*>(xs + ch * 4) = make_uint2(n0 | (n1 << 16), n2 | (n3 << 16));
-        }
+        if constexpr (NORM) *reinterpret_cast<uint2*>(c.sm->gs + ch * 4) = gv[j0 + j < GPER ? j0 + j : 0];
+        *reinterpret_cast<uint2*>(xs + ch * 4) =
+            make_uint2((v[j].x & 0xffffu) | (v[j].y << 16), (v[j].z & 0xffffu) | (v[j].w << 16));
       }
     }
   }
-  return true;
+  if constexpr (NORM) {
+    ss = wave_sum<64>(ss);
+    if (lane == 0) c.sm->ssp[sw] = ss;
+  }
+  return ok;
 }
 
-// Stager for plain bf16 input written before the launch (layer 0).
+// Stagers for the layer-0 input: plain bf16 written before the launch (the
+// embedding row or a preloaded hidden state), staged like an RMSNorm input.
 template <int K>
-__device__ void stage_wave_plain(const uint16_t* src, const uint16_t* gamma, float eps,
-                                 uint16_t* xs, float* raw) {
+__device__ void stage_wave_plain(Ctx& c, const uint16_t* src, const uint16_t* gamma, uint16_t* xs,
+                                 float* raw) {
   constexpr int CH = K / 4;
-  const int lane = threadIdx.x & 63;
+  const int sw = c.wave - kCW;
   float ss = 0.0f;
-  for (int ch = lane; ch < CH; ch += 64) {
+  for (int ch = sw * 64 + c.lane; ch < CH; ch += 64 * kSW) {
     const uint2 w = ldg_u2(src + ch * 4);
     const float f[4] = {bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y)};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ss += f[q] * f[q];
-      raw[ch * 4 + q] = f[q];
-    }
+    for (int q = 0; q < 4; ++q) ss += f[q] * f[q];
+    *reinterpret_cast<float4*>(raw + ch * 4) = make_float4(f[0], f[1], f[2], f[3]);
+    *reinterpret_cast<uint2*>(c.sm->gs + ch * 4) = ldg_u2(gamma + ch * 4);
     *reinterpret_cast<uint2*>(xs + ch * 4) = w;
   }
-  if (gamma == nullptr) return;
   ss = wave_sum<64>(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)K + eps);
-  for (int ch = lane; ch < CH; ch += 64) {
-    const uint2 g = ldg_u2(gamma + ch * 4);
-    const uint32_t n0 = f32_to_bf16((raw[ch * 4 + 0] * inv) * bf_lo(g.x));
-    const uint32_t n1 = f32_to_bf16((raw[ch * 4 + 1] * inv) * bf_hi(g.x));
-    const uint32_t n2 = f32_to_bf16((raw[ch * 4 + 2] * inv) * bf_lo(g.y));
-    const uint32_t n3 = f32_to_bf16((raw[ch * 4 + 3] * inv) * bf_hi(g.y));
-    *reinterpret_cast<uint2*>(xs + ch * 4) = make_uint2(n0 | (n1 << 16), n2 | (n3 << 16));
+  if (c.lane == 0) c.sm->ssp[sw] = ss;
+}
+
+// RMSNorm of the staged input in place (cpu_backend.py:71-76), on all waves
+// after the hand-off barrier: bf16((x * inv) * gamma) with
+// inv = 1 / sqrt(mean(x^2) + eps); the partial sums are added in a fixed
+// order, so every thread uses the same factor.  Ends with a barrier.
+template <int K>
+__device__ __forceinline__ void normalise_staged(Ctx& c, uint16_t* xs, float eps) {
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kSW; ++i) total += c.sm->ssp[i];
+  const float inv = 1.0f / sqrtf(total / (float)K + eps);
+  uint32_t* xw = reinterpret_cast<uint32_t*>(xs);
+  const uint32_t* gw = reinterpret_cast<const uint32_t*>(c.sm->gs);
+  for (int i = threadIdx.x; i < K / 2; i += kPT) {
+    const uint32_t x = xw[i], g = gw[i];
+    const uint32_t n0 = f32_to_bf16((bf_lo(x) * inv) * bf_lo(g));
+    const uint32_t n1 = f32_to_bf16((bf_hi(x) * inv) * bf_hi(g));
+    xw[i] = n0 | (n1 << 16);
   }
+  __syncthreads();
 }
 
 // Issue the loads of this wave's row group (rows group*RPW + sub) of W [M, K]
@@ -727,7 +747,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   c.wave = threadIdx.x >> 6;
   c.lane = threadIdx.x & 63;
   c.gw = c.wg * kCW + c.wave;
-  const bool stager = c.wave == kCW;
+  const bool stager = c.wave >= kCW;
   if (threadIdx.x == 0) {
     sm.abort = 0;
     sm.out_count = 0;
@@ -769,16 +789,19 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   const bool lg = c.lane % S::g.lpr == 0, ld = c.lane % S::d.lpr == 0;
   uint16_t* const dst_h = is_d && row_d < S::H ? a.h + row_d : reinterpret_cast<uint16_t*>(pad);
   const int res_o = min(row_o, S::H - 1), res_d = min(row_d, S::H - 1);
-  const unsigned bias_off = is_q && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
+  const unsigned bias_off = is_q && !stager && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
+  // Every wave issues every weight prefetch (the stager's, like those of
+  // workgroups that sit a phase out, read zero from outside the resource):
+  // a prefetch skipped on one path would keep the registers' previous values
+  // live around the whole layer loop.
+  const bool pq = is_q && !stager, po = is_o && !stager, pg = is_g && !stager, pd = is_d && !stager;
 
   u32x4 pf[kPf];
   float acc, accu, bias_q = 0.0f;
   int buf = 0;  // LDS staging buffer of the next GEMV phase
-  if (!stager) {
-    prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, is_q);
-    bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                           rsrc(sm.layers[0].qkv_bias, S::QKV * 4), bias_off, 0, 0));
-  }
+  prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
+  bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         rsrc(sm.layers[0].qkv_bias, S::QKV * 4), bias_off, 0, 0));
 
   // The stager fills xs[buf]; the barrier hands it to the compute waves.
   // Returns false (in every wave) when the launch is abandoned.
@@ -796,11 +819,12 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
       bool ok = true;
       if (stager) {
         if (l == 0)
-          stage_wave_plain<S::H>(x0, lw.in_norm, a.eps, sm.xs[buf], sm.raw_h);
+          stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
         else
-          ok = stage_wave<S::H, true>(a, a.th, tag_of(ep), lw.in_norm, a.eps, sm.xs[buf], sm.raw_h);
+          ok = stage_wave<S::H, true, true>(c, a.th, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
       }
       if (!handoff(ok)) return;
+      normalise_staged<S::H>(c, sm.xs[buf], a.eps);
     }
     if (!stager) {
       dot_group<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.xs[buf], S::H, acc, accu);
@@ -815,44 +839,48 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
       __syncthreads();  // LDS reuse
       if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2))) return;
     }
-    if (!stager) {
-      prefetch<S::o.lpr, S::o.nj, false, S::off_o>(pf, lw.o, S::H, S::AO, c.gw, is_o);
-      prefetch<S::g.lpr, S::g.nj, true, S::off_g>(pf, lw.gate_up, S::I, S::H, c.gw, is_g);
-    }
+    prefetch<S::o.lpr, S::o.nj, false, S::off_o>(pf, lw.o, S::H, S::AO, c.gw, po);
+    prefetch<S::g.lpr, S::g.nj, true, S::off_g>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
     // ---- O ----
     if (is_o) {
       bool ok = true;
-      if (stager) ok = stage_wave<S::AO, false>(a, a.tattn, tag_of(ep + 2), nullptr, 0.0f, sm.xs[buf], nullptr);
+      if (stager) ok = stage_wave<S::AO, false, false>(c, a.tattn, tag_of(ep + 2), nullptr, sm.xs[buf], nullptr);
       if (!handoff(ok)) return;
     }
     if (!stager) {
       dot_group<S::o.lpr, S::o.nj, false, S::off_o>(pf, sm.xs[buf], S::AO, acc, accu);
       publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
-                       lo, a.th1 + fo, nvo, pad, false);
+                       lo, a.th1 + fo, nvo, pad, true);
+    }
+    // down and the next layer's QKV go out here rather than after gate/up:
+    // issued there, they would queue in this CU's memory pipeline ahead of the
+    // stagers' polls for the down input, the largest one of the layer
+    {
+      prefetch<S::d.lpr, S::d.nj, false, S::off_d>(pf, lw.down, S::H, S::I, c.gw, pd);
+      const bool more = l + 1 < L;
+      const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
+      prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             rsrc(nx.qkv_bias, S::QKV * 4), bias_off, 0, 0));
     }
     if (is_o) buf ^= 1;
     // ---- G ----
     if (is_g) {
       bool ok = true;
-      if (stager) ok = stage_wave<S::H, true>(a, a.th1, tag_of(ep + 3), lw.post_norm, a.eps, sm.xs[buf], sm.raw_h1);
+      if (stager) ok = stage_wave<S::H, true, true>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], sm.raw_h1);
       if (!handoff(ok)) return;
+      normalise_staged<S::H>(c, sm.xs[buf], a.eps);
     }
     if (!stager) {
       dot_group<S::g.lpr, S::g.nj, true, S::off_g>(pf, sm.xs[buf], S::H, acc, accu);
       publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
-                       lg, a.tact + fg, nvg, pad, true);
-      prefetch<S::d.lpr, S::d.nj, false, S::off_d>(pf, lw.down, S::H, S::I, c.gw, is_d);
-      const bool more = l + 1 < L;
-      const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
-      prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, nx.qkv, S::QKV, S::H, c.gw, is_q && more);
-      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             rsrc(nx.qkv_bias, S::QKV * 4), bias_off, 0, 0));
+                       lg, a.tact + fg, nvg, pad, false);
     }
     if (is_g) buf ^= 1;
     // ---- D ----
     if (is_d) {
       bool ok = true;
-      if (stager) ok = stage_wave<S::I, false>(a, a.tact, tag_of(ep + 4), nullptr, 0.0f, sm.xs[buf], nullptr);
+      if (stager) ok = stage_wave<S::I, false, false>(c, a.tact, tag_of(ep + 4), nullptr, sm.xs[buf], nullptr);
       if (!handoff(ok)) return;
     }
     if (!stager) {
@@ -882,8 +910,9 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   if (!stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
   {
     bool ok = true;
-    if (stager) ok = stage_wave<S::H, true>(a, a.th, tag_of(ep_layers), a.final_norm, a.eps, sm.xs[buf], nullptr);
+    if (stager) ok = stage_wave<S::H, true, false>(c, a.th, tag_of(ep_layers), a.final_norm, sm.xs[buf], nullptr);
     if (!handoff(ok)) return;
+    normalise_staged<S::H>(c, sm.xs[buf], a.eps);
   }
   if (stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
   const uint16_t* xh = sm.xs[buf];
