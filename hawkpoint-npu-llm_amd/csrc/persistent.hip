@@ -64,6 +64,7 @@ constexpr int kCW = kPW - kSW;            // compute waves
 constexpr int kChunk = kPersistentChunk;  // attention slots per task
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kGroupsPV = kPT / kHalf;    // slot groups of the P @ V loop
+constexpr int kSlotsPV = kChunk / kGroupsPV;  // consecutive slots per group
 constexpr int kPartStride = kHeadDim + 2;
 constexpr int kSc1 = 16;                  // buffer-load cache policy: device scope (sc1)
 static_assert(2 * kChunk == kPT, "two threads per attention slot");
@@ -530,25 +531,27 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   for (int ch = 0; ch < kHeadDim / 16; ++ch)
     krow[ch] = __builtin_amdgcn_raw_buffer_load_b128(kc, slot * kHeadDim * 2 + half * kHeadDim,
                                                      ch * 16, 0);
+  // P @ V: thread (gi, dp) takes dimensions 2dp, 2dp+1 of the kSlotsPV
+  // consecutive slots gi * kSlotsPV ..; slots past p read zero
   const int dp = tid & (kHalf - 1);
   const int gi = tid / kHalf;
-  uint32_t vw[kChunk / kGroupsPV];
-  const int voff = (t0 + gi) * kHeadDim * 2 + dp * 4;
+  uint32_t vw[kSlotsPV];
+  const int voff = (t0 + gi * kSlotsPV) * kHeadDim * 2 + dp * 4;
 #pragma unroll
-  for (int k = 0; k < kChunk / kGroupsPV; ++k)
-    vw[k] = __builtin_amdgcn_raw_buffer_load_b32(vc, voff, k * kGroupsPV * kHeadDim * 2, 0);
+  for (int k = 0; k < kSlotsPV; ++k)
+    vw[k] = __builtin_amdgcn_raw_buffer_load_b32(vc, voff, k * kHeadDim * 2, 0);
 
   const int qr = h * kHeadDim, kr = (S::HQ + g) * kHeadDim, vr = (S::HQ + S::HKV + g) * kHeadDim;
   const uint32_t* tq = a.tqkv;
   bool ok = true;
   // the slot-p value word of the P @ V loop, for the group holding slot p
-  if ((p - t0 - gi) % kGroupsPV == 0 && p - t0 - gi >= 0) {
-    const int kp = (p - t0 - gi) / kGroupsPV;
+  if (p - t0 - gi * kSlotsPV >= 0 && p - t0 - gi * kSlotsPV < kSlotsPV) {
+    const int kp = p - t0 - gi * kSlotsPV;
     uint32_t lo = 0, hi = 0;
     ok = poll_word(a, tq + vr + 2 * dp, tag_q, lo) && poll_word(a, tq + vr + 2 * dp + 1, tag_q, hi);
     const uint32_t word = (lo & 0xffffu) | (hi << 16);
 #pragma unroll
-    for (int k = 0; k < kChunk / kGroupsPV; ++k)
+    for (int k = 0; k < kSlotsPV; ++k)
       if (k == kp) vw[k] = word;
   }
   // rotated q head and new key (bf16-rounded); the group's first query head
@@ -634,16 +637,24 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   if (half == 0) pr[si] = nsplit == 1 ? e / sum : e;  // a single chunk normalises first, as NumPy does
   __syncthreads();
 
+  // probabilities of slots past the chunk's live ones are zero, and so are
+  // their value words, so the loop needs no bounds test; the four 16-byte
+  // LDS reads go out together
   float o0 = 0.0f, o1 = 0.0f;
+  {
+    const float4* pr4 = reinterpret_cast<const float4*>(pr + gi * kSlotsPV);
+    float4 pq[kSlotsPV / 4];
 #pragma unroll
-  for (int k = 0; k < kChunk / kGroupsPV; ++k) {
-    const int t = gi + k * kGroupsPV;
-    if (t < n) {
-      const float pt = pr[t];
-      o0 = fmaf(pt, bf_lo(vw[k]), o0);
-      o1 = fmaf(pt, bf_hi(vw[k]), o1);
+    for (int q = 0; q < kSlotsPV / 4; ++q) pq[q] = pr4[q];
+#pragma unroll
+    for (int q = 0; q < kSlotsPV / 4; ++q) {
+      const float pt[4] = {pq[q].x, pq[q].y, pq[q].z, pq[q].w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        o0 = fmaf(pt[r], bf_lo(vw[4 * q + r]), o0);
+        o1 = fmaf(pt[r], bf_hi(vw[4 * q + r]), o1);
+      }
     }
-    if (k % 8 == 7) __builtin_amdgcn_sched_barrier(0);
   }
   acc[gi * kHeadDim + 2 * dp] = o0;
   acc[gi * kHeadDim + 2 * dp + 1] = o1;
