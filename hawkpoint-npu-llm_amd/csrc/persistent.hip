@@ -300,6 +300,13 @@ __device__ __forceinline__ void publish(Ctx& c, unsigned* flag, unsigned epoch) 
   if (threadIdx.x == 0) st_c32(flag, epoch);
 }
 
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Stagers: poll the K tagged words at src until all carry `tag` (stager
 // wave s of kSW takes the 16-byte chunks s*64 + lane + 64*kSW*j, keeping up to
 // kBatch of them in flight at once) and write them to xs as bf16, the raw
@@ -377,6 +384,9 @@ __device__ bool stage_wave(Ctx& c, const uint32_t* src, unsigned tag, const uint
     ss = wave_sum<64>(ss);
     if (lane == 0) c.sm->ssp[sw] = ss;
   }
+  // every load of this wave has returned by now; saying so leaves the
+  // compiler nothing to wait for on this path after the hand-off barrier
+  wait_vm<0>();
   return ok;
 }
 
@@ -716,10 +726,12 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
 // tens of kilobytes of prefetch.
 template <int RPW>
 __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t word, bool row_lead,
-                                             uint32_t* first, int valid_rows, uint32_t* pad,
-                                             bool then_load) {
+                                             __amdgpu_buffer_rsrc_t tagged_buf, unsigned first,
+                                             int valid_rows, unsigned pad, bool then_load) {
   static_assert(kCW * RPW <= kCW * 16, "gather buffer too small");
-  uint32_t* dst = pad;
+  // word offsets into the tagged-activation buffer (a buffer store with a
+  // 32-bit offset holds fewer registers than a 64-bit address)
+  unsigned dst = pad;
   uint32_t v = 0;
   unsigned old = 0;
   if (producer) {
@@ -732,7 +744,8 @@ __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t wor
       dst = first + c.lane;
     }
   }
-  st_c32(dst, v);
+  // device-coherent (sc1) like st_c32
+  __builtin_amdgcn_raw_buffer_store_b32(v, tagged_buf, dst * 4u, 0, kSc1);
   if (!producer) return;
   const unsigned done = old - old % kCW + kCW;
   if (old % kCW == kCW - 1) {
@@ -787,7 +800,12 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   // Row of this lane in each GEMV phase.  Every compute wave stores once per
   // phase: a row it does not own (or a phase its workgroup sits out) goes to
   // the wave's own pad word, so all compute waves issue the same stores.
-  uint32_t* pad = a.pad + c.wg * kPW + c.wave;
+  // publish targets as word offsets in the one tagged-activation allocation
+  // (h, h1, qkv, attn, act, then one pad word per wave)
+  const unsigned o_h = 0, o_h1 = (unsigned)(a.th1 - a.th), o_qkv = (unsigned)(a.tqkv - a.th);
+  const unsigned o_act = (unsigned)(a.tact - a.th), o_pad = (unsigned)(a.pad - a.th);
+  const __amdgpu_buffer_rsrc_t tbuf = rsrc(a.th, (int)(o_pad + kPersistentGrid * kPW) * 4);
+  const unsigned pad = o_pad + c.wg * kPW + c.wave;
   const int row_q = c.gw * (64 / S::q.lpr) + c.lane / S::q.lpr;
   const int row_o = c.gw * (64 / S::o.lpr) + c.lane / S::o.lpr;
   const int row_g = c.gw * (64 / S::g.lpr) + c.lane / S::g.lpr;
@@ -798,7 +816,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   const int nvq = S::QKV - fq, nvo = S::H - fo, nvg = S::I - fg, nvd = S::H - fd;
   const bool lq = c.lane % S::q.lpr == 0, lo = c.lane % S::o.lpr == 0;
   const bool lg = c.lane % S::g.lpr == 0, ld = c.lane % S::d.lpr == 0;
-  uint16_t* const dst_h = is_d && row_d < S::H ? a.h + row_d : reinterpret_cast<uint16_t*>(pad);
+  const unsigned dst_h = is_d && row_d < S::H ? (unsigned)row_d * 2u : kOutside;  // byte offset in h
   const int res_o = min(row_o, S::H - 1), res_d = min(row_d, S::H - 1);
   const unsigned bias_off = is_q && !stager && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
   // Every wave issues every weight prefetch (the stager's, like those of
@@ -840,7 +858,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     if (!stager) {
       dot_group<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.xs[buf], S::H, acc, accu);
       const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
-      publish_rows<RQ>(c, is_q, tagged(y, tag_of(ep + 1)), lq, a.tqkv + fq, nvq, pad, true);
+      publish_rows<RQ>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, nvq, pad, true);
     }
     if (is_q) buf ^= 1;
     // ---- A ---- (tasks go to the highest workgroups, which own no Q rows;
@@ -861,7 +879,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     if (!stager) {
       dot_group<S::o.lpr, S::o.nj, false, S::off_o>(pf, sm.xs[buf], S::AO, acc, accu);
       publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
-                       lo, a.th1 + fo, nvo, pad, true);
+                       lo, tbuf, o_h1 + fo, nvo, pad, true);
     }
     // down and the next layer's QKV go out here rather than after gate/up:
     // issued there, they would queue in this CU's memory pipeline ahead of the
@@ -885,7 +903,7 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     if (!stager) {
       dot_group<S::g.lpr, S::g.nj, true, S::off_g>(pf, sm.xs[buf], S::H, acc, accu);
       publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
-                       lg, a.tact + fg, nvg, pad, false);
+                       lg, tbuf, o_act + fg, nvg, pad, false);
     }
     if (is_g) buf ^= 1;
     // ---- D ----
@@ -897,8 +915,9 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     if (!stager) {
       dot_group<S::d.lpr, S::d.nj, false, S::off_d>(pf, sm.xs[buf], S::I, acc, accu);
       const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
-      publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, a.th + fd, nvd, pad, false);
-      stg(dst_h, (uint16_t)y);  // plain copy: the final hidden for hk_engine_final_hidden
+      publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, tbuf, o_h + fd, nvd, pad, false);
+      // plain copy: the final hidden for hk_engine_final_hidden
+      __builtin_amdgcn_raw_buffer_store_b16((uint16_t)y, rsrc(a.h, S::H * 2), dst_h, 0, 0);
     }
     if (is_d) buf ^= 1;
   }
