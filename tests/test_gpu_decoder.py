@@ -98,3 +98,48 @@ def test_decoder_engine_returns_final_norm(package):
         assert np.abs(got - want).max() <= 0.02 * np.abs(want).max()
     finally:
         eng.close()
+
+
+def test_generate_messages_on_the_gpu(tmp_path):
+    """The generation stack (ChatML prompt, batched prefill, host sampling,
+    stop sequences, log probabilities) over the GPU engine, against the
+    oracle's greedy continuation of the same prompt ids."""
+    from runtime.generate import NPUDecoder
+    from runtime.sampling import SamplingParams
+    from runtime.tokenizer import write_chatml_tokenizer
+
+    announce("NPUDecoder generate_messages (synthetic ChatML tokenizer)")
+    model = SyntheticModel(SMALL, seed=21, std=0.08)
+    path = write_package(model, tmp_path / "chat")
+    write_chatml_tokenizer(path, SMALL["vocab_size"])
+    dec = NPUDecoder(path, context_length=160)
+    try:
+        msgs = [{"role": "user", "content": "Hello GPU"}]
+        prompt = dec.tokenizer.encode_chat_window(msgs, 160 - 8)[0]
+        oracle = OracleDecoder(XDNA1Model(path), 160)
+        ref, _ = oracle.generate_greedy(prompt, 8)
+        eos = dec.tokenizer.eos_id
+        want = ref[:ref.index(eos)] if eos in ref else ref
+        chunks = list(dec.generate_messages(msgs, 8))
+        stats = chunks[-1][1]
+        assert stats["generated_token_ids"] == want
+        assert stats["prompt_tokens"] == len(prompt) and stats["cached_prompt_tokens"] == 0
+        assert "".join(c[0] for c in chunks) == dec.tokenizer.decode(want)
+        # the same request again reuses the prompt; with log probabilities the tokens do not change
+        chunks = list(dec.generate_messages(msgs, 8, logprobs=2))
+        assert chunks[-1][1]["generated_token_ids"] == want
+        assert chunks[-1][1]["cached_prompt_tokens"] == len(prompt) - 1
+        entries = [e for c in chunks for e in c[2]]
+        assert len(entries) == len(want) and all(len(e["top_logprobs"]) == 2 for e in entries)
+        assert all(e["top_logprobs"][0]["logprob"] >= e["top_logprobs"][1]["logprob"] for e in entries)
+        # seeded sampling repeats; logit bias forces a token
+        p = SamplingParams.build(temperature=0.9, top_k=20, seed=7)
+        a = list(dec.generate_messages(msgs, 6, p))[-1][1]["generated_token_ids"]
+        b = list(dec.generate_messages(msgs, 6, p))[-1][1]["generated_token_ids"]
+        assert a == b
+        forced = list(dec.generate_messages(msgs, 4, SamplingParams.build(logit_bias={"65": 100.0})))
+        assert forced[-1][1]["generated_token_ids"] == [65] * 4
+        text = "".join(c[0] for c in list(dec.generate_messages(msgs, 8, stop=dec.tokenizer.decode([65]))))
+        assert dec.tokenizer.decode([65]) not in text
+    finally:
+        dec.close()
