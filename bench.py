@@ -194,6 +194,9 @@ def main():
     ap.add_argument("--no-parts", action="store_true",
                     help="skip the graph-replayed step and per-part timing (for profiler runs)")
     ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--workload", choices=("decode", "experts"), default="decode",
+                    help="experts: the GGML MUL_MAT_ID / Colibri expert-group shims instead of "
+                    "the decode step (prints its own JSON line)")
     ap.add_argument("--probe", action="store_true",
                     help="only the counter-calibration workload: decode-step launches, then "
                     "4 device copies of 256 MiB")
@@ -202,6 +205,9 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               "(the engine runs on a single MI355X)", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "experts":
+        experts_main(args)
+        return
 
     import numpy as np
 
@@ -376,6 +382,136 @@ def main():
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
         result["cpu_baseline"] = cpu_baseline(model, prompt[:8], args.cpu_steps)
+    print(json.dumps(result), flush=True)
+
+
+EXPERTS, EXPERT_ROWS, EXPERT_COLS = 8, 2048, 2048  # the reference's 8 expert slots of 2048 x 2048
+EXPERT_POOL = 128  # experts resident on the device: 512 MiB of int8, twice the 256 MB Infinity Cache
+GROUP_HIDDEN, GROUP_MID = 2048, 1408  # an 8-expert group of the 64-expert H2048/I1408 MoE
+
+
+def expert_launch_bytes():
+    """Algorithmic HBM bytes of one MUL_MAT_ID launch over 8 slots: int8
+    weights and float32 row scales of 8 experts, the bf16 input row read by
+    every slot, and 8 float32 output rows."""
+    per_slot = EXPERT_ROWS * EXPERT_COLS + 4 * EXPERT_ROWS + 2 * EXPERT_COLS + 4 * EXPERT_ROWS
+    return EXPERTS * per_slot
+
+
+def experts_cpu_baseline(weights, x, budget_s=10.0):
+    """The oracle's expert projection (pre-quantised, one BLAS thread) on the
+    same 8-slot call, repeated for about ``budget_s`` seconds."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import experts as ox
+
+    packed = [ox.requantize_rows(weights[e]) for e in range(EXPERTS)]
+    calls, t0 = 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        while time.perf_counter() - t0 < budget_s or calls == 0:
+            for q, s in packed:
+                ox.project(q, s, x)
+            calls += 1
+    elapsed = time.perf_counter() - t0
+    return {"value": round(calls / elapsed, 3), "unit": "calls/s", "cores": 1, "kind": "port",
+            "sample": f"{calls} MUL_MAT_ID calls (8 x {EXPERT_ROWS} x {EXPERT_COLS}, weights "
+            "pre-quantised) through oracle/experts.py with one BLAS thread"}
+
+
+def experts_main(args):
+    """Expert shims: the MUL_MAT_ID kernel over 8-expert slices of 128
+    resident 2048 x 2048 W8 experts, rotating so that no launch finds its
+    weights in the Infinity Cache (timed with HIP events); the host-pointer
+    call rate of both contracts; and the oracle on the host."""
+    import numpy as np
+
+    from runtime import experts, hip
+
+    hip.init(0)
+    rng = np.random.default_rng(5)
+    log(f"requantising {EXPERT_POOL} x {EXPERT_ROWS} x {EXPERT_COLS} expert weights")
+    w = rng.standard_normal((EXPERT_POOL, EXPERT_ROWS, EXPERT_COLS), dtype=np.float32)
+    w *= np.float32(0.02)
+    x = rng.normal(0, 1, EXPERT_COLS).astype(np.float32)
+    ids = np.arange(EXPERTS, dtype=np.int32)
+    ggml = experts.GgmlExperts(w)
+    for _ in range(max(args.warmup, 1)):
+        ggml.mul_mat_id(x, ids)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ggml.mul_mat_id(x, ids)
+    call_s = (time.perf_counter() - t0) / args.steps
+    n = args.kernel_launches
+    rotating = (np.arange(n)[:, None] * EXPERTS + np.arange(EXPERTS)[None, :]) % EXPERT_POOL
+    same = np.tile(ids, (n, 1))
+    ggml.repeat_ms(rotating)  # warm
+    kernel_ms = ggml.repeat_ms(rotating)
+    warm_ms = ggml.repeat_ms(same)
+    nbytes = expert_launch_bytes()
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    log(f"MUL_MAT_ID 8x2048x2048: kernel {kernel_ms * 1e3:.2f} us ({achieved:.0f} GB/s) rotating over "
+        f"{EXPERT_POOL} experts, {warm_ms * 1e3:.2f} us on the same 8; call {call_s * 1e6:.1f} us host-inclusive")
+
+    # Colibri expert group: 8 experts of 2048 -> 1408 -> 2048, one row each
+    experts.coli_init(0)
+    mk = lambda shape: rng.normal(0, 0.02, shape).astype(np.float32)
+    g = [experts.ColiTensor(mk((GROUP_MID, GROUP_HIDDEN)), None, 0, GROUP_HIDDEN, GROUP_MID) for _ in range(8)]
+    u = [experts.ColiTensor(mk((GROUP_MID, GROUP_HIDDEN)), None, 0, GROUP_HIDDEN, GROUP_MID) for _ in range(8)]
+    d = [experts.ColiTensor(mk((GROUP_HIDDEN, GROUP_MID)), None, 0, GROUP_MID, GROUP_HIDDEN) for _ in range(8)]
+    gx = rng.normal(0, 1, 8 * GROUP_HIDDEN).astype(np.float32)
+    for _ in range(max(args.warmup, 1)):
+        experts.expert_group(g, u, d, gx)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        experts.expert_group(g, u, d, gx)
+    group_s = (time.perf_counter() - t0) / args.steps
+    log(f"Colibri expert group 8 x (2048->1408->2048): {group_s * 1e6:.1f} us per call host-inclusive")
+    for t in g + u + d:
+        t.close()
+    experts.coli_shutdown()
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_expert_w8_mul_mat_id.json"
+    if tfile.is_file():
+        traffic = json.loads(tfile.read_text()).get("traffic_bytes_per_launch")
+    result = {
+        "metric": "MUL_MAT_ID expert GEMV launches/s, 8 x 2048 x 2048 W8 experts per launch from HBM",
+        "value": round(1e3 / kernel_ms, 1),
+        "unit": "launches/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(kernel_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights, f32 accumulate",
+        "data": "synthetic",
+        "config": {
+            "workload": "GGML MUL_MAT_ID, 8 ids per launch over 128 resident experts of 2048 x 2048 "
+            "(N(0,0.02) weights requantised to int8 + row scale), one float32 input row, launch i "
+            "using experts 8i..8i+7 mod 128; Colibri expert group of 8 experts 2048 -> 1408 -> 2048",
+            "experts_per_launch": EXPERTS, "resident_experts": EXPERT_POOL, "rows": EXPERT_ROWS,
+            "cols": EXPERT_COLS,
+        },
+        "kernel_us_same_experts": round(warm_ms * 1e3, 3),
+        "call_us_host_inclusive": round(call_s * 1e6, 2),
+        "coli_group_us_host_inclusive": round(group_s * 1e6, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"expert_w8_kernel, one launch per MUL_MAT_ID call (bytes/launch {nbytes})",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle")
+        result["cpu_baseline"] = experts_cpu_baseline(w[:EXPERTS], x)
+    ggml.close()
     print(json.dumps(result), flush=True)
 
 

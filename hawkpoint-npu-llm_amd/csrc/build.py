@@ -15,7 +15,7 @@ HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent.parent
 LIB_DIR = HERE.parent / "lib"
 OBJ_DIR = HERE / "_build"
-SOURCES = ["gemv.hip", "attention.hip", "ops.hip", "prefill.hip", "moe.hip", "persistent.hip", "engine.hip"]
+SOURCES = ["gemv.hip", "attention.hip", "ops.hip", "prefill.hip", "moe.hip", "experts.hip", "persistent.hip", "engine.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: a*b+c stays two roundings, as NumPy evaluates it.

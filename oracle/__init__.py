@@ -19,6 +19,8 @@ cpu_backend  ``CPUDecoderStage`` (per-layer decode arithmetic), the step loop of
              ``NPUDecoder.decode_token`` with ``npu_layers=0`` and its argmax.
 quant        the per-output-row int8 quantiser and the W8 projection formula.
 moe          the routed-expert block (router, top-k, experts, combine).
+experts      the GGML MUL_MAT_ID and Colibri expert-group offload contracts
+             (upload formats, W8 requantisation, 2048-column tiles, SwiGLU).
 
 Pinning status of each function is recorded in its docstring and checked by
 ``tests/test_oracle_*.py``.

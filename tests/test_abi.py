@@ -46,3 +46,34 @@ def test_error_path_without_gpu_work():
     rc = lib.hk_engine_create(None, None, None)
     assert rc == hip.HK_ERR_INVALID
     assert "null" in hip.last_error()
+
+
+def _declared_experts():
+    text = (ROOT / "include" / "hk_experts.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b((?:hk_ggml|coli_cuda)_[a-z0-9_]+)\s*\(", text))
+
+
+def test_expert_shims_are_exported_and_bound():
+    from runtime import experts, hip
+
+    names = _declared_experts()
+    assert {"hk_ggml_mul_mat_id", "coli_cuda_expert_group_pinned", "coli_cuda_matmul"} <= names
+    lib = ctypes.CDLL(str(hip.LIB_PATH))
+    assert not [n for n in sorted(names) if not hasattr(lib, n)]
+    assert set(experts.EXPORTED) == names
+
+
+def test_expert_shim_validation_without_gpu_work():
+    from runtime import experts
+
+    lib = experts.lib()
+    # the supports_op table (ggml-xdna.cpp:1681-1716)
+    assert experts.ggml_supported(2048, 2048, 8, 8, 8)
+    assert experts.ggml_supported(1, 1, 64, 1, 1)
+    for bad in ((2049, 16, 8, 1, 1), (16, 2049, 8, 1, 1), (16, 16, 7, 1, 1), (16, 16, 8, 9, 9),
+                (16, 16, 8, 0, 1), (16, 16, 8, 4, 2), (0, 16, 8, 1, 1)):
+        assert not experts.ggml_supported(*bad), bad
+    # Colibri: nothing is up before coli_cuda_init, and a bad device list is refused
+    assert lib.coli_cuda_device_count() == 0 and lib.coli_cuda_device_at(0) == -1
+    assert lib.coli_cuda_init(None, 1) == 0
