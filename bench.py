@@ -390,6 +390,45 @@ EXPERT_POOL = 128  # experts resident on the device: 512 MiB of int8, twice the 
 GROUP_HIDDEN, GROUP_MID = 2048, 1408  # an 8-expert group of the 64-expert H2048/I1408 MoE
 
 
+QUANT_POOLS = {"q4_k": (12, 144, 256), "q6_k": (14, 210, 160)}  # ggml type, block bytes, resident experts
+
+
+def quant_launch_bytes(block_bytes):
+    """Algorithmic bytes of one quantised MUL_MAT_ID launch over 8 slots:
+    the experts' GGML blocks, the bf16 input row per slot, float32 outputs."""
+    per_slot = EXPERT_ROWS * (EXPERT_COLS // 256) * block_bytes + 2 * EXPERT_COLS + 4 * EXPERT_ROWS
+    return EXPERTS * per_slot
+
+
+def quant_mul_mat_id(experts, rng, x, n):
+    """Q4_K / Q6_K MUL_MAT_ID launches rotating over more experts than the
+    Infinity Cache holds (random valid blocks: random quants and scales,
+    small fp16 d)."""
+    import numpy as np
+
+    out = {}
+    for name, (gtype, block_bytes, pool) in QUANT_POOLS.items():
+        nb = EXPERT_COLS // 256
+        blocks = rng.integers(0, 256, (pool * EXPERT_ROWS, nb, block_bytes), dtype=np.uint8)
+        d_at = (0, 2) if gtype == 12 else (208,)
+        for off in d_at:
+            blocks[..., off:off + 2] = rng.uniform(0.001, 0.01, (pool * EXPERT_ROWS, nb)).astype(
+                np.float16).view(np.uint8).reshape(pool * EXPERT_ROWS, nb, 2)
+        qset = experts.GgmlExperts.quant(gtype, blocks, pool, EXPERT_ROWS, EXPERT_COLS)
+        del blocks
+        qset.mul_mat_id(x, np.arange(EXPERTS, dtype=np.int32))
+        rotating = (np.arange(n)[:, None] * EXPERTS + np.arange(EXPERTS)[None, :]) % pool
+        qset.repeat_ms(rotating)  # warm
+        ms = qset.repeat_ms(rotating)
+        nbytes = quant_launch_bytes(block_bytes)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"{name} MUL_MAT_ID 8x2048x2048: kernel {ms * 1e3:.2f} us ({gbs:.0f} GB/s) rotating over {pool} experts")
+        out[name] = {"kernel_us": round(ms * 1e3, 3), "bytes_per_launch": nbytes, "achieved_gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "resident_experts": pool}
+        qset.close()
+    return out
+
+
 def expert_launch_bytes():
     """Algorithmic HBM bytes of one MUL_MAT_ID launch over 8 slots: int8
     weights and float32 row scales of 8 experts, the bf16 input row read by
@@ -453,6 +492,8 @@ def experts_main(args):
     log(f"MUL_MAT_ID 8x2048x2048: kernel {kernel_ms * 1e3:.2f} us ({achieved:.0f} GB/s) rotating over "
         f"{EXPERT_POOL} experts, {warm_ms * 1e3:.2f} us on the same 8; call {call_s * 1e6:.1f} us host-inclusive")
 
+    quant = quant_mul_mat_id(experts, rng, x, n)
+
     # Colibri expert group: 8 experts of 2048 -> 1408 -> 2048, one row each
     experts.coli_init(0)
     mk = lambda shape: rng.normal(0, 0.02, shape).astype(np.float32)
@@ -498,6 +539,7 @@ def experts_main(args):
         "kernel_us_same_experts": round(warm_ms * 1e3, 3),
         "call_us_host_inclusive": round(call_s * 1e6, 2),
         "coli_group_us_host_inclusive": round(group_s * 1e6, 2),
+        "quant_mul_mat_id": quant,
         "roofline": {
             "bound": "hbm",
             "kernel": f"expert_w8_kernel, one launch per MUL_MAT_ID call (bytes/launch {nbytes})",

@@ -15,8 +15,12 @@ import numpy as np
 
 from runtime import hip
 
-__all__ = ["EXPORTED", "GgmlExperts", "ggml_supported", "ColiTensor", "coli_init", "coli_shutdown",
-           "coli_matmul", "expert_group", "expert_mlp"]
+__all__ = ["EXPORTED", "GgmlExperts", "ggml_supported", "dense_supported", "quant_supported", "GGML_Q4_K",
+           "GGML_Q6_K", "ColiTensor", "coli_init", "coli_shutdown", "coli_matmul", "expert_group", "expert_mlp"]
+
+GGML_Q4_K = 12  # ggml_type values (include/hk_experts.h)
+GGML_Q6_K = 14
+BLOCK_BYTES = {GGML_Q4_K: 144, GGML_Q6_K: 210}
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -28,6 +32,11 @@ _SIGNATURES = {
     "hk_ggml_mul_mat_id": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp]),
     "hk_ggml_experts_destroy": (None, [_vp]),
     "hk_ggml_mul_mat_id_repeat": (ctypes.c_int, [_vp, _vp, _i64, ctypes.POINTER(ctypes.c_float)]),
+    "hk_ggml_dense_supported": (ctypes.c_int, [_i64, _i64, _i64]),
+    "hk_ggml_quant_supported": (ctypes.c_int, [ctypes.c_int, _i64]),
+    "hk_ggml_dense_create": (ctypes.c_int, [_vp, _i64, _i64, ctypes.POINTER(_vp)]),
+    "hk_ggml_quant_create": (ctypes.c_int, [ctypes.c_int, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
+    "hk_ggml_mul_mat": (ctypes.c_int, [_vp, _vp, _vp]),
     "coli_cuda_init": (ctypes.c_int, [_vp, ctypes.c_int]),
     "coli_cuda_shutdown": (None, []),
     "coli_cuda_available_device_count": (ctypes.c_int, []),
@@ -77,10 +86,28 @@ def ggml_supported(in_dim, out_dim, n_experts, n_ids, input_rows):
     return bool(lib().hk_ggml_experts_supported(in_dim, out_dim, n_experts, n_ids, input_rows))
 
 
-class GgmlExperts:
-    """One MUL_MAT_ID weight tensor, float32 [n_experts][out][in] on the host."""
+def dense_supported(in_dim, out_dim, input_rows=1):
+    return bool(lib().hk_ggml_dense_supported(in_dim, out_dim, input_rows))
 
-    def __init__(self, weights):
+
+def quant_supported(ggml_type, in_dim):
+    return bool(lib().hk_ggml_quant_supported(ggml_type, in_dim))
+
+
+class GgmlExperts:
+    """One GGML weight tensor on the device.
+
+    ``GgmlExperts(w)``: float32 [n_experts][out][in], requantised per row
+    (MUL_MAT_ID).  ``GgmlExperts.dense(w)``: float32 [out][in], one scale per
+    (row, 2048-column tile) (MUL_MAT).  ``GgmlExperts.quant(type, blocks,
+    n_experts, out, in)``: Q4_K / Q6_K blocks as GGML holds them (both).
+    """
+
+    def __init__(self, weights=None, *, _handle=None, _shape=None):
+        if _handle is not None:
+            self.handle = _handle
+            self.n_experts, self.out_dim, self.in_dim = _shape
+            return
         w = _f32(weights)
         if w.ndim != 3:
             raise ValueError("weights must be [n_experts][out][in]")
@@ -89,6 +116,35 @@ class GgmlExperts:
         hip.check(lib().hk_ggml_experts_create(w.ctypes.data, *w.shape, ctypes.byref(handle)),
                   "hk_ggml_experts_create")
         self.handle = handle.value
+
+    @classmethod
+    def dense(cls, weights):
+        w = _f32(weights)
+        if w.ndim != 2:
+            raise ValueError("weights must be [out][in]")
+        handle = _vp()
+        hip.check(lib().hk_ggml_dense_create(w.ctypes.data, w.shape[0], w.shape[1], ctypes.byref(handle)),
+                  "hk_ggml_dense_create")
+        return cls(_handle=handle.value, _shape=(1, w.shape[0], w.shape[1]))
+
+    @classmethod
+    def quant(cls, ggml_type, blocks, n_experts, out_dim, in_dim):
+        b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+        need = n_experts * out_dim * (in_dim // 256) * BLOCK_BYTES.get(ggml_type, 0)
+        if ggml_type in BLOCK_BYTES and in_dim % 256 == 0 and b.size != need:
+            raise ValueError(f"expected {need} bytes of blocks, got {b.size}")
+        handle = _vp()
+        hip.check(lib().hk_ggml_quant_create(ggml_type, b.ctypes.data, n_experts, out_dim, in_dim,
+                                             ctypes.byref(handle)), "hk_ggml_quant_create")
+        return cls(_handle=handle.value, _shape=(n_experts, out_dim, in_dim))
+
+    def mul_mat(self, x):
+        x = _f32(x).reshape(-1)
+        if x.size != self.in_dim:
+            raise ValueError("input length must equal in_dim")
+        out = np.empty(self.out_dim, dtype=np.float32)
+        hip.check(lib().hk_ggml_mul_mat(self.handle, x.ctypes.data, out.ctypes.data), "hk_ggml_mul_mat")
+        return out
 
     def mul_mat_id(self, inputs, ids):
         x = _f32(inputs).reshape(-1, self.in_dim)

@@ -15,7 +15,9 @@
  *    pack_expert, :692-735).  A GGML backend shim calls
  *    hk_ggml_experts_supported from supports_op, hk_ggml_experts_create once
  *    per weight tensor (dequantising it to float32 with ggml's to_float first)
- *    and hk_ggml_mul_mat_id from graph_compute.
+ *    and hk_ggml_mul_mat_id from graph_compute.  Q4_K and Q6_K tensors go to
+ *    hk_ggml_quant_create unchanged instead, and dense single-row MUL_MATs to
+ *    hk_ggml_dense_create / hk_ggml_quant_create and hk_ggml_mul_mat.
  *
  * 2. Colibri coli_cuda_* (colibri-xdna/backend/backend_xdna.cpp).  The
  *    symbols below keep Colibri's names and signatures, so a Colibri build
@@ -40,9 +42,14 @@
 extern "C" {
 #endif
 
-/* ---- GGML MUL_MAT_ID ---- */
+/* ---- GGML MUL_MAT_ID and MUL_MAT ---- */
 
 typedef struct hk_ggml_experts hk_ggml_experts;
+
+/* ggml_type values of the two block formats the reference's native kernels
+ * take (upstream ggml's enum ggml_type). */
+#define HK_GGML_Q4_K 12
+#define HK_GGML_Q6_K 14
 
 /* 1 when the shapes fit the contract (ggml-xdna.cpp:1681-1716: 0 < in, out
  * <= 2048; n_experts >= 8; 1 <= n_ids <= 8; input_rows 1 or n_ids), else 0.
@@ -59,19 +66,53 @@ int hk_ggml_experts_create(const float* weights, int64_t n_experts, int64_t out_
 /* out[slot][:] for slot < n_ids (host float32 [n_ids][out_dim]) from input
  * (host float32 [input_rows][in_dim]; row 0 for every slot when input_rows
  * is 1) and ids (host int32 [n_ids]); HK_ERR_INVALID for an id outside
- * [0, n_experts) (ggml-xdna.cpp:1301-1441). */
+ * [0, n_experts) (ggml-xdna.cpp:1301-1441).  Takes sets from
+ * hk_ggml_experts_create and hk_ggml_quant_create (dims <= 2048). */
 int hk_ggml_mul_mat_id(hk_ggml_experts* set, const float* input, int64_t input_rows, const int32_t* ids,
                        int64_t n_ids, float* out);
 
 void hk_ggml_experts_destroy(hk_ggml_experts* set);
+
+/* 1 when a dense single-row MUL_MAT fits the reference's dense offload
+ * (supports_dense_qwen, ggml-xdna.cpp:1718-1748: out_dim <= 32768, one input
+ * row), else 0. */
+int hk_ggml_dense_supported(int64_t in_dim, int64_t out_dim, int64_t input_rows);
+
+/* 1 when `ggml_type` is Q4_K or Q6_K and in_dim is a multiple of 256: the
+ * native-block path (supports_native_experts / supports_native_dense,
+ * ggml-xdna.cpp:967-993), else 0. */
+int hk_ggml_quant_supported(int ggml_type, int64_t in_dim);
+
+/* Dense MUL_MAT weights, float32 [out_dim][in_dim] (host), requantised to
+ * int8 with one scale per (row, 2048-column tile): the reference's dense
+ * tiles (pack_dense_tile, ggml-xdna.cpp:768-832).  Use with hk_ggml_mul_mat. */
+int hk_ggml_dense_create(const float* weights, int64_t out_dim, int64_t in_dim, hk_ggml_experts** out);
+
+/* GGML Q4_K or Q6_K weights as the tensor holds them: n_experts x out_dim
+ * rows of in_dim / 256 blocks (144 or 210 bytes each), back to back (host).
+ * They stay in block form on the device and are dequantised inside the dot
+ * product (npu_llm/kernels/project_q4k_bf16.cc:76-117,
+ * project_q6k_bf16.cc:53-99): per 2048-column tile bf16(sum_c w_c * bf16(x_c)),
+ * tiles summed in float32.  With n_experts > 1 and dims <= 2048 the set
+ * serves hk_ggml_mul_mat_id (compute_experts_native, ggml-xdna.cpp:1180-1299);
+ * with one matrix of up to 32768 rows, hk_ggml_mul_mat (compute_dense_native,
+ * :1101-1178). */
+int hk_ggml_quant_create(int ggml_type, const void* blocks, int64_t n_experts, int64_t out_dim, int64_t in_dim,
+                         hk_ggml_experts** out);
+
+/* out[out_dim] = W @ input[in_dim] for a dense set (host float32):
+ * ggml-xdna.cpp:1444-1538 (W8 tiles) and :1101-1178 (Q4_K / Q6_K). */
+int hk_ggml_mul_mat(hk_ggml_experts* set, const float* input, float* out);
 
 /* Measurement hook with no counterpart in the reference: after a successful
  * hk_ggml_mul_mat_id call on `set`, launches its kernel `launches` more times
  * back to back over the input that call left in device memory, launch i with
  * the n_ids expert ids ids[i * n_ids ...] (host int32 [launches][n_ids], n_ids
  * of that call), so a timing can rotate through more experts than the
- * caches hold.  Stores the average time per launch (HIP events) in
- * *ms_per_launch; the output of that call is overwritten. */
+ * caches hold.  The launches are captured into a HIP graph on a stream of
+ * their own and replayed between two events (with HK_EAGER=1 in the
+ * environment they are launched directly); stores the average time per
+ * launch in *ms_per_launch.  The output of that call is overwritten. */
 int hk_ggml_mul_mat_id_repeat(hk_ggml_experts* set, const int32_t* ids, int64_t launches, float* ms_per_launch);
 
 /* ---- Colibri ---- */

@@ -119,3 +119,76 @@ def tile_rounding_row():
     w[0, 2048], x[2048] = -127, 2
     w[0, 2049], x[2049] = -1, 1
     return w, x
+
+
+# ---- GGML Q4_K / Q6_K block writers ----
+#
+# Written from ggml's published block layouts (the reader under test is
+# oracle/experts.py), column by column:
+#   Q4_K (144 bytes): fp16 d, fp16 dmin, 12 bytes of 6-bit (scale, min) pairs
+#     for the eight 32-column sub-blocks, then 128 bytes of nibbles; column c
+#     sits in byte 16 + 32 * (c // 64) + c % 32, in the low nibble when
+#     c % 64 < 32, else the high nibble, and belongs to sub-block c // 32.
+#     Pairs 0..3 take the low 6 bits of bytes j (scale) and j + 4 (min);
+#     pairs 4..7 keep their low 4 bits in byte j + 4 (scale low, min high) and
+#     their top 2 bits in the top bits of bytes j - 4 (scale) and j (min).
+#   Q6_K (210 bytes): ql[128], qh[64], int8 scales[16], fp16 d; 6-bit q (the
+#     weight is d * scale * (q - 32)); column c in half h = c // 128, quarter
+#     k = (c % 128) // 32, l = c % 32: low 4 bits in ql[64 h + l + 32 (k & 1)]
+#     (low nibble for k < 2, else high), top 2 bits in bits 2k, 2k + 1 of
+#     qh[32 h + l]; scale index 8 h + (c % 128) // 16.
+
+def f16_bytes(value):
+    return np.frombuffer(np.float16(value).tobytes(), np.uint8)
+
+
+def q4k_block(d, dmin, sc, mn, q):
+    """One Q4_K block: sc, mn 8 values in 0..63, q 256 values in 0..15."""
+    b = np.zeros(144, np.uint8)
+    b[0:2], b[2:4] = f16_bytes(d), f16_bytes(dmin)
+    s = np.zeros(12, np.uint32)
+    for j in range(4):
+        s[j] |= sc[j] & 63
+        s[j + 4] |= mn[j] & 63
+    for j in range(4, 8):
+        s[j + 4] |= (sc[j] & 15) | ((mn[j] & 15) << 4)
+        s[j - 4] |= (sc[j] >> 4) << 6
+        s[j] |= (mn[j] >> 4) << 6
+    b[4:16] = s.astype(np.uint8)
+    for c in range(256):
+        i = 16 + 32 * (c // 64) + c % 32
+        b[i] |= (q[c] & 15) if c % 64 < 32 else (q[c] & 15) << 4
+    return b
+
+
+def q6k_block(d, sc, q):
+    """One Q6_K block: sc 16 int8 values, q 256 values in 0..63."""
+    b = np.zeros(210, np.uint8)
+    for c in range(256):
+        h, k, l = c // 128, (c % 128) // 32, c % 32
+        i = 64 * h + l + 32 * (k & 1)
+        b[i] |= (q[c] & 15) if k < 2 else (q[c] & 15) << 4
+        b[128 + 32 * h + l] |= (q[c] >> 4) << (2 * k)
+    b[192:208] = np.asarray(sc, np.int8).view(np.uint8)
+    b[208:210] = f16_bytes(d)
+    return b
+
+
+def _f16_pairs(values):
+    return np.asarray(values, np.float16).view(np.uint8).reshape(np.shape(values) + (2,))
+
+
+def random_q4k(rng, rows, cols):
+    """Random valid Q4_K rows: random quants, scales and mins; d, dmin small."""
+    nb = cols // 256
+    b = rng.integers(0, 256, (rows, nb, 144), dtype=np.uint8)
+    b[..., 0:2] = _f16_pairs(rng.uniform(0.002, 0.01, (rows, nb)))
+    b[..., 2:4] = _f16_pairs(rng.uniform(0.001, 0.01, (rows, nb)))
+    return b.reshape(-1)
+
+
+def random_q6k(rng, rows, cols):
+    nb = cols // 256
+    b = rng.integers(0, 256, (rows, nb, 210), dtype=np.uint8)
+    b[..., 208:210] = _f16_pairs(rng.uniform(0.0005, 0.002, (rows, nb)))
+    return b.reshape(-1)

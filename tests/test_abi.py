@@ -74,6 +74,11 @@ def test_expert_shim_validation_without_gpu_work():
     for bad in ((2049, 16, 8, 1, 1), (16, 2049, 8, 1, 1), (16, 16, 7, 1, 1), (16, 16, 8, 9, 9),
                 (16, 16, 8, 0, 1), (16, 16, 8, 4, 2), (0, 16, 8, 1, 1)):
         assert not experts.ggml_supported(*bad), bad
+    # dense and quantised paths (ggml-xdna.cpp:1718-1748, 967-993)
+    assert experts.dense_supported(18944, 3584) and experts.dense_supported(896, 32768)
+    assert not experts.dense_supported(896, 32769) and not experts.dense_supported(896, 10, 2)
+    assert experts.quant_supported(experts.GGML_Q4_K, 2048) and experts.quant_supported(experts.GGML_Q6_K, 256)
+    assert not experts.quant_supported(experts.GGML_Q4_K, 896) and not experts.quant_supported(13, 2048)
     # Colibri: nothing is up before coli_cuda_init, and a bad device list is refused
     assert lib.coli_cuda_device_count() == 0 and lib.coli_cuda_device_at(0) == -1
     assert lib.coli_cuda_init(None, 1) == 0
