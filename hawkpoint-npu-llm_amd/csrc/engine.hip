@@ -418,12 +418,15 @@ int dalloc(T** p, size_t count) {
   return 0;
 }
 
-constexpr int kPrefillRows = 512;  // tokens per prefill chunk
+// Tokens per prefill chunk: a whole 4096-token prompt is one chunk, so every
+// GEMM has (tokens / 64) x (outputs / 64) tiles to spread over the CUs.
+constexpr int kPrefillRows = 4096;
 
 int prefill_workspace(hk_engine* e) {
   if (e->pf_rows) return 0;
   const hk_model_desc& d = e->d;
-  const size_t r = kPrefillRows;
+  const int rows = std::min(kPrefillRows, (int)d.max_context);
+  const size_t r = rows;
   HK_TRY(dalloc(&e->pf_x, r * d.hidden));
   HK_TRY(dalloc(&e->pf_h1, r * d.hidden));
   HK_TRY(dalloc(&e->pf_xn, r * d.hidden));
@@ -432,7 +435,7 @@ int prefill_workspace(hk_engine* e) {
   HK_TRY(dalloc(&e->pf_att, r * d.q_heads * kHeadDim));
   HK_TRY(dalloc(&e->pf_act, r * d.intermediate));
   HK_TRY(dalloc(&e->pf_tokens, r));
-  e->pf_rows = kPrefillRows;
+  e->pf_rows = rows;
   return 0;
 }
 

@@ -218,134 +218,140 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(PrefillAttnArgs a
   }
 }
 
-// Causal GQA attention for token i (slot p = start + i) and KV head g, over
-// slots 0..p in chunks of 256.  One chunk: P = p / sum, then P @ V (NumPy's
-// order).  Several chunks: running max / sum / P@V with log-sum-exp rescaling.
+// Causal GQA attention for a block of 64 query tokens (token i at slot
+// p = start + i) of one query head, flash-style over the KV cache in blocks
+// of 64 slots (slots 0..p of each token; cpu_backend.py:110-129):
+//   S^T = K Q^T        v_mfma_f32_16x16x32_bf16: bf16 products are exact, f32 sums
+//   online softmax     per token: running max m and sum l, P = exp(S / 8 - m)
+//   O^T += V^T P^T     v_mfma_f32_16x16x4_f32: P stays float32, as in the
+//                      reference's NumPy softmax
+// and out = bf16(O / l).  Computing S^T rather than S leaves lane L holding
+// P[token L % 16][slots 16 sb + 4 (L / 16) + r], which is exactly the B
+// operand of the float32 MFMA when its k index L / 16 stands for slot
+// 16 sb + 4 (L / 16) + r; V^T is staged in LDS so that the matching A values
+// (4 consecutive slots of one dimension) are one 8-byte read.  Wave w owns
+// tokens 16 w .. 16 w + 15 of the block; all four share the K and V tiles.
+constexpr int kFaRows = 64;                 // query tokens per workgroup
+constexpr int kFaSlots = 64;                // KV slots per block
+constexpr int kFaKRow = kHeadDim + 8;       // bf16 per K row in LDS (padding)
+constexpr int kFaVRow = kFaSlots + 8;       // bf16 per V^T row in LDS
+
 __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttnArgs a) {
-  const int g = blockIdx.x;
-  const int i = blockIdx.y;
-  const int p = a.start + i;
-  const int qpk = a.q_heads / a.kv_heads;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int half = kHeadDim / 2;
-  const size_t head_base = (size_t)g * a.max_ctx;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kFaSlots][kFaKRow];  // [slot][dim]
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim][kFaVRow];  // [dim][slot]
+  const int h = blockIdx.x;
+  const int nblk = (a.n + kFaRows - 1) / kFaRows;
+  const int qb = nblk - 1 - (int)blockIdx.y;  // the longest blocks start first
+  const int g = h / (a.q_heads / a.kv_heads);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, quad = lane >> 4;
+  const int tok = qb * kFaRows + wave * 16 + col;  // this lane's token
+  const bool tok_ok = tok < a.n;
+  const int p = a.start + (tok_ok ? tok : 0);
+  const int last_slot = a.start + min(qb * kFaRows + kFaRows - 1, a.n - 1);
+  const int nkv = last_slot / kFaSlots + 1;
+  const size_t kv_base = (size_t)g * a.max_ctx;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
 
-  __shared__ float qs[kMaxQPerKV][kHeadDim];
-  __shared__ float sc[kMaxQPerKV][kAttnChunk];
-  __shared__ uint32_t vs[kAttnChunk][kHeadDim / 2];
-  __shared__ float hmax[kMaxQPerKV], hsum[kMaxQPerKV], hscale[kMaxQPerKV];
-  __shared__ float run_m[kMaxQPerKV], run_l[kMaxQPerKV];
+  // B operand of S^T = K Q^T: Q[tok][32 kk + 8 quad .. + 8]
+  bf16x8 qf[2];
+  {
+    const uint16_t* qrow = a.qrot + (size_t)(tok_ok ? tok : 0) * a.q_heads * kHeadDim + (size_t)h * kHeadDim + quad * 8;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, tok_ok ? load16(qrow + 32 * kk) : zero);
+  }
 
-  for (int e = tid; e < qpk * kHeadDim; e += kThreads) {
-    const int h = e / kHeadDim, d = e % kHeadDim;
-    qs[h][d] = bf16_to_f32(a.qrot[(size_t)i * a.q_heads * kHeadDim + (size_t)(g * qpk + h) * kHeadDim + d]);
-  }
-  if (tid < qpk) {
-    run_m[tid] = -INFINITY;
-    run_l[tid] = 0.0f;
-  }
-  const int nchunks = p / kAttnChunk + 1;
-  // running P@V: thread owns (head, dim pair) entries e = tid + k * 256
-  float o0[4] = {0.f, 0.f, 0.f, 0.f}, o1[4] = {0.f, 0.f, 0.f, 0.f};
-  const float scale = 1.0f / 8.0f;
-  for (int c = 0; c < nchunks; ++c) {
-    const int t0 = c * kAttnChunk;
-    const int n = min(kAttnChunk, p + 1 - t0);
-    __syncthreads();
-    for (int e = tid; e < n * (kHeadDim / 8); e += kThreads) {
-      const int t = e / (kHeadDim / 8), cc = e % (kHeadDim / 8);
-      const u32x4 w = load16(a.vcache + (head_base + t0 + t) * kHeadDim + cc * 8);
-      vs[t][cc * 4 + 0] = w.x;
-      vs[t][cc * 4 + 1] = w.y;
-      vs[t][cc * 4 + 2] = w.z;
-      vs[t][cc * 4 + 3] = w.w;
-    }
-    for (int e = tid; e < n * qpk; e += kThreads) {
-      const int t = e / qpk, h = e % qpk;
-      const uint16_t* kr = a.kcache + (head_base + t0 + t) * kHeadDim;
-      float dot = 0.0f;
+  // tile loads: thread t takes slot t / 4, dimensions 16 (t % 4) .. + 16 of K
+  // and V; slots past the block's last one read as zero
+  const int ls = tid >> 2, ld0 = (tid & 3) * 16;
+  u32x4 kr[2], vr[2];
+  auto load_tile = [&](int kb) {
+    const int slot = kb * kFaSlots + ls;
+    const bool ok = slot <= last_slot;
+    const size_t off = (kv_base + (ok ? slot : 0)) * kHeadDim + ld0;
+    kr[0] = ok ? load16(a.kcache + off) : zero;
+    kr[1] = ok ? load16(a.kcache + off + 8) : zero;
+    vr[0] = ok ? load16(a.vcache + off) : zero;
+    vr[1] = ok ? load16(a.vcache + off + 8) : zero;
+  };
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4 o[4];
 #pragma unroll
-      for (int cc = 0; cc < kHeadDim / 8; ++cc) {
-        const u32x4 w = load16(kr + cc * 8);
-        dot = fmaf(qs[h][cc * 8 + 0], bf_lo(w.x), dot);
-        dot = fmaf(qs[h][cc * 8 + 1], bf_hi(w.x), dot);
-        dot = fmaf(qs[h][cc * 8 + 2], bf_lo(w.y), dot);
-        dot = fmaf(qs[h][cc * 8 + 3], bf_hi(w.y), dot);
-        dot = fmaf(qs[h][cc * 8 + 4], bf_lo(w.z), dot);
-        dot = fmaf(qs[h][cc * 8 + 5], bf_hi(w.z), dot);
-        dot = fmaf(qs[h][cc * 8 + 6], bf_lo(w.w), dot);
-        dot = fmaf(qs[h][cc * 8 + 7], bf_hi(w.w), dot);
-      }
-      sc[h][t] = dot * scale;
-    }
-    __syncthreads();
-    for (int h = wave; h < qpk; h += kThreads / 64) {
-      float m = -INFINITY;
-      for (int t = lane; t < n; t += 64) m = fmaxf(m, sc[h][t]);
-      m = group_max<64>(m);
-      float sum = 0.0f;
-      for (int t = lane; t < n; t += 64) {
-        const float e = expf(sc[h][t] - m);
-        sc[h][t] = e;
-        sum += e;
-      }
-      sum = group_sum<64>(sum);
-      if (lane == 0) {
-        hmax[h] = m;
-        hsum[h] = sum;
-      }
-    }
-    __syncthreads();
-    if (nchunks == 1) {
-      for (int e = tid; e < qpk * n; e += kThreads) {
-        const int h = e / n, t = e % n;
-        sc[h][t] = sc[h][t] / hsum[h];
-      }
-    } else if (tid < qpk) {
-      // rescale factors for the running sums
-      const float mn = fmaxf(run_m[tid], hmax[tid]);
-      const float fo = expf(run_m[tid] - mn);  // 0 on the first chunk
-      const float fc = expf(hmax[tid] - mn);
-      run_l[tid] = fmaf(run_l[tid], fo, hsum[tid] * fc);
-      run_m[tid] = mn;
-      hscale[tid] = fo;
-      hsum[tid] = fc;  // reused: factor for this chunk's p @ V
-    }
-    __syncthreads();
+  for (int db = 0; db < 4; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  load_tile(0);
+  for (int kb = 0; kb < nkv; ++kb) {
+    __syncthreads();  // the previous tile has been read
+    *reinterpret_cast<u32x4*>(&Ks[ls][ld0]) = kr[0];
+    *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8]) = kr[1];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int e = tid + k * kThreads;
-      if (e >= qpk * half) break;
-      const int h = e / half, dp = e % half;
-      float c0 = 0.f, c1 = 0.f;
-      for (int t = 0; t < n; ++t) {
-        const uint32_t v2 = vs[t][dp];
-        c0 = fmaf(sc[h][t], bf_lo(v2), c0);
-        c1 = fmaf(sc[h][t], bf_hi(v2), c1);
-      }
-      if (nchunks == 1) {
-        o0[k] = c0;
-        o1[k] = c1;
-      } else {
-        o0[k] = fmaf(o0[k], hscale[h], c0 * hsum[h]);
-        o1[k] = fmaf(o1[k], hscale[h], c1 * hsum[h]);
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t w = (e < 8 ? vr[0] : vr[1])[(e & 7) >> 1];
+      Vt[ld0 + e][ls] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+    }
+    __syncthreads();
+    if (kb + 1 < nkv) load_tile(kb + 1);  // in flight during this tile's math
+
+    // S^T blocks: lane holds slots s0 + 16 sb + 4 quad + r of token `tok`
+    const int s0 = kb * kFaSlots;
+    f32x4 sv[4];
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      sv[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[16 * sb + col][32 * kk + 8 * quad]);
+        sv[sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[kk], sv[sb], 0, 0, 0);
       }
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int slot = s0 + 16 * sb + 4 * quad + r;
+        const float v = (tok_ok && slot <= p) ? sv[sb][r] * 0.125f : -INFINITY;  // 1 / sqrt(64)
+        sv[sb][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // a token with no live slot yet
+    const float alpha = expf(m_run - m_use);
+    float rs = 0.0f;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = expf(sv[sb][r] - m_use);
+        sv[sb][r] = e;
+        rs += e;
+      }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    // O^T[16 db + 4 quad + r][tok] += sum over the block's slots of V^T P^T
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint2 vv = *reinterpret_cast<const uint2*>(&Vt[16 * db + col][16 * sb + 4 * quad]);
+        const float v4[4] = {bf_lo(vv.x), bf_hi(vv.x), bf_lo(vv.y), bf_hi(vv.y)};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[r], sv[sb][r], o[db], 0, 0, 0);
+      }
   }
+  if (!tok_ok) return;
+  uint16_t* out = a.out + (size_t)tok * a.ld_out + (size_t)h * kHeadDim + 4 * quad;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int e = tid + k * kThreads;
-    if (e >= qpk * half) break;
-    const int h = e / half, dp = e % half;
-    float r0 = o0[k], r1 = o1[k];
-    if (nchunks > 1) {
-      r0 = r0 / run_l[h];
-      r1 = r1 / run_l[h];
-    }
-    uint32_t* out = reinterpret_cast<uint32_t*>(a.out + (size_t)i * a.ld_out +
-                                                (size_t)(g * qpk + h) * kHeadDim);
-    out[dp] = f32_to_bf16(r0) | (f32_to_bf16(r1) << 16);
+  for (int db = 0; db < 4; ++db) {
+    const uint32_t lo = f32_to_bf16(o[db][0] / l_run) | (f32_to_bf16(o[db][1] / l_run) << 16);
+    const uint32_t hi = f32_to_bf16(o[db][2] / l_run) | (f32_to_bf16(o[db][3] / l_run) << 16);
+    *reinterpret_cast<uint2*>(out + 16 * db) = make_uint2(lo, hi);
   }
 }
 
@@ -387,13 +393,14 @@ int launch_rmsnorm_rows(const uint16_t* X, int ldx, const uint16_t* gamma, float
 }
 
 int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream) {
-  if (a.q_heads % a.kv_heads != 0 || a.q_heads / a.kv_heads > kMaxQPerKV)
-    return fail("prefill attention: unsupported head grouping");
+  if (a.q_heads % a.kv_heads != 0) return fail("prefill attention: unsupported head grouping");
+  if (a.ld_out % 4 != 0) return fail("prefill attention: output rows must be 8-byte aligned");
   if (a.start < 0 || a.start + a.n > a.max_ctx) return fail("prefill attention: slots out of range");
   hipLaunchKernelGGL(rope_append_kernel, dim3(a.n), dim3(kThreads), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "rope append launch");
-  hipLaunchKernelGGL(attention_prefill_kernel, dim3(a.kv_heads, a.n), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(attention_prefill_kernel, dim3(a.q_heads, (a.n + kFaRows - 1) / kFaRows), dim3(kThreads), 0,
+                     stream, a);
   err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "prefill attention launch");
 }

@@ -105,11 +105,32 @@ def test_prefill_qwen_full_depth():
     _prefill_case(model, _prompt(151936, 40, 12), 4, 72, 2.5e-2, "qwen2.5-0.5b")
 
 
-def test_prefill_chunked_long_prompt():
-    """600 tokens: a 512-token chunk then an 88-token chunk that attends to it
-    (multi-chunk causal attention past 256 slots)."""
+def test_prefill_long_prompt():
+    """600 tokens: causal attention over ten 64-slot KV blocks, the last one
+    partly masked."""
     model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
     _prefill_case(model, _prompt(151936, 600, 14), 4, 1024, 1e-2, "qwen-2L-600")
+
+
+def test_prefill_longer_than_one_chunk():
+    """4200 tokens in one call run as a 4096-token chunk and a 104-token chunk
+    that attends to it; the same prompt split over two calls (1000 + 3200,
+    each a single chunk) must give the same logits and token."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("prefill over two chunks vs two calls, 4200 tokens")
+    model = SyntheticModel(QWEN25_05B, seed=6, layers=2)
+    prompt = _prompt(151936, 4200, 16)
+    engine = QwenDecoderEngine(model, context_length=8192)
+    try:
+        t_one, l_one = engine.prefill(prompt, 0)
+        engine.reset()
+        engine.prefill(prompt[:1000], 0, logits=False)
+        t_two, l_two = engine.prefill(prompt[1000:], 1000)
+        assert t_one == t_two
+        assert rel_l2(l_two, l_one) <= 1e-3
+    finally:
+        engine.close()
 
 
 def test_prefill_continues_from_cached_prefix():
