@@ -218,23 +218,166 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(PrefillAttnArgs a
   }
 }
 
+// Large-M GEMM (prompt chunks of 128+ tokens): a 256-thread workgroup owns
+// 128 tokens x BN outputs (for SwiGLU, BN gate and BN up rows); the waves
+// split it 2 x 2, so each owns 64 x BN/2 as 4 x BN/32 MFMA blocks (twice
+// that for SwiGLU).  K advances 64 at a time through two LDS buffers: the
+// next step's tiles are loaded into registers while this step's MFMAs run,
+// then written to the other buffer, so one barrier per step suffices.
+constexpr int kBM = 128;
+constexpr int kBK = 64;
+constexpr int kBRow = kBK + 8;  // bf16 per LDS row (rows 144 B apart: no bank conflicts)
+
+template <int BN, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
+  constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
+  constexpr int NB = BN / 32;             // 16-wide output blocks per wave
+  constexpr int AL = kBM * kBK / 8 / kThreads;  // 16-byte pieces per thread, A tile
+  constexpr int WL = WR * kBK / 8 / kThreads;   // and weight tile
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM][kBRow];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][WR][kBRow];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // Workgroups go to the 8 XCDs in turn (workgroup b to XCD b % 8).  Tile
+  // t = (b % 8) * per + b / 8 gives each XCD a contiguous run of tiles, and
+  // with token tiles varying fastest within the run, an XCD works through a
+  // few weight tiles only, which its own L2 keeps while it sweeps the tokens.
+  const int mt = (a.M + kBM - 1) / kBM, ntile = (a.N + BN - 1) / BN;
+  const int per = (mt * ntile + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (t >= mt * ntile) return;
+  const int m0 = (t % mt) * kBM, n0 = (t / mt) * BN;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * (BN / 2);
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+  // piece i of this thread: row tid / 8 + 32 i, k (tid % 8) * 8 of the tile
+  const int pr = tid >> 3, pk = (tid & 7) * 8;
+  const uint16_t* a_src[AL];
+  bool a_ok[AL];
+#pragma unroll
+  for (int i = 0; i < AL; ++i) {
+    const int m = m0 + pr + 32 * i;
+    a_ok[i] = m < a.M;
+    a_src[i] = a.A + (size_t)(a_ok[i] ? m : 0) * a.lda + pk;
+  }
+  const uint16_t* w_src[WL];
+  bool w_ok[WL];
+#pragma unroll
+  for (int i = 0; i < WL; ++i) {
+    const int r = pr + 32 * i;  // tile row: gate rows first, then up rows
+    const int n = n0 + (PAIR ? r % BN : r);
+    w_ok[i] = n < a.N;
+    w_src[i] = a.W + (size_t)((w_ok[i] ? n : 0) + (PAIR && r >= BN ? a.N : 0)) * a.K + pk;
+  }
+
+  u32x4 av[AL], wv[WL];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i) av[i] = a_ok[i] ? load16(a_src[i] + k0) : zero;
+#pragma unroll
+    for (int i = 0; i < WL; ++i) wv[i] = w_ok[i] ? load_stream16(w_src[i] + k0) : zero;
+  };
+  auto store = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i) *reinterpret_cast<u32x4*>(&As[b][pr + 32 * i][pk]) = av[i];
+#pragma unroll
+    for (int i = 0; i < WL; ++i) *reinterpret_cast<u32x4*>(&Ws[b][pr + 32 * i][pk]) = wv[i];
+  };
+
+  f32x4 acc[4][NB], accu[PAIR ? 4 : 1][PAIR ? NB : 1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (PAIR) accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  const int nk = a.K / kBK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int b = kt & 1;
+    if (kt + 1 < nk) load((kt + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK; ks += 32) {
+      bf16x8 af[4], bf[NB], uf[PAIR ? NB : 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(&As[b][wm + 16 * i + fr][ks + fk]);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        bf[j] = *reinterpret_cast<const bf16x8*>(&Ws[b][wn + 16 * j + fr][ks + fk]);
+        if constexpr (PAIR) uf[j] = *reinterpret_cast<const bf16x8*>(&Ws[b][BN + wn + 16 * j + fr][ks + fk]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          if constexpr (PAIR)
+            accu[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], uf[j], accu[i][j], 0, 0, 0);
+        }
+    }
+    if (kt + 1 < nk) store(b ^ 1);
+    __syncthreads();
+  }
+
+  // D layout: lane holds rows 4 (lane / 16) + r, column lane % 16 of each block
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
+        const int n = n0 + wn + 16 * j + fr;
+        if (m >= a.M || n >= a.N) continue;
+        const float v = acc[i][j][r];
+        uint16_t* y = a.Y + (size_t)m * a.ldy + n;
+        switch (a.epi) {
+          case EPI_BF16:
+            *y = (uint16_t)f32_to_bf16(v);
+            break;
+          case EPI_BIAS:
+            *y = (uint16_t)f32_to_bf16(round_bf16(v) + a.bias[n]);
+            break;
+          case EPI_RESID:
+            *y = (uint16_t)f32_to_bf16(round_bf16(v) + bf16_to_f32(a.resid[(size_t)m * a.ldr + n]));
+            break;
+          case EPI_SWIGLU:
+            if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(v), round_bf16(accu[i][j][r])));
+            break;
+          default:
+            break;
+        }
+      }
+}
+
 // Causal GQA attention for a block of 64 query tokens (token i at slot
 // p = start + i) of one query head, flash-style over the KV cache in blocks
-// of 64 slots (slots 0..p of each token; cpu_backend.py:110-129):
+// of 128 slots (slots 0..p of each token; cpu_backend.py:110-129):
 //   S^T = K Q^T        v_mfma_f32_16x16x32_bf16: bf16 products are exact, f32 sums
 //   online softmax     per token: running max m and sum l, P = exp(S / 8 - m)
-//   O^T += V^T P^T     v_mfma_f32_16x16x4_f32: P stays float32, as in the
-//                      reference's NumPy softmax
+//   O^T += V^T P^T     v_mfma_f32_16x16x32_bf16 twice, on P's top 16 bits
+//                      and on the remainder: about 16 significant bits of the
+//                      float32 P (the reference's NumPy softmax), at an
+//                      eighth of the cost of float32 MFMAs
 // and out = bf16(O / l).  Computing S^T rather than S leaves lane L holding
-// P[token L % 16][slots 16 sb + 4 (L / 16) + r], which is exactly the B
-// operand of the float32 MFMA when its k index L / 16 stands for slot
-// 16 sb + 4 (L / 16) + r; V^T is staged in LDS so that the matching A values
-// (4 consecutive slots of one dimension) are one 8-byte read.  Wave w owns
-// tokens 16 w .. 16 w + 15 of the block; all four share the K and V tiles.
+// P[token L % 16][slots 16 sb + 4 (L / 16) + r], which serves directly as the
+// B operand of P @ V once the MFMA's k index is read as the matching slot;
+// V^T is staged in LDS so that the A values (4 consecutive slots of one
+// dimension) are 8-byte reads.  Wave w owns tokens 16 w .. 16 w + 15 of the
+// block; all four share the K and V tiles.
 constexpr int kFaRows = 64;                 // query tokens per workgroup
-constexpr int kFaSlots = 64;                // KV slots per block
+constexpr int kFaSlots = 128;               // KV slots per block
 constexpr int kFaKRow = kHeadDim + 8;       // bf16 per K row in LDS (padding)
 constexpr int kFaVRow = kFaSlots + 8;       // bf16 per V^T row in LDS
+constexpr int kFaSB = kFaSlots / 16;        // 16-slot S^T blocks per KV block
+// exp(s / 8 - m) = exp2(s * log2(e) / 8 - m'): the scores are kept in base-2
+// units so that each exponential is one v_exp_f32
+constexpr float kFaScale = 0.125f * 1.4426950408889634f;
 
 __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kFaSlots][kFaKRow];  // [slot][dim]
@@ -261,18 +404,28 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     for (int kk = 0; kk < 2; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, tok_ok ? load16(qrow + 32 * kk) : zero);
   }
 
-  // tile loads: thread t takes slot t / 4, dimensions 16 (t % 4) .. + 16 of K
-  // and V; slots past the block's last one read as zero
-  const int ls = tid >> 2, ld0 = (tid & 3) * 16;
-  u32x4 kr[2], vr[2];
+  // tile loads; slots past the block's last one read as zero.  K: thread t
+  // takes slot t / 2, dimensions 32 (t % 2) .. + 32.  V: thread t takes the
+  // slot pair 2 (t % 64), + 1 and dimensions 16 (t / 64) .. + 16, so that it
+  // writes V^T as 32-bit words (two slots of one dimension), a wave's 64
+  // threads covering 64 consecutive words of one V^T row
+  const int ls = tid >> 1, ld0 = (tid & 1) * 32;
+  const int vp = tid & 63, vd = (tid >> 6) * 16;
+  u32x4 kr[4], vr[4];
   auto load_tile = [&](int kb) {
     const int slot = kb * kFaSlots + ls;
     const bool ok = slot <= last_slot;
     const size_t off = (kv_base + (ok ? slot : 0)) * kHeadDim + ld0;
-    kr[0] = ok ? load16(a.kcache + off) : zero;
-    kr[1] = ok ? load16(a.kcache + off + 8) : zero;
-    vr[0] = ok ? load16(a.vcache + off) : zero;
-    vr[1] = ok ? load16(a.vcache + off + 8) : zero;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kr[i] = ok ? load16(a.kcache + off + 8 * i) : zero;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int vs = kb * kFaSlots + 2 * vp + j;
+      const bool vok = vs <= last_slot;
+      const size_t voff = (kv_base + (vok ? vs : 0)) * kHeadDim + vd;
+      vr[2 * j] = vok ? load16(a.vcache + voff) : zero;
+      vr[2 * j + 1] = vok ? load16(a.vcache + voff + 8) : zero;
+    }
   };
 
   float m_run = -INFINITY, l_run = 0.0f;
@@ -282,21 +435,22 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
   load_tile(0);
   for (int kb = 0; kb < nkv; ++kb) {
     __syncthreads();  // the previous tile has been read
-    *reinterpret_cast<u32x4*>(&Ks[ls][ld0]) = kr[0];
-    *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8]) = kr[1];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t w = (e < 8 ? vr[0] : vr[1])[(e & 7) >> 1];
-      Vt[ld0 + e][ls] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8 * i]) = kr[i];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {  // dimension vd + d of slots 2 vp, 2 vp + 1
+      const uint32_t w0 = vr[d >> 3][(d & 7) >> 1], w1 = vr[2 + (d >> 3)][(d & 7) >> 1];
+      const uint32_t pair = (d & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u)) : ((w0 & 0xffffu) | (w1 << 16));
+      *reinterpret_cast<uint32_t*>(&Vt[vd + d][2 * vp]) = pair;
     }
     __syncthreads();
     if (kb + 1 < nkv) load_tile(kb + 1);  // in flight during this tile's math
 
     // S^T blocks: lane holds slots s0 + 16 sb + 4 quad + r of token `tok`
     const int s0 = kb * kFaSlots;
-    f32x4 sv[4];
+    f32x4 sv[kFaSB];
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
+    for (int sb = 0; sb < kFaSB; ++sb) {
       sv[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
@@ -306,11 +460,11 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb)
+    for (int sb = 0; sb < kFaSB; ++sb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int slot = s0 + 16 * sb + 4 * quad + r;
-        const float v = (tok_ok && slot <= p) ? sv[sb][r] * 0.125f : -INFINITY;  // 1 / sqrt(64)
+        const float v = (tok_ok && slot <= p) ? sv[sb][r] * kFaScale : -INFINITY;
         sv[sb][r] = v;
         mx = fmaxf(mx, v);
       }
@@ -318,13 +472,13 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // a token with no live slot yet
-    const float alpha = expf(m_run - m_use);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float rs = 0.0f;
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb)
+    for (int sb = 0; sb < kFaSB; ++sb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float e = expf(sv[sb][r] - m_use);
+        const float e = __builtin_amdgcn_exp2f(sv[sb][r] - m_use);
         sv[sb][r] = e;
         rs += e;
       }
@@ -334,16 +488,35 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     m_run = m_new;
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] *= alpha;
-    // O^T[16 db + 4 quad + r][tok] += sum over the block's slots of V^T P^T
+    // O^T[16 db + 4 quad + r][tok] += sum over the block's slots of V^T P^T,
+    // 32 slots per bf16 MFMA: k index 8 quad + e stands for slot
+    // 32 t + 16 (e / 4) + 4 quad + e % 4, the 8 P values this lane holds for
+    // blocks 2t, 2t + 1.  P (finite, in [0, 1]) goes in as two bf16 terms:
+    // hi, its top 16 bits, and lo, the top 16 bits of the exact remainder
+    // P - hi; together they carry about 16 significant bits.
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb)
+    for (int t = 0; t < kFaSB / 2; ++t) {
+      uint32_t ph[4], pl[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = sv[2 * t + (e >> 2)][e & 3], p1 = sv[2 * t + (e >> 2)][(e & 3) + 1];
+        const uint32_t u0 = __float_as_uint(p0) & 0xffff0000u, u1 = __float_as_uint(p1) & 0xffff0000u;
+        const uint32_t r0 = __float_as_uint(p0 - __uint_as_float(u0));
+        const uint32_t r1 = __float_as_uint(p1 - __uint_as_float(u1));
+        ph[e >> 1] = (u0 >> 16) | u1;
+        pl[e >> 1] = (r0 >> 16) | (r1 & 0xffff0000u);
+      }
+      const bf16x8 phi = __builtin_bit_cast(bf16x8, u32x4{ph[0], ph[1], ph[2], ph[3]});
+      const bf16x8 plo = __builtin_bit_cast(bf16x8, u32x4{pl[0], pl[1], pl[2], pl[3]});
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const uint2 vv = *reinterpret_cast<const uint2*>(&Vt[16 * db + col][16 * sb + 4 * quad]);
-        const float v4[4] = {bf_lo(vv.x), bf_hi(vv.x), bf_lo(vv.y), bf_hi(vv.y)};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[r], sv[sb][r], o[db], 0, 0, 0);
+        const uint2 v0 = *reinterpret_cast<const uint2*>(&Vt[16 * db + col][32 * t + 4 * quad]);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(&Vt[16 * db + col][32 * t + 16 + 4 * quad]);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{v0.x, v0.y, v1.x, v1.y});
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo, o[db], 0, 0, 0);
       }
+    }
   }
   if (!tok_ok) return;
   uint16_t* out = a.out + (size_t)tok * a.ld_out + (size_t)h * kHeadDim + 4 * quad;
@@ -369,10 +542,24 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     grid.y = (a.max_rows + kTM - 1) / kTM;
     grid.z = a.max_groups;
   }
-  if (a.epi == EPI_SWIGLU)
+  const bool pair = a.epi == EPI_SWIGLU;
+  if (a.grp_count == nullptr && a.M >= kBM && a.K % kBK == 0) {
+    // 128-token tiles; 128-wide outputs only when that still gives 512 tiles
+    const int mt = (a.M + kBM - 1) / kBM;
+    const bool wide = !pair && mt * ((a.N + 127) / 128) >= 512;
+    const int bn = wide ? 128 : 64;
+    const dim3 g(8 * ((mt * ((a.N + bn - 1) / bn) + 7) / 8));
+    if (pair)
+      hipLaunchKernelGGL((gemm_big_kernel<64, true>), g, dim3(kThreads), 0, stream, a);
+    else if (wide)
+      hipLaunchKernelGGL((gemm_big_kernel<128, false>), g, dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gemm_big_kernel<64, false>), g, dim3(kThreads), 0, stream, a);
+  } else if (pair) {
     hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a);
-  else
+  } else {
     hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a);
+  }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "prefill gemm launch");
 }

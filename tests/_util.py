@@ -55,5 +55,9 @@ def check_bf16(y_bits, ref_bits, sum_bound, exact_frac=0.97):
 
     y = bf16.from_bits(y_bits).astype(np.float64)
     ref = bf16.from_bits(ref_bits).astype(np.float64)
-    assert np.all(np.abs(y - ref) <= ulp_bf16(ref) + 2 * sum_bound)
-    assert (np.asarray(y_bits) == np.asarray(ref_bits)).mean() >= exact_frac
+    excess = np.abs(y - ref) - (ulp_bf16(ref) + 2 * sum_bound)
+    worst = np.unravel_index(np.argmax(excess), excess.shape)
+    assert np.all(excess <= 0), (f"{int((excess > 0).sum())} outside the bound; worst at {worst}: "
+                                 f"got {y[worst]!r}, want {ref[worst]!r}")
+    exact = (np.asarray(y_bits) == np.asarray(ref_bits)).mean()
+    assert exact >= exact_frac, f"only {exact:.4f} bit-exact"
