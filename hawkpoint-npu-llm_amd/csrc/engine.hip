@@ -173,6 +173,8 @@ struct hk_engine {
   uint16_t* pf_att = nullptr;  // attention output [rows, Hq * 64]
   uint16_t* pf_act = nullptr;  // SwiGLU output [rows, I]
   int32_t* pf_tokens = nullptr;
+  float* pf_split = nullptr;   // split-K partial sums for prompts of up to kSplitRowsMax tokens
+  size_t pf_split_floats = 0;
 };
 
 namespace {
@@ -405,7 +407,7 @@ void free_engine(hk_engine* e) {
                   e->normed,  e->logits,   e->kcache,   e->vcache,     e->partial,
                   e->counters, e->keys,    e->ctrl,     e->out_tokens, e->result,
                   e->pf_x,    e->pf_h1,    e->pf_xn,    e->pf_qkv,     e->pf_q,
-                  e->pf_att,  e->pf_act,   e->pf_tokens, e->players, e->psync, e->ptag};
+                  e->pf_att,  e->pf_act,   e->pf_tokens, e->pf_split, e->players, e->psync, e->ptag};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -435,6 +437,12 @@ int prefill_workspace(hk_engine* e) {
   HK_TRY(dalloc(&e->pf_att, r * d.q_heads * kHeadDim));
   HK_TRY(dalloc(&e->pf_act, r * d.intermediate));
   HK_TRY(dalloc(&e->pf_tokens, r));
+  const int QD = d.q_heads * kHeadDim, m = std::min(rows, kSplitRowsMax);
+  e->pf_split_floats = std::max({split_ws_need(m, e->qkv_rows, d.hidden, false),
+                                 split_ws_need(m, d.hidden, QD, false),
+                                 split_ws_need(m, d.intermediate, d.hidden, true),
+                                 split_ws_need(m, d.hidden, d.intermediate, false)});
+  HK_TRY(dalloc(&e->pf_split, e->pf_split_floats));
   e->pf_rows = rows;
   return 0;
 }
@@ -459,6 +467,8 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     q.N = e->qkv_rows;
     q.K = H;
     q.epi = lw.qkv_bias ? EPI_BIAS : EPI_BF16;
+    q.split_ws = e->pf_split;
+    q.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(q, s));
     PrefillAttnArgs at = {};
     at.qkv = e->pf_qkv;
@@ -488,6 +498,8 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     o.N = H;
     o.K = QD;
     o.epi = EPI_RESID;
+    o.split_ws = e->pf_split;
+    o.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(o, s));
     HK_TRY(launch_rmsnorm_rows(e->pf_h1, H, lw.post_attn_norm, d.rms_eps, e->pf_xn, H, n, H, s));
     PrefillGemmArgs g = {};
@@ -500,6 +512,8 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     g.N = I;
     g.K = H;
     g.epi = EPI_SWIGLU;
+    g.split_ws = e->pf_split;
+    g.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(g, s));
     PrefillGemmArgs dn = {};
     dn.A = e->pf_act;
@@ -513,6 +527,8 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     dn.N = H;
     dn.K = I;
     dn.epi = EPI_RESID;
+    dn.split_ws = e->pf_split;
+    dn.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(dn, s));
   }
   return 0;

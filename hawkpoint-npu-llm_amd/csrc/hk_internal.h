@@ -175,7 +175,18 @@ struct PrefillGemmArgs {
   long long w_stride;
   int max_groups;         // grid size in z
   int max_rows;           // rows per group bound (grid size in y = ceil / 64)
+  // Optional float32 workspace for short prompts (M <= kSplitRowsMax): K is
+  // split across workgroups that write partial sums here, and a second
+  // kernel adds them up and applies the epilogue.
+  float* split_ws;
+  size_t split_ws_floats;
 };
+
+constexpr int kSplitRowsMax = 64;   // prompt rows that take the split-K path
+constexpr int kSplitTarget = 256;   // workgroups the split aims for
+// float32 workspace the split-K path needs for an M x N GEMM (2N outputs
+// with SwiGLU) with K columns: one M x outputs slice per K part.
+size_t split_ws_need(int M, int N, int K, bool pair);
 
 int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream);
 

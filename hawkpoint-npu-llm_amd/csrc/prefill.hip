@@ -16,6 +16,8 @@
 // a 64-token x 64-output tile (two weight tiles for SwiGLU pairs); each wave
 // owns a 32x32 quarter as 2x2 MFMA blocks.  K advances 32 at a time through
 // LDS; A and W tiles arrive with one 16-byte load per thread each.
+#include <algorithm>
+
 #include "hk_common.h"
 #include "hk_internal.h"
 
@@ -228,26 +230,41 @@ constexpr int kBM = 128;
 constexpr int kBK = 64;
 constexpr int kBRow = kBK + 8;  // bf16 per LDS row (rows 144 B apart: no bank conflicts)
 
-template <int BN, bool PAIR>
+// SPLIT (short prompts, BM = 64): workgroup (x, y) takes output tile x and
+// the y-th of gridDim.y runs of K steps, and stores float32 partial sums to
+// split_ws[y][m][outputs] (SwiGLU: up outputs at N + n) for
+// split_reduce_kernel.
+template <int BM, int BN, bool PAIR, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
   constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
+  constexpr int MB = BM / 32;             // 16-row blocks per wave
   constexpr int NB = BN / 32;             // 16-wide output blocks per wave
-  constexpr int AL = kBM * kBK / 8 / kThreads;  // 16-byte pieces per thread, A tile
-  constexpr int WL = WR * kBK / 8 / kThreads;   // and weight tile
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM][kBRow];
+  constexpr int AL = BM * kBK / 8 / kThreads;  // 16-byte pieces per thread, A tile
+  constexpr int WL = WR * kBK / 8 / kThreads;  // and weight tile
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][kBRow];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][WR][kBRow];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // Workgroups go to the 8 XCDs in turn (workgroup b to XCD b % 8).  Tile
-  // t = (b % 8) * per + b / 8 gives each XCD a contiguous run of tiles, and
-  // with token tiles varying fastest within the run, an XCD works through a
-  // few weight tiles only, which its own L2 keeps while it sweeps the tokens.
-  const int mt = (a.M + kBM - 1) / kBM, ntile = (a.N + BN - 1) / BN;
-  const int per = (mt * ntile + 7) / 8;
-  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-  if (t >= mt * ntile) return;
-  const int m0 = (t % mt) * kBM, n0 = (t / mt) * BN;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * (BN / 2);
+  const int mt = (a.M + BM - 1) / BM, ntile = (a.N + BN - 1) / BN;
+  int m0, n0, kt0 = 0, kt1 = a.K / kBK;
+  if constexpr (SPLIT) {
+    m0 = 0;
+    n0 = blockIdx.x * BN;
+    const int per = (kt1 + gridDim.y - 1) / gridDim.y;
+    kt0 = blockIdx.y * per;
+    kt1 = min(kt1, kt0 + per);
+  } else {
+    // Workgroups go to the 8 XCDs in turn (workgroup b to XCD b % 8).  Tile
+    // t = (b % 8) * per + b / 8 gives each XCD a contiguous run of tiles, and
+    // with token tiles varying fastest within the run, an XCD works through a
+    // few weight tiles only, which its own L2 keeps while it sweeps the tokens.
+    const int per = (mt * ntile + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (t >= mt * ntile) return;
+    m0 = (t % mt) * BM;
+    n0 = (t / mt) * BN;
+  }
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
@@ -285,34 +302,35 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
     for (int i = 0; i < WL; ++i) *reinterpret_cast<u32x4*>(&Ws[b][pr + 32 * i][pk]) = wv[i];
   };
 
-  f32x4 acc[4][NB], accu[PAIR ? 4 : 1][PAIR ? NB : 1];
+  f32x4 acc[MB][NB], accu[PAIR ? MB : 1][PAIR ? NB : 1];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (PAIR) accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  const int nk = a.K / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int b = kt & 1;
-    if (kt + 1 < nk) load((kt + 1) * kBK);
+  if (kt0 < kt1) {  // always true: split_parts leaves no part empty
+    load(kt0 * kBK);
+    store(0);
+    __syncthreads();
+  }
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int b = (kt - kt0) & 1;
+    if (kt + 1 < kt1) load((kt + 1) * kBK);
 #pragma unroll
     for (int ks = 0; ks < kBK; ks += 32) {
-      bf16x8 af[4], bf[NB], uf[PAIR ? NB : 1];
+      bf16x8 af[MB], bf[NB], uf[PAIR ? NB : 1];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(&As[b][wm + 16 * i + fr][ks + fk]);
+      for (int i = 0; i < MB; ++i) af[i] = *reinterpret_cast<const bf16x8*>(&As[b][wm + 16 * i + fr][ks + fk]);
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
         bf[j] = *reinterpret_cast<const bf16x8*>(&Ws[b][wn + 16 * j + fr][ks + fk]);
         if constexpr (PAIR) uf[j] = *reinterpret_cast<const bf16x8*>(&Ws[b][BN + wn + 16 * j + fr][ks + fk]);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
@@ -320,13 +338,13 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
             accu[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], uf[j], accu[i][j], 0, 0, 0);
         }
     }
-    if (kt + 1 < nk) store(b ^ 1);
+    if (kt + 1 < kt1) store(b ^ 1);
     __syncthreads();
   }
 
   // D layout: lane holds rows 4 (lane / 16) + r, column lane % 16 of each block
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
@@ -335,6 +353,13 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
         const int n = n0 + wn + 16 * j + fr;
         if (m >= a.M || n >= a.N) continue;
         const float v = acc[i][j][r];
+        if constexpr (SPLIT) {
+          const int outs = PAIR ? 2 * a.N : a.N;
+          float* part = a.split_ws + ((size_t)blockIdx.y * a.M + m) * outs;
+          part[n] = v;
+          if constexpr (PAIR) part[a.N + n] = accu[i][j][r];
+          continue;
+        }
         uint16_t* y = a.Y + (size_t)m * a.ldy + n;
         switch (a.epi) {
           case EPI_BF16:
@@ -353,6 +378,48 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
             break;
         }
       }
+}
+
+// Sum of the split-K partial sums of output (m, n) in slice order, then the
+// epilogue of the GEMM (the same rounding points as gemm_big_kernel's).
+__global__ __launch_bounds__(kThreads) void split_reduce_kernel(PrefillGemmArgs a, int parts) {
+  const int e = blockIdx.x * kThreads + threadIdx.x;
+  if (e >= a.M * a.N) return;
+  const int m = e / a.N, n = e % a.N;
+  const bool pair = a.epi == EPI_SWIGLU;
+  const int outs = pair ? 2 * a.N : a.N;
+  float v = 0.0f, u = 0.0f;
+  for (int s = 0; s < parts; ++s) {
+    const float* part = a.split_ws + ((size_t)s * a.M + m) * outs;
+    v += part[n];
+    if (pair) u += part[a.N + n];
+  }
+  uint16_t* y = a.Y + (size_t)m * a.ldy + n;
+  switch (a.epi) {
+    case EPI_BF16:
+      *y = (uint16_t)f32_to_bf16(v);
+      break;
+    case EPI_BIAS:
+      *y = (uint16_t)f32_to_bf16(round_bf16(v) + a.bias[n]);
+      break;
+    case EPI_RESID:
+      *y = (uint16_t)f32_to_bf16(round_bf16(v) + bf16_to_f32(a.resid[(size_t)m * a.ldr + n]));
+      break;
+    case EPI_SWIGLU:
+      *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(v), round_bf16(u)));
+      break;
+    default:
+      break;
+  }
+}
+
+// K parts of the split path: about kSplitTarget workgroups, every part
+// holding ceil(nk / parts) steps or, the last, fewer but at least one.
+int split_parts(int N, int K) {
+  const int ntile = (N + 63) / 64, nk = K / kBK;
+  const int want = std::max(1, std::min(nk, (kSplitTarget + ntile - 1) / ntile));
+  const int per = (nk + want - 1) / want;
+  return (nk + per - 1) / per;
 }
 
 // Causal GQA attention for a block of 64 query tokens (token i at slot
@@ -530,6 +597,10 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
 
 }  // namespace
 
+size_t split_ws_need(int M, int N, int K, bool pair) {
+  return (size_t)split_parts(N, K) * M * (pair ? 2 * N : N);
+}
+
 int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0) return fail("prefill gemm: sizes must be positive");
   if (a.K % kTK != 0) return fail("prefill gemm: K must be a multiple of 32");
@@ -543,6 +614,22 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     grid.z = a.max_groups;
   }
   const bool pair = a.epi == EPI_SWIGLU;
+  if (a.grp_count == nullptr && a.split_ws != nullptr && a.M <= kSplitRowsMax && a.K % kBK == 0 &&
+      split_ws_need(a.M, a.N, a.K, pair) <= a.split_ws_floats) {
+    // short prompt: 64-token tiles, K split over ~kSplitTarget workgroups
+    const int parts = split_parts(a.N, a.K);
+    const dim3 g((a.N + 63) / 64, parts);
+    if (pair)
+      hipLaunchKernelGGL((gemm_big_kernel<64, 64, true, true>), g, dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gemm_big_kernel<64, 64, false, true>), g, dim3(kThreads), 0, stream, a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "split gemm launch");
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((a.M * a.N + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                       stream, a, parts);
+    err = hipGetLastError();
+    return err == hipSuccess ? 0 : hip_fail(err, "split reduce launch");
+  }
   if (a.grp_count == nullptr && a.M >= kBM && a.K % kBK == 0) {
     // 128-token tiles; 128-wide outputs only when that still gives 512 tiles
     const int mt = (a.M + kBM - 1) / kBM;
@@ -550,11 +637,11 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     const int bn = wide ? 128 : 64;
     const dim3 g(8 * ((mt * ((a.N + bn - 1) / bn) + 7) / 8));
     if (pair)
-      hipLaunchKernelGGL((gemm_big_kernel<64, true>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, true, false>), g, dim3(kThreads), 0, stream, a);
     else if (wide)
-      hipLaunchKernelGGL((gemm_big_kernel<128, false>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 128, false, false>), g, dim3(kThreads), 0, stream, a);
     else
-      hipLaunchKernelGGL((gemm_big_kernel<64, false>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, false, false>), g, dim3(kThreads), 0, stream, a);
   } else if (pair) {
     hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a);
   } else {
