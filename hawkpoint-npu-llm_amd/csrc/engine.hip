@@ -173,7 +173,7 @@ struct hk_engine {
   uint16_t* pf_att = nullptr;  // attention output [rows, Hq * 64]
   uint16_t* pf_act = nullptr;  // SwiGLU output [rows, I]
   int32_t* pf_tokens = nullptr;
-  float* pf_split = nullptr;   // split-K partial sums for prompts of up to kSplitRowsMax tokens
+  float* pf_split = nullptr;   // split-K partial sums of GEMMs with few tiles
   size_t pf_split_floats = 0;
 };
 
@@ -437,11 +437,14 @@ int prefill_workspace(hk_engine* e) {
   HK_TRY(dalloc(&e->pf_att, r * d.q_heads * kHeadDim));
   HK_TRY(dalloc(&e->pf_act, r * d.intermediate));
   HK_TRY(dalloc(&e->pf_tokens, r));
-  const int QD = d.q_heads * kHeadDim, m = std::min(rows, kSplitRowsMax);
-  e->pf_split_floats = std::max({split_ws_need(m, e->qkv_rows, d.hidden, false),
-                                 split_ws_need(m, d.hidden, QD, false),
-                                 split_ws_need(m, d.intermediate, d.hidden, true),
-                                 split_ws_need(m, d.hidden, d.intermediate, false)});
+  // the largest split workspace any chunk length up to `rows` asks for
+  const int QD = d.q_heads * kHeadDim;
+  e->pf_split_floats = 1;
+  for (int m = 1; m <= rows; ++m)
+    e->pf_split_floats = std::max({e->pf_split_floats, split_ws_need(m, e->qkv_rows, d.hidden, false),
+                                   split_ws_need(m, d.hidden, QD, false),
+                                   split_ws_need(m, d.intermediate, d.hidden, true),
+                                   split_ws_need(m, d.hidden, d.intermediate, false)});
   HK_TRY(dalloc(&e->pf_split, e->pf_split_floats));
   e->pf_rows = rows;
   return 0;

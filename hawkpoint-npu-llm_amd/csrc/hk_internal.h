@@ -175,17 +175,19 @@ struct PrefillGemmArgs {
   long long w_stride;
   int max_groups;         // grid size in z
   int max_rows;           // rows per group bound (grid size in y = ceil / 64)
-  // Optional float32 workspace for short prompts (M <= kSplitRowsMax): K is
-  // split across workgroups that write partial sums here, and a second
-  // kernel adds them up and applies the epilogue.
+  // Optional float32 workspace: when the GEMM has too few tiles to fill the
+  // GPU (short prompts, narrow outputs), K is split across workgroups that
+  // write partial sums here, and a second kernel adds them up in order and
+  // applies the epilogue.  Without it (or when it is too small) the GEMM runs
+  // unsplit.
   float* split_ws;
   size_t split_ws_floats;
 };
 
-constexpr int kSplitRowsMax = 64;   // prompt rows that take the split-K path
-constexpr int kSplitTarget = 256;   // workgroups the split aims for
+constexpr int kSplitTarget = 256;  // workgroups the split aims for
 // float32 workspace the split-K path needs for an M x N GEMM (2N outputs
-// with SwiGLU) with K columns: one M x outputs slice per K part.
+// with SwiGLU) with K columns: one M x outputs slice per K part (0 when
+// the GEMM is not split).
 size_t split_ws_need(int M, int N, int K, bool pair);
 
 int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream);

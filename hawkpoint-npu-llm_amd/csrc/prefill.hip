@@ -230,10 +230,10 @@ constexpr int kBM = 128;
 constexpr int kBK = 64;
 constexpr int kBRow = kBK + 8;  // bf16 per LDS row (rows 144 B apart: no bank conflicts)
 
-// SPLIT (short prompts, BM = 64): workgroup (x, y) takes output tile x and
-// the y-th of gridDim.y runs of K steps, and stores float32 partial sums to
-// split_ws[y][m][outputs] (SwiGLU: up outputs at N + n) for
-// split_reduce_kernel.
+// SPLIT (too few tiles to fill the GPU): workgroup (x, y) takes tile x
+// (token tiles varying fastest) and the y-th of gridDim.y runs of K steps,
+// and stores float32 partial sums to split_ws[y][m][outputs] (SwiGLU: up
+// outputs at N + n) for split_reduce_kernel.
 template <int BM, int BN, bool PAIR, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
   constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
@@ -248,8 +248,8 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
   const int mt = (a.M + BM - 1) / BM, ntile = (a.N + BN - 1) / BN;
   int m0, n0, kt0 = 0, kt1 = a.K / kBK;
   if constexpr (SPLIT) {
-    m0 = 0;
-    n0 = blockIdx.x * BN;
+    m0 = (blockIdx.x % mt) * BM;
+    n0 = (blockIdx.x / mt) * BN;
     const int per = (kt1 + gridDim.y - 1) / gridDim.y;
     kt0 = blockIdx.y * per;
     kt1 = min(kt1, kt0 + per);
@@ -413,11 +413,18 @@ __global__ __launch_bounds__(kThreads) void split_reduce_kernel(PrefillGemmArgs 
   }
 }
 
-// K parts of the split path: about kSplitTarget workgroups, every part
-// holding ceil(nk / parts) steps or, the last, fewer but at least one.
-int split_parts(int N, int K) {
-  const int ntile = (N + 63) / 64, nk = K / kBK;
-  const int want = std::max(1, std::min(nk, (kSplitTarget + ntile - 1) / ntile));
+// Token rows per tile: 64 for prompts that fit one such tile, else kBM.
+int split_bm(int M) { return M <= 64 ? 64 : kBM; }
+
+// Tiles of the un-split GEMM (64-wide outputs).
+int gemm_tiles(int M, int N) { return ((M + split_bm(M) - 1) / split_bm(M)) * ((N + 63) / 64); }
+
+// K parts of the split path: enough that the tiles times the parts reach
+// about kSplitTarget workgroups, every part holding ceil(nk / parts) steps
+// or, the last, fewer but at least one.  1 means no split.
+int split_parts(int M, int N, int K) {
+  const int tiles = gemm_tiles(M, N), nk = K / kBK;
+  const int want = std::max(1, std::min(nk, (kSplitTarget + tiles - 1) / tiles));
   const int per = (nk + want - 1) / want;
   return (nk + per - 1) / per;
 }
@@ -598,7 +605,8 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
 }  // namespace
 
 size_t split_ws_need(int M, int N, int K, bool pair) {
-  return (size_t)split_parts(N, K) * M * (pair ? 2 * N : N);
+  const int parts = split_parts(M, N, K);
+  return parts > 1 ? (size_t)parts * M * (pair ? 2 * N : N) : 0;
 }
 
 int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
@@ -614,15 +622,21 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     grid.z = a.max_groups;
   }
   const bool pair = a.epi == EPI_SWIGLU;
-  if (a.grp_count == nullptr && a.split_ws != nullptr && a.M <= kSplitRowsMax && a.K % kBK == 0 &&
+  if (a.grp_count == nullptr && a.split_ws != nullptr && a.K % kBK == 0 && split_parts(a.M, a.N, a.K) > 1 &&
       split_ws_need(a.M, a.N, a.K, pair) <= a.split_ws_floats) {
-    // short prompt: 64-token tiles, K split over ~kSplitTarget workgroups
-    const int parts = split_parts(a.N, a.K);
-    const dim3 g((a.N + 63) / 64, parts);
-    if (pair)
-      hipLaunchKernelGGL((gemm_big_kernel<64, 64, true, true>), g, dim3(kThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((gemm_big_kernel<64, 64, false, true>), g, dim3(kThreads), 0, stream, a);
+    // too few tiles to fill the GPU: K split over ~kSplitTarget workgroups
+    const int parts = split_parts(a.M, a.N, a.K);
+    const dim3 g(gemm_tiles(a.M, a.N), parts);
+    if (split_bm(a.M) == 64) {
+      if (pair)
+        hipLaunchKernelGGL((gemm_big_kernel<64, 64, true, true>), g, dim3(kThreads), 0, stream, a);
+      else
+        hipLaunchKernelGGL((gemm_big_kernel<64, 64, false, true>), g, dim3(kThreads), 0, stream, a);
+    } else if (pair) {
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, true, true>), g, dim3(kThreads), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, false, true>), g, dim3(kThreads), 0, stream, a);
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "split gemm launch");
     hipLaunchKernelGGL(split_reduce_kernel, dim3((a.M * a.N + kThreads - 1) / kThreads), dim3(kThreads), 0,

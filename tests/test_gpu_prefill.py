@@ -121,8 +121,11 @@ def test_prefill_long_prompt():
 
 def test_prefill_longer_than_one_chunk():
     """4200 tokens in one call run as a 4096-token chunk and a 104-token chunk
-    that attends to it; the same prompt split over two calls (1000 + 3200,
-    each a single chunk) must give the same logits and token."""
+    that attends to it; the same prompt over two calls (1000 + 3200, each a
+    single chunk) must agree.  The GEMMs split K only when a chunk has too few
+    tiles, so the two runs sum some projections in different orders: they
+    are held to the float tolerance of the decode path (rel-L2 <= 1e-2) and
+    the same greedy token unless the top two logits nearly tie."""
     from runtime.qwen_engine import QwenDecoderEngine
 
     announce("prefill over two chunks vs two calls, 4200 tokens")
@@ -134,8 +137,10 @@ def test_prefill_longer_than_one_chunk():
         engine.reset()
         engine.prefill(prompt[:1000], 0, logits=False)
         t_two, l_two = engine.prefill(prompt[1000:], 1000)
-        assert t_one == t_two
-        assert rel_l2(l_two, l_one) <= 1e-3
+        err = rel_l2(l_two, l_one)
+        announce(f"  one call vs two calls: rel-L2 {err:.3e}, tokens {t_one} / {t_two}")
+        assert err <= 1e-2
+        assert t_one == t_two or near_tie(l_one)
     finally:
         engine.close()
 
