@@ -313,9 +313,16 @@ def main():
     long_decode = RUN / (time.perf_counter() - t0)
     log(f"ctx 4096: prefill {long_n} tokens {t_long * 1e3:.1f} ms "
         f"({long_flops / t_long / 1e12:.1f} TFLOP/s), decode {long_decode:.1f} tok/s")
+    # which step kernel ran at the timed positions (both share one contract)
+    split = engine.step_kind(end_pos) == "xcd_split"
     engine.close()
+    if split:
+        kernel_name = "decode_step_xa_kernel (attention block on XCD 0, MLP on XCDs 1-7)"
+        tfile = ROOT / "profiles" / "traffic_decode_step_xcd_split_qwen05b.json"
+    else:
+        kernel_name = "decode_step_kernel"
+        tfile = ROOT / "profiles" / "traffic_decode_step_qwen05b.json"
     traffic = None
-    tfile = ROOT / "profiles" / "traffic_decode_step_qwen05b.json"
     if tfile.is_file():
         # HBM bytes per launch from the committed rocprofv3 --pmc runs
         traffic = json.loads(tfile.read_text()).get("traffic_bytes_per_launch")
@@ -365,7 +372,7 @@ def main():
         "per_kernel_path_us": {k: round(v, 3) for k, v in parts.items()},
         "roofline": {
             "bound": "hbm",
-            "kernel": f"decode_step_kernel, one launch per token (bytes/launch {dom_bytes} at "
+            "kernel": f"{kernel_name}, one launch per token (bytes/launch {dom_bytes} at "
             f"position {end_pos})",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

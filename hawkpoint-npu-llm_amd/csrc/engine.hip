@@ -156,6 +156,11 @@ struct hk_engine {
   int32_t* result = nullptr;      // [2]: last argmax token, persistent-step error word
   // whole step in one persistent launch (persistent.hip); -1: per-kernel graph
   int pshape = -1;
+  // the step may also run split by XCD (attention block on XCD 0); it does so
+  // while the context is short enough for one attention task per workgroup
+  // there, judged by next_pos, the position the next launch decodes
+  bool xcd_split = false;
+  int next_pos = 0;
   PersistentLayer* players = nullptr;  // device copy of the layer pointers
   unsigned int spin_limit = kPersistentSpinLimit;
   unsigned int* psync = nullptr;       // per-workgroup epochs
@@ -289,6 +294,13 @@ int launch_part(hk_engine* e, int part, int l) {
   }
 }
 
+// Whether a persistent launch at `position` runs split by XCD.
+bool split_at(const hk_engine* e, int position) {
+  return e->xcd_split &&
+         e->d.q_heads * (position / kPersistentChunk + 1) <= persistent_split_tasks_max();
+}
+bool split_step(const hk_engine* e) { return split_at(e, e->next_pos); }
+
 int launch_persistent(hk_engine* e, bool head) {
   const hk_model_desc& d = e->d;
   PersistentArgs a = {};
@@ -323,7 +335,7 @@ int launch_persistent(hk_engine* e, bool head) {
   a.progress = e->psync;
   a.error = reinterpret_cast<unsigned int*>(e->result + 1);
   a.spin_limit = e->spin_limit;
-  return launch_persistent_step(e->pshape, a, e->stream);
+  return launch_persistent_step(e->pshape, a, e->stream, split_step(e));
 }
 
 size_t psync_words(const hk_engine*) { return (size_t)kPersistentGrid * kFlagStride; }
@@ -339,6 +351,9 @@ size_t ptag_words(const hk_engine* e) {
 // clean, and report it.
 int check_persistent(hk_engine* e, const int32_t* result_host) {
   if (e->pshape < 0 || result_host[1] == 0) return 0;
+  // a split launch also leaves when a workgroup finds itself on another XCD
+  // than the split assumes: later steps run undivided
+  e->xcd_split = false;
   HK_CHECK(hipStreamSynchronize(e->stream));
   HK_CHECK(hipMemset(e->psync, 0, psync_words(e) * sizeof(unsigned int)));
   HK_CHECK(hipMemset(e->ptag, 0, ptag_words(e) * sizeof(uint32_t)));
@@ -393,6 +408,7 @@ int set_ctrl_keep(hk_engine* e) {
 }
 
 int set_ctrl(hk_engine* e, int32_t token, int32_t position, int32_t advance) {
+  e->next_pos = position;
   hipLaunchKernelGGL(set_ctrl_kernel, dim3(1), dim3(1), 0, e->stream, e->ctrl, token, position,
                      advance);
   HK_CHECK(hipGetLastError());
@@ -640,6 +656,13 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     // (a small value forces the abandon path, for tests of it)
     if (const char* spin = getenv("HK_PERSISTENT_SPIN"))
       e->spin_limit = (unsigned int)strtoul(spin, nullptr, 10);
+    // HK_XCD_SPLIT: 0 off, 1 required (creation fails with the reason when
+    // the device cannot run it), unset: on where the device allows it
+    const char* split = getenv("HK_XCD_SPLIT");
+    if (e->pshape >= 0 && !(split && split[0] == '0')) {
+      e->xcd_split = persistent_xcd_split(e->pshape, e->stream) == 1;
+      if (!e->xcd_split && split && split[0] == '1') return HK_ERR_INVALID;
+    }
     if (e->pshape >= 0) {
       std::vector<PersistentLayer> pl(d.layers);
       for (int l = 0; l < d.layers; ++l) {
@@ -710,7 +733,11 @@ int hk_engine_generate(hk_engine* e, int32_t token, int32_t position, int32_t n_
   if (token < 0 || token >= e->d.vocab) return fail("token id outside the vocabulary");
   HK_CHECK(hipSetDevice(e->device));
   HK_TRY(set_ctrl(e, token, position, 1));
-  for (int i = 0; i < n_steps; ++i) HK_TRY(run_step(e, true));
+  for (int i = 0; i < n_steps; ++i) {
+    e->next_pos = position + i;
+    HK_TRY(run_step(e, true));
+  }
+  e->next_pos = position + n_steps;
   int32_t result[2] = {0, 0};
   HK_CHECK(hipMemcpyAsync(tokens_host, e->out_tokens, (size_t)n_steps * sizeof(int32_t),
                           hipMemcpyDeviceToHost, e->stream));
@@ -792,7 +819,8 @@ int hk_engine_launch_part_repeat(hk_engine* e, int32_t part, int32_t count) {
   if (count <= 0 || count > 100000) return fail("hk_engine_launch_part_repeat: count out of range");
   HK_CHECK(hipSetDevice(e->device));
   if (part >= HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
-  const long long key = (long long)part << 32 | (unsigned)count;
+  const long long key = (long long)part << 32 | (unsigned)count |
+                        (part == HK_PART_STEP && e->pshape >= 0 && split_step(e) ? 1LL << 62 : 0);
   auto it = e->repeat_graphs.find(key);
   if (it == e->repeat_graphs.end()) {
     hipGraph_t graph = nullptr;
@@ -863,6 +891,14 @@ int hk_engine_reset(hk_engine* e) {
 }
 
 void* hk_engine_stream(hk_engine* e) { return e ? (void*)e->stream : nullptr; }
+
+int hk_engine_step_kind(hk_engine* e, int32_t position, int32_t* kind_out) {
+  if (!e || !kind_out) return fail("hk_engine_step_kind: null argument");
+  if (position < 0 || position >= e->d.max_context)
+    return fail("position outside the " + std::to_string(e->d.max_context) + "-token context");
+  *kind_out = e->pshape < 0 ? HK_STEP_KERNELS : split_at(e, position) ? HK_STEP_XCD_SPLIT : HK_STEP_PERSISTENT;
+  return HK_OK;
+}
 
 void hk_engine_destroy(hk_engine* e) {
   if (!e) return;

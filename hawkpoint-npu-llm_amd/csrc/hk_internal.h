@@ -150,7 +150,16 @@ constexpr unsigned kPersistentSpinLimit = 1u << 20;
 
 // Model shapes the persistent step is compiled for (-1: use the per-kernel step).
 int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bool w8);
-int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream);
+// 1 when the step of this shape can also run split by XCD (attention block on
+// XCD 0, MLP on the others) on the current device; else 0 with the reason in
+// hk_last_error().  Runs a small probe kernel on `stream` and waits for it.
+int persistent_xcd_split(int shape, hipStream_t stream);
+// Attention tasks per layer up to which the XCD split keeps one task per
+// workgroup of XCD 0 (query heads x 256-slot chunks); beyond it the split is
+// correct but slower than the undivided step.
+int persistent_split_tasks_max();
+int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream,
+                           bool xcd_split = false);
 
 // ---- batched prefill (prefill.hip) ----
 

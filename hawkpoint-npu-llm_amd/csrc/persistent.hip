@@ -67,6 +67,14 @@ constexpr int kGroupsPV = kPT / kHalf;    // slot groups of the P @ V loop
 constexpr int kSlotsPV = kChunk / kGroupsPV;  // consecutive slots per group
 constexpr int kPartStride = kHeadDim + 2;
 constexpr int kSc1 = 16;                  // buffer-load cache policy: device scope (sc1)
+// Cache policy of hand-offs inside one XCD: loads with sc0|nt miss the CU's
+// L1 and read the XCD's shared L2, which every CU of the XCD writes through
+// to; stores use the default policy (0) and stay in that L2.
+constexpr int kLocal = 3;
+// MI355X: 8 XCDs of 32 CUs; workgroup i of a one-per-CU launch runs on XCD
+// i % 8 (the XCD split checks this against the XCC_ID register).
+constexpr int kXcds = 8;
+constexpr int kXcdWg = kPersistentGrid / kXcds;
 static_assert(2 * kChunk == kPT, "two threads per attention slot");
 
 // ---- device-coherent accesses ----
@@ -210,6 +218,21 @@ struct Shape {
   // in every phase between the write of its raw residual copy and its use
   static_assert(no <= nq && nd <= ng && no <= ng && nd <= nq && nd <= no,
                 "residual copies need nested producer sets");
+  // XCD split (decode_step_xa_kernel): the attention block runs on the
+  // kXcdWg workgroups of XCD 0 (QKV rows in slots 0.., O rows after them),
+  // the MLP on the other XCDs (gate/up pairs in slots 0.., down rows after)
+  static constexpr int kAW = kXcdWg * kCW, kMW = (kPersistentGrid - kXcdWg) * kCW;
+  static constexpr PhaseCfg xq = pick_cfg(QKV, H, false, kAW, kPf / 2);
+  static constexpr PhaseCfg xo = pick_cfg(H, AO, false, kAW, kPf / 2);
+  static constexpr PhaseCfg xg = pick_cfg(I, H, true, kMW, kPf / 2);
+  static constexpr PhaseCfg xd = pick_cfg(H, I, false, kMW, kPf - 2 * xg.nj);
+  static constexpr int xnq = producers(xq, QKV), xno = producers(xo, H);
+  static constexpr int xng = producers(xg, I), xnd = producers(xd, H);
+  // O rows take their residual from the Q stagers' copy of h, down rows from
+  // the gate/up stagers' copy of h1
+  static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr && xd.lpr && xq.nj + xo.nj <= kPf &&
+                             2 * xg.nj + xd.nj <= kPf && xno <= xnq && xnd <= xng &&
+                             xnq <= kXcdWg && xng <= kPersistentGrid - kXcdWg;
 };
 
 struct PShared {
@@ -247,9 +270,17 @@ __device__ __forceinline__ bool give_up(const PersistentArgs& a) {
 }
 
 // Poll one tagged word until it carries `tag`; false when the launch is abandoned.
-__device__ bool poll_word(const PersistentArgs& a, const uint32_t* p, unsigned tag, uint32_t& out) {
+// The word is p, also reachable as byte `off` of the buffer `r` (used by the
+// XCD-local policy, whose loads go through a buffer resource).
+template <int POL>
+__device__ bool poll_word(const PersistentArgs& a, const uint32_t* p, unsigned tag, uint32_t& out,
+                          __amdgpu_buffer_rsrc_t r, unsigned off) {
   for (unsigned spins = 1;; ++spins) {
-    const uint32_t w = ld_c32(p);
+    uint32_t w;
+    if constexpr (POL == kSc1)
+      w = ld_c32(p);
+    else
+      w = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
     if ((w >> 16) == tag) {
       out = w;
       return true;
@@ -315,7 +346,7 @@ __device__ __forceinline__ void wait_vm() {
 // the job on all waves.  False when abandoned.
 constexpr int kBatch = 10;
 
-template <int K, bool NORM, bool RAW>
+template <int K, bool NORM, bool RAW, int POL = kSc1>
 __device__ bool stage_wave(Ctx& c, const uint32_t* src, unsigned tag, const uint16_t* gamma,
                            uint16_t* xs, float* raw) {
   const PersistentArgs& a = *c.a;
@@ -350,7 +381,7 @@ __device__ bool stage_wave(Ctx& c, const uint32_t* src, unsigned tag, const uint
       for (int j = 0; j < B; ++j)
         if ((pending >> j) & 1u)
           v[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src, K * 4), first * 16,
-                                                       (j0 + j) * STRIDE * 16, kSc1);
+                                                       (j0 + j) * STRIDE * 16, POL);
 #pragma unroll
       for (int j = 0; j < B; ++j)
         if (((pending >> j) & 1u) && (v[j].x >> 16) == tag && (v[j].y >> 16) == tag &&
@@ -462,15 +493,22 @@ __device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const uint16_t* W, in
   }
 }
 
+// Eight bf16 products of a weight chunk and an x chunk, into two float32
+// accumulators.  v_dot2_f32_bf16 multiplies the packed halves (bf16 x bf16
+// is exact in float32) and adds both products to the accumulator: one VALU
+// instruction per two weights and no unpacking, where separate FMAs take
+// two shifts/masks and two FMAs -- the dot products are VALU-bound on the
+// critical path of every phase.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x), c,
+                                         false);
+}
 __device__ __forceinline__ void fma8(const u32x4 w, const u32x4 x, float& a0, float& a1) {
-  a0 = fmaf(bf_lo(w.x), bf_lo(x.x), a0);
-  a1 = fmaf(bf_hi(w.x), bf_hi(x.x), a1);
-  a0 = fmaf(bf_lo(w.y), bf_lo(x.y), a0);
-  a1 = fmaf(bf_hi(w.y), bf_hi(x.y), a1);
-  a0 = fmaf(bf_lo(w.z), bf_lo(x.z), a0);
-  a1 = fmaf(bf_hi(w.z), bf_hi(x.z), a1);
-  a0 = fmaf(bf_lo(w.w), bf_lo(x.w), a0);
-  a1 = fmaf(bf_hi(w.w), bf_hi(x.w), a1);
+  a0 = dot2(w.x, x.x, a0);
+  a1 = dot2(w.y, x.y, a1);
+  a0 = dot2(w.z, x.z, a0);
+  a1 = dot2(w.w, x.w, a1);
 }
 
 // Dot products of the prefetched row group with the staged x; every lane of
@@ -512,7 +550,9 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 // ---- attention task: query head h, slots [s * kChunk, ...] of layer l ----
-template <class S>
+// POL: cache policy of the q/k/v polls and the output store (kSc1 across
+// the device, kLocal when producers and consumers share an XCD).
+template <class S, int POL = kSc1>
 __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_q,
                                unsigned tag_a) {
   const PersistentArgs& a = *c.a;
@@ -553,12 +593,14 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
 
   const int qr = h * kHeadDim, kr = (S::HQ + g) * kHeadDim, vr = (S::HQ + S::HKV + g) * kHeadDim;
   const uint32_t* tq = a.tqkv;
+  const __amdgpu_buffer_rsrc_t tqr = rsrc(a.tqkv, S::QKV * 4);
   bool ok = true;
   // the slot-p value word of the P @ V loop, for the group holding slot p
   if (p - t0 - gi * kSlotsPV >= 0 && p - t0 - gi * kSlotsPV < kSlotsPV) {
     const int kp = p - t0 - gi * kSlotsPV;
     uint32_t lo = 0, hi = 0;
-    ok = poll_word(a, tq + vr + 2 * dp, tag_q, lo) && poll_word(a, tq + vr + 2 * dp + 1, tag_q, hi);
+    ok = poll_word<POL>(a, tq + vr + 2 * dp, tag_q, lo, tqr, (vr + 2 * dp) * 4) &&
+         poll_word<POL>(a, tq + vr + 2 * dp + 1, tag_q, hi, tqr, (vr + 2 * dp + 1) * 4);
     const uint32_t word = (lo & 0xffffu) | (hi << 16);
 #pragma unroll
     for (int k = 0; k < kSlotsPV; ++k)
@@ -569,11 +611,13 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   if (tid < 2 * kHalf && ok) {
     const int j = tid & (kHalf - 1);
     const bool is_k = tid >= kHalf;
-    const uint32_t* src = tq + (is_k ? kr : qr);
+    const int src_row = is_k ? kr : qr;
+    const uint32_t* src = tq + src_row;
     const float cs = ldg(a.cos_tab + (size_t)p * kHalf + j);
     const float sn = ldg(a.sin_tab + (size_t)p * kHalf + j);
     uint32_t w1 = 0, w2 = 0;
-    ok = poll_word(a, src + j, tag_q, w1) && poll_word(a, src + j + kHalf, tag_q, w2);
+    ok = poll_word<POL>(a, src + j, tag_q, w1, tqr, (src_row + j) * 4) &&
+         poll_word<POL>(a, src + j + kHalf, tag_q, w2, tqr, (src_row + j + kHalf) * 4);
     const float x1 = bf_lo(w1), x2 = bf_lo(w2);
     const uint32_t r1 = f32_to_bf16(x1 * cs - x2 * sn);
     const uint32_t r2 = f32_to_bf16(x2 * cs + x1 * sn);
@@ -582,7 +626,8 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     dst[j + kHalf] = bf16_to_f32(r2);
     if (is_k && holds_new && h % S::QPK == 0 && ok) {
       uint32_t v1 = 0, v2 = 0;
-      ok = poll_word(a, tq + vr + j, tag_q, v1) && poll_word(a, tq + vr + j + kHalf, tag_q, v2);
+      ok = poll_word<POL>(a, tq + vr + j, tag_q, v1, tqr, (vr + j) * 4) &&
+           poll_word<POL>(a, tq + vr + j + kHalf, tag_q, v2, tqr, (vr + j + kHalf) * 4);
       uint16_t* kd = a.kcache + (head_base + p) * kHeadDim;
       uint16_t* vd = a.vcache + (head_base + p) * kHeadDim;
       stg(kd + j, (uint16_t)r1);
@@ -675,8 +720,15 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     for (int k = 0; k < kGroupsPV; ++k) o += acc[k * kHeadDim + tid];
   }
   uint32_t* out = a.tattn + (size_t)h * kHeadDim;
+  // the head's output words; XCD-local stores go through a buffer resource
+  auto store_out = [&](uint32_t v) {
+    if constexpr (POL == kSc1)
+      st_c32(out + tid, v);
+    else
+      __builtin_amdgcn_raw_buffer_store_b32(v, rsrc(a.tattn, S::AO * 4), (h * kHeadDim + tid) * 4, 0, 0);
+  };
   if (nsplit == 1) {
-    if (tid < kHeadDim) st_c32(out + tid, tagged(f32_to_bf16(o), tag_a));
+    if (tid < kHeadDim) store_out(tagged(f32_to_bf16(o), tag_a));
     return true;
   }
 
@@ -706,7 +758,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
       lsum = fmaf(ld_cf(pj + kHeadDim + 1), f, lsum);
       r = fmaf(ld_cf(pj + tid), f, r);
     }
-    st_c32(out + tid, tagged(f32_to_bf16(r / lsum), tag_a));
+    store_out(tagged(f32_to_bf16(r / lsum), tag_a));
   }
   if (tid == 0)
     (void)__hip_atomic_exchange(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -714,7 +766,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
 }
 
 // Publish one GEMV phase's outputs.  Each compute wave parks its rows'
-// tagged words in LDS; the last of the seven to arrive stores the workgroup's
+// tagged words in LDS; the last of the kCW to arrive stores the workgroup's
 // rows (contiguous: kCW * RPW of them from `first`) with one instruction, so a
 // cache line of outputs has a few writers instead of one per wave -- that is
 // what makes it visible to the pollers quickly.  Every compute wave issues
@@ -724,7 +776,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
 // gathered store has been issued before it goes on to issue weight loads:
 // the CU's memory pipeline is in order, so the store must not queue behind
 // tens of kilobytes of prefetch.
-template <int RPW>
+template <int RPW, int POL = kSc1>
 __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t word, bool row_lead,
                                              __amdgpu_buffer_rsrc_t tagged_buf, unsigned first,
                                              int valid_rows, unsigned pad, bool then_load) {
@@ -744,8 +796,8 @@ __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t wor
       dst = first + c.lane;
     }
   }
-  // device-coherent (sc1) like st_c32
-  __builtin_amdgcn_raw_buffer_store_b32(v, tagged_buf, dst * 4u, 0, kSc1);
+  // device-coherent (sc1) like st_c32, or XCD-local (the default policy)
+  __builtin_amdgcn_raw_buffer_store_b32(v, tagged_buf, dst * 4u, 0, POL == kSc1 ? kSc1 : 0);
   if (!producer) return;
   const unsigned done = old - old % kCW + kCW;
   if (old % kCW == kCW - 1) {
@@ -760,173 +812,22 @@ __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t wor
   }
 }
 
-// ---- the step kernel ----
+// LM head over all eight waves, double-buffered row groups, then the argmax
+// over the workgroups' keys on workgroup 0 (shared by both step kernels).
+// `buf` is the free LDS staging buffer, `ep_layers` the epoch of the last
+// layer's down phase.
 template <class S>
-__global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
-  __shared__ PShared sm;
-  Ctx c;
-  c.a = &args;
-  c.sm = &sm;
-  c.wg = blockIdx.x;
-  c.wave = threadIdx.x >> 6;
-  c.lane = threadIdx.x & 63;
-  c.gw = c.wg * kCW + c.wave;
+__device__ __forceinline__ void lm_head_phase(Ctx& c, u32x4 (&pf)[kPf], int buf, unsigned ep_layers,
+                                              unsigned* my_flag, int p) {
+  const PersistentArgs& a = *c.a;
+  PShared& sm = *c.sm;
   const bool stager = c.wave >= kCW;
-  if (threadIdx.x == 0) {
-    sm.abort = 0;
-    sm.out_count = 0;
-    sm.out_stored = 0;
-  }
-
-  const PersistentArgs& a = args;
-  const int L = a.layers;
-  static_assert(sizeof(PersistentLayer) % 8 == 0, "layer table is copied in 8-byte words");
-  {
-    constexpr int kWords = sizeof(PersistentLayer) / 8;
-    const unsigned long long* src = reinterpret_cast<const unsigned long long*>(a.w);
-    unsigned long long* dst = reinterpret_cast<unsigned long long*>(sm.layers);
-    for (int i = threadIdx.x; i < L * kWords; i += kPT) dst[i] = ldg(src + i);
-  }
-  __syncthreads();
-  unsigned* my_flag = a.progress + (size_t)c.wg * kFlagStride;
-  const unsigned base = ld_c32(my_flag);  // the epoch this workgroup ended the last launch on
-  const int token = ldg(&a.ctrl->token);
-  const int p = ldg(&a.ctrl->position);
-  // layer 0 reads the embedding row, or the hidden state the host preloaded
-  const uint16_t* x0 = token >= 0 ? a.embed + (size_t)min(token, a.vocab - 1) * S::H : a.h;
-  const bool is_q = c.wg < S::nq, is_o = c.wg < S::no, is_g = c.wg < S::ng, is_d = c.wg < S::nd;
-  const int tasks = S::HQ * (p / kChunk + 1);
-
-  // Row of this lane in each GEMV phase.  Every compute wave stores once per
-  // phase: a row it does not own (or a phase its workgroup sits out) goes to
-  // the wave's own pad word, so all compute waves issue the same stores.
-  // publish targets as word offsets in the one tagged-activation allocation
-  // (h, h1, qkv, attn, act, then one pad word per wave)
-  const unsigned o_h = 0, o_h1 = (unsigned)(a.th1 - a.th), o_qkv = (unsigned)(a.tqkv - a.th);
-  const unsigned o_act = (unsigned)(a.tact - a.th), o_pad = (unsigned)(a.pad - a.th);
-  const __amdgpu_buffer_rsrc_t tbuf = rsrc(a.th, (int)(o_pad + kPersistentGrid * kPW) * 4);
-  const unsigned pad = o_pad + c.wg * kPW + c.wave;
-  const int row_q = c.gw * (64 / S::q.lpr) + c.lane / S::q.lpr;
-  const int row_o = c.gw * (64 / S::o.lpr) + c.lane / S::o.lpr;
-  const int row_g = c.gw * (64 / S::g.lpr) + c.lane / S::g.lpr;
-  const int row_d = c.gw * (64 / S::d.lpr) + c.lane / S::d.lpr;
-  // first row of this workgroup in each phase and how many of its rows exist
-  constexpr int RQ = 64 / S::q.lpr, RO = 64 / S::o.lpr, RG = 64 / S::g.lpr, RD = 64 / S::d.lpr;
-  const int fq = c.wg * kCW * RQ, fo = c.wg * kCW * RO, fg = c.wg * kCW * RG, fd = c.wg * kCW * RD;
-  const int nvq = S::QKV - fq, nvo = S::H - fo, nvg = S::I - fg, nvd = S::H - fd;
-  const bool lq = c.lane % S::q.lpr == 0, lo = c.lane % S::o.lpr == 0;
-  const bool lg = c.lane % S::g.lpr == 0, ld = c.lane % S::d.lpr == 0;
-  const unsigned dst_h = is_d && row_d < S::H ? (unsigned)row_d * 2u : kOutside;  // byte offset in h
-  const int res_o = min(row_o, S::H - 1), res_d = min(row_d, S::H - 1);
-  const unsigned bias_off = is_q && !stager && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
-  // Every wave issues every weight prefetch (the stager's, like those of
-  // workgroups that sit a phase out, read zero from outside the resource):
-  // a prefetch skipped on one path would keep the registers' previous values
-  // live around the whole layer loop.
-  const bool pq = is_q && !stager, po = is_o && !stager, pg = is_g && !stager, pd = is_d && !stager;
-
-  u32x4 pf[kPf];
-  float acc, accu, bias_q = 0.0f;
-  int buf = 0;  // LDS staging buffer of the next GEMV phase
-  prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
-  bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         rsrc(sm.layers[0].qkv_bias, S::QKV * 4), bias_off, 0, 0));
-
-  // The stager fills xs[buf]; the barrier hands it to the compute waves.
-  // Returns false (in every wave) when the launch is abandoned.
+  float acc, accu;
   auto handoff = [&](bool ok) -> bool {
     if (stager && c.lane == 0 && !ok) sm.abort = 1;
     __syncthreads();
     return sm.abort == 0;
   };
-
-  for (int l = 0; l < L; ++l) {
-    const PersistentLayer& lw = sm.layers[l];
-    const unsigned ep = base + 5u * (unsigned)l;  // epoch of the previous layer's down phase
-    // ---- Q ----
-    if (is_q) {
-      bool ok = true;
-      if (stager) {
-        if (l == 0)
-          stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
-        else
-          ok = stage_wave<S::H, true, true>(c, a.th, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
-      }
-      if (!handoff(ok)) return;
-      normalise_staged<S::H>(c, sm.xs[buf], a.eps);
-    }
-    if (!stager) {
-      dot_group<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.xs[buf], S::H, acc, accu);
-      const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
-      publish_rows<RQ>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, nvq, pad, true);
-    }
-    if (is_q) buf ^= 1;
-    // ---- A ---- (tasks go to the highest workgroups, which own no Q rows;
-    // the O and gate/up weights are requested after it, so that registers
-    // are not held across attention)
-    for (int t = kPersistentGrid - 1 - c.wg; t < tasks; t += kPersistentGrid) {
-      __syncthreads();  // LDS reuse
-      if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2))) return;
-    }
-    prefetch<S::o.lpr, S::o.nj, false, S::off_o>(pf, lw.o, S::H, S::AO, c.gw, po);
-    prefetch<S::g.lpr, S::g.nj, true, S::off_g>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
-    // ---- O ----
-    if (is_o) {
-      bool ok = true;
-      if (stager) ok = stage_wave<S::AO, false, false>(c, a.tattn, tag_of(ep + 2), nullptr, sm.xs[buf], nullptr);
-      if (!handoff(ok)) return;
-    }
-    if (!stager) {
-      dot_group<S::o.lpr, S::o.nj, false, S::off_o>(pf, sm.xs[buf], S::AO, acc, accu);
-      publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
-                       lo, tbuf, o_h1 + fo, nvo, pad, true);
-    }
-    // down and the next layer's QKV go out here rather than after gate/up:
-    // issued there, they would queue in this CU's memory pipeline ahead of the
-    // stagers' polls for the down input, the largest one of the layer
-    {
-      prefetch<S::d.lpr, S::d.nj, false, S::off_d>(pf, lw.down, S::H, S::I, c.gw, pd);
-      const bool more = l + 1 < L;
-      const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
-      prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
-      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             rsrc(nx.qkv_bias, S::QKV * 4), bias_off, 0, 0));
-    }
-    if (is_o) buf ^= 1;
-    // ---- G ----
-    if (is_g) {
-      bool ok = true;
-      if (stager) ok = stage_wave<S::H, true, true>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], sm.raw_h1);
-      if (!handoff(ok)) return;
-      normalise_staged<S::H>(c, sm.xs[buf], a.eps);
-    }
-    if (!stager) {
-      dot_group<S::g.lpr, S::g.nj, true, S::off_g>(pf, sm.xs[buf], S::H, acc, accu);
-      publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
-                       lg, tbuf, o_act + fg, nvg, pad, false);
-    }
-    if (is_g) buf ^= 1;
-    // ---- D ----
-    if (is_d) {
-      bool ok = true;
-      if (stager) ok = stage_wave<S::I, false, false>(c, a.tact, tag_of(ep + 4), nullptr, sm.xs[buf], nullptr);
-      if (!handoff(ok)) return;
-    }
-    if (!stager) {
-      dot_group<S::d.lpr, S::d.nj, false, S::off_d>(pf, sm.xs[buf], S::I, acc, accu);
-      const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
-      publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, tbuf, o_h + fd, nvd, pad, false);
-      // plain copy: the final hidden for hk_engine_final_hidden
-      __builtin_amdgcn_raw_buffer_store_b16((uint16_t)y, rsrc(a.h, S::H * 2), dst_h, 0, 0);
-    }
-    if (is_d) buf ^= 1;
-  }
-  const unsigned ep_layers = base + 5u * (unsigned)L;
-  if (!a.head) {
-    if (threadIdx.x == 0) st_c32(my_flag, ep_layers);
-    return;
-  }
-
   // ---- H: LM head over all eight waves, double-buffered row groups; every
   // wave runs the same (even) number of iterations, past-the-end groups read
   // zero and store to the pad ----
@@ -1003,6 +904,368 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   }
 }
 
+// The QKV bias as a buffer: a model without one gets an empty range, so the
+// loads read zero instead of dereferencing a null base.
+template <class S>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bias_rsrc(const float* bias) {
+  return rsrc(bias, bias ? S::QKV * 4 : 0);
+}
+
+// ---- the step kernel ----
+template <class S>
+__global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
+  __shared__ PShared sm;
+  Ctx c;
+  c.a = &args;
+  c.sm = &sm;
+  c.wg = blockIdx.x;
+  c.wave = threadIdx.x >> 6;
+  c.lane = threadIdx.x & 63;
+  c.gw = c.wg * kCW + c.wave;
+  const bool stager = c.wave >= kCW;
+  if (threadIdx.x == 0) {
+    sm.abort = 0;
+    sm.out_count = 0;
+    sm.out_stored = 0;
+  }
+
+  const PersistentArgs& a = args;
+  const int L = a.layers;
+  static_assert(sizeof(PersistentLayer) % 8 == 0, "layer table is copied in 8-byte words");
+  {
+    constexpr int kWords = sizeof(PersistentLayer) / 8;
+    const unsigned long long* src = reinterpret_cast<const unsigned long long*>(a.w);
+    unsigned long long* dst = reinterpret_cast<unsigned long long*>(sm.layers);
+    for (int i = threadIdx.x; i < L * kWords; i += kPT) dst[i] = ldg(src + i);
+  }
+  __syncthreads();
+  unsigned* my_flag = a.progress + (size_t)c.wg * kFlagStride;
+  const unsigned base = ld_c32(my_flag);  // the epoch this workgroup ended the last launch on
+  const int token = ldg(&a.ctrl->token);
+  const int p = ldg(&a.ctrl->position);
+  // layer 0 reads the embedding row, or the hidden state the host preloaded
+  const uint16_t* x0 = token >= 0 ? a.embed + (size_t)min(token, a.vocab - 1) * S::H : a.h;
+  const bool is_q = c.wg < S::nq, is_o = c.wg < S::no, is_g = c.wg < S::ng, is_d = c.wg < S::nd;
+  const int tasks = S::HQ * (p / kChunk + 1);
+
+  // Row of this lane in each GEMV phase.  Every compute wave stores once per
+  // phase: a row it does not own (or a phase its workgroup sits out) goes to
+  // the wave's own pad word, so all compute waves issue the same stores.
+  // publish targets as word offsets in the one tagged-activation allocation
+  // (h, h1, qkv, attn, act, then one pad word per wave)
+  const unsigned o_h = 0, o_h1 = (unsigned)(a.th1 - a.th), o_qkv = (unsigned)(a.tqkv - a.th);
+  const unsigned o_act = (unsigned)(a.tact - a.th), o_pad = (unsigned)(a.pad - a.th);
+  const __amdgpu_buffer_rsrc_t tbuf = rsrc(a.th, (int)(o_pad + kPersistentGrid * kPW) * 4);
+  const unsigned pad = o_pad + c.wg * kPW + c.wave;
+  const int row_q = c.gw * (64 / S::q.lpr) + c.lane / S::q.lpr;
+  const int row_o = c.gw * (64 / S::o.lpr) + c.lane / S::o.lpr;
+  const int row_g = c.gw * (64 / S::g.lpr) + c.lane / S::g.lpr;
+  const int row_d = c.gw * (64 / S::d.lpr) + c.lane / S::d.lpr;
+  // first row of this workgroup in each phase and how many of its rows exist
+  constexpr int RQ = 64 / S::q.lpr, RO = 64 / S::o.lpr, RG = 64 / S::g.lpr, RD = 64 / S::d.lpr;
+  const int fq = c.wg * kCW * RQ, fo = c.wg * kCW * RO, fg = c.wg * kCW * RG, fd = c.wg * kCW * RD;
+  const int nvq = S::QKV - fq, nvo = S::H - fo, nvg = S::I - fg, nvd = S::H - fd;
+  const bool lq = c.lane % S::q.lpr == 0, lo = c.lane % S::o.lpr == 0;
+  const bool lg = c.lane % S::g.lpr == 0, ld = c.lane % S::d.lpr == 0;
+  const unsigned dst_h = is_d && row_d < S::H ? (unsigned)row_d * 2u : kOutside;  // byte offset in h
+  const int res_o = min(row_o, S::H - 1), res_d = min(row_d, S::H - 1);
+  const unsigned bias_off = is_q && !stager && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
+  // Every wave issues every weight prefetch (the stager's, like those of
+  // workgroups that sit a phase out, read zero from outside the resource):
+  // a prefetch skipped on one path would keep the registers' previous values
+  // live around the whole layer loop.
+  const bool pq = is_q && !stager, po = is_o && !stager, pg = is_g && !stager, pd = is_d && !stager;
+
+  u32x4 pf[kPf];
+  float acc, accu, bias_q = 0.0f;
+  int buf = 0;  // LDS staging buffer of the next GEMV phase
+  prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
+  bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         bias_rsrc<S>(sm.layers[0].qkv_bias), bias_off, 0, 0));
+
+  // The stager fills xs[buf]; the barrier hands it to the compute waves.
+  // Returns false (in every wave) when the launch is abandoned.
+  auto handoff = [&](bool ok) -> bool {
+    if (stager && c.lane == 0 && !ok) sm.abort = 1;
+    __syncthreads();
+    return sm.abort == 0;
+  };
+
+  for (int l = 0; l < L; ++l) {
+    const PersistentLayer& lw = sm.layers[l];
+    const unsigned ep = base + 5u * (unsigned)l;  // epoch of the previous layer's down phase
+    // ---- Q ----
+    if (is_q) {
+      bool ok = true;
+      if (stager) {
+        if (l == 0)
+          stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
+        else
+          ok = stage_wave<S::H, true, true>(c, a.th, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
+      }
+      if (!handoff(ok)) return;
+      normalise_staged<S::H>(c, sm.xs[buf], a.eps);
+    }
+    if (!stager) {
+      dot_group<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.xs[buf], S::H, acc, accu);
+      const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
+      publish_rows<RQ>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, nvq, pad, true);
+    }
+    if (is_q) buf ^= 1;
+    // ---- A ---- (tasks go to the highest workgroups, which own no Q rows;
+    // the O and gate/up weights are requested after it, so that registers
+    // are not held across attention)
+    for (int t = kPersistentGrid - 1 - c.wg; t < tasks; t += kPersistentGrid) {
+      __syncthreads();  // LDS reuse
+      if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2))) return;
+    }
+    prefetch<S::o.lpr, S::o.nj, false, S::off_o>(pf, lw.o, S::H, S::AO, c.gw, po);
+    prefetch<S::g.lpr, S::g.nj, true, S::off_g>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
+    // ---- O ----
+    if (is_o) {
+      bool ok = true;
+      if (stager) ok = stage_wave<S::AO, false, false>(c, a.tattn, tag_of(ep + 2), nullptr, sm.xs[buf], nullptr);
+      if (!handoff(ok)) return;
+    }
+    if (!stager) {
+      dot_group<S::o.lpr, S::o.nj, false, S::off_o>(pf, sm.xs[buf], S::AO, acc, accu);
+      publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
+                       lo, tbuf, o_h1 + fo, nvo, pad, true);
+    }
+    // down and the next layer's QKV go out here rather than after gate/up:
+    // issued there, they would queue in this CU's memory pipeline ahead of the
+    // stagers' polls for the down input, the largest one of the layer
+    {
+      prefetch<S::d.lpr, S::d.nj, false, S::off_d>(pf, lw.down, S::H, S::I, c.gw, pd);
+      const bool more = l + 1 < L;
+      const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
+      prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
+    }
+    if (is_o) buf ^= 1;
+    // ---- G ----
+    if (is_g) {
+      bool ok = true;
+      if (stager) ok = stage_wave<S::H, true, true>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], sm.raw_h1);
+      if (!handoff(ok)) return;
+      normalise_staged<S::H>(c, sm.xs[buf], a.eps);
+    }
+    if (!stager) {
+      dot_group<S::g.lpr, S::g.nj, true, S::off_g>(pf, sm.xs[buf], S::H, acc, accu);
+      publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
+                       lg, tbuf, o_act + fg, nvg, pad, false);
+    }
+    if (is_g) buf ^= 1;
+    // ---- D ----
+    if (is_d) {
+      bool ok = true;
+      if (stager) ok = stage_wave<S::I, false, false>(c, a.tact, tag_of(ep + 4), nullptr, sm.xs[buf], nullptr);
+      if (!handoff(ok)) return;
+    }
+    if (!stager) {
+      dot_group<S::d.lpr, S::d.nj, false, S::off_d>(pf, sm.xs[buf], S::I, acc, accu);
+      const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
+      publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, tbuf, o_h + fd, nvd, pad, false);
+      // plain copy: the final hidden for hk_engine_final_hidden
+      __builtin_amdgcn_raw_buffer_store_b16((uint16_t)y, rsrc(a.h, S::H * 2), dst_h, 0, 0);
+    }
+    if (is_d) buf ^= 1;
+  }
+  const unsigned ep_layers = base + 5u * (unsigned)L;
+  if (!a.head) {
+    if (threadIdx.x == 0) st_c32(my_flag, ep_layers);
+    return;
+  }
+
+  lm_head_phase<S>(c, pf, buf, ep_layers, my_flag, p);
+}
+
+// ---- the step kernel, split by XCD ----
+// The attention block (input RMSNorm, QKV, attention, O + residual) runs on
+// the 32 workgroups of XCD 0 and the MLP (post-attention RMSNorm, gate/up +
+// SwiGLU, down + residual) on the 224 workgroups of the other XCDs.  The
+// QKV -> attention and attention -> O hand-offs then stay inside one L2
+// (kLocal policy, ~0.5 us against ~1.3 us across XCDs), and each side
+// streams its next layer's weights while the other side computes, so no
+// prefetch queues ahead of a poll.  Epochs, tags and flags are those of
+// decode_step_kernel: launches of the two kernels may alternate.  Data the
+// XCD-local stores leave in XCD 0's L2 is written back at the end of the
+// launch, before another kernel can read it from another XCD.
+template <class S>
+__global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args) {
+  __shared__ PShared sm;
+  Ctx c;
+  c.a = &args;
+  c.sm = &sm;
+  c.wg = blockIdx.x;
+  c.wave = threadIdx.x >> 6;
+  c.lane = threadIdx.x & 63;
+  const bool stager = c.wave >= kCW;
+  if (threadIdx.x == 0) {
+    sm.abort = 0;
+    sm.out_count = 0;
+    sm.out_stored = 0;
+  }
+  const PersistentArgs& a = args;
+  const int L = a.layers;
+  {
+    constexpr int kWords = sizeof(PersistentLayer) / 8;
+    const unsigned long long* src = reinterpret_cast<const unsigned long long*>(a.w);
+    unsigned long long* dst = reinterpret_cast<unsigned long long*>(sm.layers);
+    for (int i = threadIdx.x; i < L * kWords; i += kPT) dst[i] = ldg(src + i);
+  }
+  __syncthreads();
+  unsigned* my_flag = a.progress + (size_t)c.wg * kFlagStride;
+  // the XCD-local hand-offs are only coherent if the workgroups that share
+  // them share an L2: leave (the launch is abandoned) if this workgroup is
+  // not on the XCD the split assumes
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  if ((xcc & 15u) != (unsigned)(c.wg % kXcds)) {
+    if (threadIdx.x == 0) give_up(a);
+    return;
+  }
+  const unsigned base = ld_c32(my_flag);
+  const int token = ldg(&a.ctrl->token);
+  const int p = ldg(&a.ctrl->position);
+  const uint16_t* x0 = token >= 0 ? a.embed + (size_t)min(token, a.vocab - 1) * S::H : a.h;
+  const bool attn = c.wg % kXcds == 0;
+  // rank of the workgroup within its side, and its compute waves' indices
+  const int rank = attn ? c.wg / kXcds : (c.wg / kXcds) * (kXcds - 1) + c.wg % kXcds - 1;
+  c.gw = rank * kCW + c.wave;
+
+  const unsigned o_h = 0, o_h1 = (unsigned)(a.th1 - a.th), o_qkv = (unsigned)(a.tqkv - a.th);
+  const unsigned o_act = (unsigned)(a.tact - a.th), o_pad = (unsigned)(a.pad - a.th);
+  const __amdgpu_buffer_rsrc_t tbuf = rsrc(a.th, (int)(o_pad + kPersistentGrid * kPW) * 4);
+  const unsigned pad = o_pad + c.wg * kPW + c.wave;
+  u32x4 pf[kPf];
+  float acc, accu;
+  int buf = 0;
+  auto handoff = [&](bool ok) -> bool {
+    if (stager && c.lane == 0 && !ok) sm.abort = 1;
+    __syncthreads();
+    return sm.abort == 0;
+  };
+
+  if (attn) {
+    constexpr PhaseCfg Q = S::xq, O = S::xo;
+    constexpr int RQ = 64 / Q.lpr, RO = 64 / O.lpr, OFF_O = Q.nj;
+    const bool is_q = rank < S::xnq, is_o = rank < S::xno;
+    const int row_q = c.gw * RQ + c.lane / Q.lpr, row_o = c.gw * RO + c.lane / O.lpr;
+    const int fq = rank * kCW * RQ, fo = rank * kCW * RO;
+    const bool lq = c.lane % Q.lpr == 0, lo = c.lane % O.lpr == 0;
+    const int res_o = min(row_o, S::H - 1);
+    const unsigned bias_off = is_q && !stager && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
+    const bool pq = is_q && !stager, po = is_o && !stager;
+    const int tasks = S::HQ * (p / kChunk + 1);
+    prefetch<Q.lpr, Q.nj, false, 0>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
+    prefetch<O.lpr, O.nj, false, OFF_O>(pf, sm.layers[0].o, S::H, S::AO, c.gw, po);
+    float bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 bias_rsrc<S>(sm.layers[0].qkv_bias), bias_off, 0, 0));
+    for (int l = 0; l < L; ++l) {
+      const PersistentLayer& lw = sm.layers[l];
+      const unsigned ep = base + 5u * (unsigned)l;
+      const bool more = l + 1 < L;
+      const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
+      // ---- Q: h from the MLP side (across XCDs) ----
+      if (is_q) {
+        bool ok = true;
+        if (stager) {
+          if (l == 0)
+            stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
+          else
+            ok = stage_wave<S::H, true, true>(c, a.th, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
+        }
+        if (!handoff(ok)) return;
+        normalise_staged<S::H>(c, sm.xs[buf], a.eps);
+      }
+      if (!stager) {
+        dot_group<Q.lpr, Q.nj, false, 0>(pf, sm.xs[buf], S::H, acc, accu);
+        const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
+        publish_rows<RQ, kLocal>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, S::QKV - fq, pad, true);
+      }
+      if (is_q) buf ^= 1;
+      prefetch<Q.lpr, Q.nj, false, 0>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
+      // ---- A: tasks on the highest ranks ----
+      for (int t = kXcdWg - 1 - rank; t < tasks; t += kXcdWg) {
+        __syncthreads();  // LDS reuse
+        if (!attention_task<S, kLocal>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2)))
+          return;
+      }
+      // ---- O: h1 to the MLP side ----
+      if (is_o) {
+        bool ok = true;
+        if (stager)
+          ok = stage_wave<S::AO, false, false, kLocal>(c, a.tattn, tag_of(ep + 2), nullptr, sm.xs[buf], nullptr);
+        if (!handoff(ok)) return;
+      }
+      if (!stager) {
+        dot_group<O.lpr, O.nj, false, OFF_O>(pf, sm.xs[buf], S::AO, acc, accu);
+        publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
+                         lo, tbuf, o_h1 + fo, S::H - fo, pad, true);
+      }
+      if (is_o) buf ^= 1;
+      prefetch<O.lpr, O.nj, false, OFF_O>(pf, nx.o, S::H, S::AO, c.gw, po && more);
+    }
+  } else {
+    constexpr PhaseCfg G = S::xg, D = S::xd;
+    constexpr int RG = 64 / G.lpr, RD = 64 / D.lpr, OFF_D = 2 * G.nj;
+    const bool is_g = rank < S::xng, is_d = rank < S::xnd;
+    const int row_d = c.gw * RD + c.lane / D.lpr;
+    const int fg = rank * kCW * RG, fd = rank * kCW * RD;
+    const bool lg = c.lane % G.lpr == 0, ld = c.lane % D.lpr == 0;
+    const int res_d = min(row_d, S::H - 1);
+    const unsigned dst_h = is_d && row_d < S::H ? (unsigned)row_d * 2u : kOutside;
+    const bool pg = is_g && !stager, pd = is_d && !stager;
+    prefetch<G.lpr, G.nj, true, 0>(pf, sm.layers[0].gate_up, S::I, S::H, c.gw, pg);
+    prefetch<D.lpr, D.nj, false, OFF_D>(pf, sm.layers[0].down, S::H, S::I, c.gw, pd);
+    for (int l = 0; l < L; ++l) {
+      const PersistentLayer& lw = sm.layers[l];
+      const unsigned ep = base + 5u * (unsigned)l;
+      const bool more = l + 1 < L;
+      const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
+      // ---- G: h1 from XCD 0 ----
+      if (is_g) {
+        bool ok = true;
+        if (stager) ok = stage_wave<S::H, true, true>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], sm.raw_h1);
+        if (!handoff(ok)) return;
+        normalise_staged<S::H>(c, sm.xs[buf], a.eps);
+      }
+      if (!stager) {
+        dot_group<G.lpr, G.nj, true, 0>(pf, sm.xs[buf], S::H, acc, accu);
+        publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
+                         lg, tbuf, o_act + fg, S::I - fg, pad, false);
+      }
+      if (is_g) buf ^= 1;
+      // ---- D: h to XCD 0 (and to the LM head after the last layer) ----
+      if (is_d) {
+        bool ok = true;
+        if (stager) ok = stage_wave<S::I, false, false>(c, a.tact, tag_of(ep + 4), nullptr, sm.xs[buf], nullptr);
+        if (!handoff(ok)) return;
+      }
+      if (!stager) {
+        dot_group<D.lpr, D.nj, false, OFF_D>(pf, sm.xs[buf], S::I, acc, accu);
+        const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
+        publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, tbuf, o_h + fd, S::H - fd, pad, true);
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)y, rsrc(a.h, S::H * 2), dst_h, 0, 0);
+      }
+      if (is_d) buf ^= 1;
+      // the next layer's MLP weights stream while XCD 0 runs its attention block
+      prefetch<G.lpr, G.nj, true, 0>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
+      prefetch<D.lpr, D.nj, false, OFF_D>(pf, nx.down, S::H, S::I, c.gw, pd && more);
+    }
+  }
+  const unsigned ep_layers = base + 5u * (unsigned)L;
+  if (!a.head) {
+    if (threadIdx.x == 0) st_c32(my_flag, ep_layers);
+    return;
+  }
+  lm_head_phase<S>(c, pf, buf, ep_layers, my_flag, p);
+}
+
 using SmolShape = Shape<576, 1536, 9, 3>;
 using QwenShape = Shape<896, 4864, 14, 2>;
 
@@ -1012,19 +1275,78 @@ bool matches(int hidden, int intermediate, int q_heads, int kv_heads) {
 }
 
 template <class S>
-int launch_shape(const PersistentArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(decode_step_kernel<S>, dim3(kPersistentGrid), dim3(kPT), 0, stream, a);
+int launch_shape(const PersistentArgs& a, hipStream_t stream, bool xcd_split) {
+  if (xcd_split) {
+    if constexpr (S::xa)
+      hipLaunchKernelGGL(decode_step_xa_kernel<S>, dim3(kPersistentGrid), dim3(kPT), 0, stream, a);
+    else
+      return fail("persistent step: no XCD split for this model shape");
+  } else {
+    hipLaunchKernelGGL(decode_step_kernel<S>, dim3(kPersistentGrid), dim3(kPT), 0, stream, a);
+  }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "persistent step launch");
 }
 
+template <class K>
+int occupancy_of(K kernel) {
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kPT, 0) != hipSuccess) return 0;
+  return blocks >= 1;
+}
+
 template <class S>
 int occupancy_ok() {
-  int blocks = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_step_kernel<S>, kPT, 0) !=
-      hipSuccess)
+  return occupancy_of(decode_step_kernel<S>);
+}
+
+// XCC_ID of every workgroup of a kPersistentGrid-workgroup launch.
+__global__ void xcc_probe_kernel(unsigned* out) {
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc & 15u;
+}
+
+// 1 when workgroup i of a launch runs on XCD i % kXcds; else 0, with the
+// reason in hk_last_error().
+int xcd_layout_ok(hipStream_t stream) {
+  unsigned* d = nullptr;
+  if (hipMalloc(&d, kPersistentGrid * sizeof(unsigned)) != hipSuccess) {
+    set_error("XCD split: hipMalloc failed");
     return 0;
-  return blocks >= 1;
+  }
+  unsigned h[kPersistentGrid] = {};
+  (void)hipGetLastError();  // an earlier call's error is not this launch's
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(kPersistentGrid), dim3(64), 0, stream, d);
+  hipError_t err = hipGetLastError();
+  if (err == hipSuccess) err = hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(stream);
+  (void)hipFree(d);
+  if (err != hipSuccess) {
+    set_error(std::string("XCD split: layout probe failed: ") + hipGetErrorString(err));
+    return 0;
+  }
+  for (int i = 0; i < kPersistentGrid; ++i)
+    if (h[i] != (unsigned)(i % kXcds)) {
+      set_error("XCD split: workgroup " + std::to_string(i) + " ran on XCD " + std::to_string(h[i]) +
+                ", not " + std::to_string(i % kXcds));
+      return 0;
+    }
+  return 1;
+}
+
+template <class S>
+int xcd_split_ok(hipStream_t stream) {
+  if constexpr (S::xa) {
+    if (!occupancy_of(decode_step_xa_kernel<S>)) {
+      set_error("XCD split: the split step kernel cannot keep one workgroup per CU");
+      return 0;
+    }
+    return xcd_layout_ok(stream);
+  } else {
+    set_error("XCD split: no register plan for this model shape");
+    return 0;
+  }
 }
 
 }  // namespace
@@ -1044,12 +1366,24 @@ int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bo
   return -1;
 }
 
-int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream) {
+int persistent_xcd_split(int shape, hipStream_t stream) {
+  switch (shape) {
+    case 0: return xcd_split_ok<SmolShape>(stream);
+    case 1: return xcd_split_ok<QwenShape>(stream);
+    default:
+      set_error("XCD split: no persistent step for this model shape");
+      return 0;
+  }
+}
+
+int persistent_split_tasks_max() { return kXcdWg; }
+
+int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream, bool xcd_split) {
   if (a.layers <= 0 || a.layers > kPersistentMaxLayers) return fail("persistent step: layer count out of range");
   if (a.max_splits < (a.max_ctx + kChunk - 1) / kChunk) return fail("persistent step: partials too small");
   switch (shape) {
-    case 0: return launch_shape<SmolShape>(a, stream);
-    case 1: return launch_shape<QwenShape>(a, stream);
+    case 0: return launch_shape<SmolShape>(a, stream, xcd_split);
+    case 1: return launch_shape<QwenShape>(a, stream, xcd_split);
     default: return fail("persistent step: unsupported model shape");
   }
 }

@@ -99,6 +99,7 @@ _SIGNATURES = {
     "hk_gemv_repeat": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "hk_engine_reset": (ctypes.c_int, [_vp]),
     "hk_engine_stream": (_vp, [_vp]),
+    "hk_engine_step_kind": (ctypes.c_int, [_vp, _i32, ctypes.POINTER(_i32)]),
     "hk_engine_destroy": (None, [_vp]),
     "hk_gemv_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "hk_gemv_w8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),

@@ -150,6 +150,18 @@ class QwenDecoderEngine:
     def stream(self):
         return self._lib.hk_engine_stream(self._engine)
 
+    STEP_KINDS = {0: "kernels", 1: "persistent", 2: "xcd_split"}
+
+    def step_kind(self, position):
+        """How a decode step at `position` runs: "kernels" (one kernel per
+        part, replayed as a hipGraph), "persistent" (one launch over all CUs)
+        or "xcd_split" (one launch, attention block on XCD 0, MLP on the
+        other XCDs)."""
+        kind = ctypes.c_int32()
+        hip.check(self._lib.hk_engine_step_kind(self._live(), int(position), ctypes.byref(kind)),
+                  "hk_engine_step_kind")
+        return self.STEP_KINDS[kind.value]
+
     def _live(self):
         if self._engine is None:
             raise RuntimeError("engine is closed")

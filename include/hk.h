@@ -120,7 +120,7 @@ int hk_engine_generate(hk_engine* engine, int32_t token, int32_t position, int32
  * float32 summation order.  Replaces the reference's per-position prefill
  * loop (npu_llm/runtime/generate.py:1110-1125) and the engine's lm_head=False
  * dispatches (npu_llm/designs/qwen_engine.py:213-219).  Prompts longer than
- * 512 tokens run in 512-token chunks. */
+ * 4096 tokens (or the context length) run in chunks of that many. */
 int hk_engine_prefill(hk_engine* engine, const int32_t* tokens_host, int32_t n, int32_t start,
                       float* logits_host, int32_t* next_token_host);
 
@@ -167,6 +167,18 @@ int hk_gemv_repeat(const void* const* weights, const float* const* scales, int32
 
 /* Zero the KV cache (QwenDecoderEngine.reset, qwen_engine.py:65-66). */
 int hk_engine_reset(hk_engine* engine);
+
+/* How a decode step at `position` runs, written to `kind_out`:
+ * HK_STEP_KERNELS (one kernel per part, replayed as a hipGraph),
+ * HK_STEP_PERSISTENT (one persistent launch over all CUs) or
+ * HK_STEP_XCD_SPLIT (one persistent launch with the attention block on XCD 0
+ * and the MLP on the other XCDs; short contexts).  HK_ERR_INVALID for a
+ * position outside the context.  No reference counterpart (the NPU engine
+ * has one dispatch form). */
+#define HK_STEP_KERNELS 0
+#define HK_STEP_PERSISTENT 1
+#define HK_STEP_XCD_SPLIT 2
+int hk_engine_step_kind(hk_engine* engine, int32_t position, int32_t* kind_out);
 
 /* The engine's HIP stream (hipStream_t), for timing with events. */
 void* hk_engine_stream(hk_engine* engine);

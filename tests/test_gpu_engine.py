@@ -18,6 +18,8 @@ validate_engine_npu.py):
   position stay zero after a reset) and holds the oracle's values.
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -143,6 +145,105 @@ def test_long_context_split_kv():
     merged by log-sum-exp); 2-layer model keeps the oracle quick."""
     model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
     _check_decode(model, _prompt(151936, 600, 14), 8, 4096, label="qwen2-layer-ctx4096")
+
+
+def test_xcd_split_is_selected_by_context():
+    """On MI355X (8 XCDs, workgroup i on XCD i % 8) the Qwen step runs split
+    by XCD while the attention tasks of a layer (14 query heads x 256-slot
+    chunks) fit the 32 workgroups of XCD 0, i.e. below position 512, and as
+    one undivided launch beyond; HK_XCD_SPLIT=0 turns the split off, and
+    HK_XCD_SPLIT=1 makes engine creation fail (with the reason) where the
+    device cannot run it."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("step kind by position")
+    model = SyntheticModel(QWEN25_05B, seed=1, layers=1)
+    for required in ("1", None):
+        if required:
+            os.environ["HK_XCD_SPLIT"] = required
+        try:
+            engine = QwenDecoderEngine(model, context_length=1024)
+        finally:
+            os.environ.pop("HK_XCD_SPLIT", None)
+        try:
+            kinds = [engine.step_kind(p) for p in (0, 40, 511, 512, 1023)]
+            announce(f"  kinds {kinds}")
+            assert kinds == ["xcd_split"] * 3 + ["persistent"] * 2
+            with pytest.raises(ValueError):
+                engine.step_kind(1024)
+        finally:
+            engine.close()
+    os.environ["HK_XCD_SPLIT"] = "0"
+    try:
+        engine = QwenDecoderEngine(model, context_length=64)
+        try:
+            assert engine.step_kind(40) == "persistent"
+        finally:
+            engine.close()
+    finally:
+        del os.environ["HK_XCD_SPLIT"]
+
+
+def test_undivided_step_short_context(monkeypatch):
+    """The undivided persistent step (HK_XCD_SPLIT=0) at the positions the
+    split takes by default holds the same bar."""
+    monkeypatch.setenv("HK_XCD_SPLIT", "0")
+    model = SyntheticModel(QWEN25_05B, seed=0, layers=4)
+    _check_decode(model, _prompt(151936, 40, 12), 32, 72, label="qwen-4L-undivided")
+
+
+def test_xcd_split_two_chunk_attention():
+    """Positions 256..511 give each head two 256-slot chunks, merged by
+    log-sum-exp, all on XCD 0 under the split."""
+    model = SyntheticModel(QWEN25_05B, seed=7, layers=2)
+    _check_decode(model, _prompt(151936, 300, 16), 8, 512, label="qwen-2L-split-two-chunks")
+
+
+def test_xcd_split_agrees_with_undivided_step(monkeypatch):
+    """The split and undivided kernels sum the QKV and O rows over different
+    lane groups (8 lanes per row against 16 and 64), so they agree to float
+    tolerance; the greedy ids agree up to a near-tie.  The second engine also
+    alternates the two kernels (the split below 512, undivided above), which
+    share tags, epochs and flags from launch to launch."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("split vs undivided step")
+    model = SyntheticModel(QWEN25_05B, seed=9, layers=4)
+    prompt = _prompt(151936, 24, 17)
+
+    def run(split):
+        if split:
+            monkeypatch.delenv("HK_XCD_SPLIT", raising=False)
+        else:
+            monkeypatch.setenv("HK_XCD_SPLIT", "0")
+        engine = QwenDecoderEngine(model, context_length=1024)
+        try:
+            logits = []
+            for pos, tok in enumerate(prompt):
+                _, lg = engine.step_token(tok, pos, logits=pos >= len(prompt) - 4)
+                if pos >= len(prompt) - 4:
+                    logits.append(lg.copy())
+            first = int(np.argmax(logits[-1]))
+            gen = engine.generate(first, len(prompt), 12)
+            # cross position 512 within one device-driven run: 505..520
+            engine.prefill(_prompt(151936, 505 - len(prompt) - 12, 18), len(prompt) + 12)
+            gen2 = engine.generate(gen[-1], 505, 16)
+            kinds = (engine.step_kind(505), engine.step_kind(520))
+            return logits, gen, gen2, kinds
+        finally:
+            engine.close()
+
+    l_split, g_split, g2_split, k_split = run(True)
+    l_flat, g_flat, g2_flat, k_flat = run(False)
+    assert k_split == ("xcd_split", "persistent") and k_flat == ("persistent", "persistent")
+    errs = [rel_l2(a, b) for a, b in zip(l_split, l_flat)]
+    announce(f"  rel-L2 split vs undivided {max(errs):.3e}; ids equal {g_split == g_flat}, {g2_split == g2_flat}")
+    assert max(errs) <= 1e-2
+    for gs, gf in ((g_split, g_flat), (g2_split, g2_flat)):
+        if gs != gf:
+            i = next(i for i, (x, y) in enumerate(zip(gs, gf)) if x != y)
+            announce(f"  first difference at step {i}: {gs[i]} vs {gf[i]}")
+            assert i > 0
 
 
 def test_step_contract_errors(qwen_model):
