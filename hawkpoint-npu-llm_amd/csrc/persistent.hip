@@ -1186,9 +1186,6 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         publish_rows<RQ, kLocal>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, S::QKV - fq, pad, true);
       }
       if (is_q) buf ^= 1;
-      prefetch<Q.lpr, Q.nj, false, 0>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
-      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
       // ---- A: tasks on the highest ranks ----
       for (int t = kXcdWg - 1 - rank; t < tasks; t += kXcdWg) {
         __syncthreads();  // LDS reuse
@@ -1208,6 +1205,13 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
                          lo, tbuf, o_h1 + fo, S::H - fo, pad, true);
       }
       if (is_o) buf ^= 1;
+      // the next layer's QKV and O rows go out once this layer's attention
+      // block is done, while the MLP side computes: issued earlier, they
+      // would queue in this CU's memory pipeline ahead of the attention
+      // task's K/V loads and the O stagers' polls
+      prefetch<Q.lpr, Q.nj, false, 0>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
       prefetch<O.lpr, O.nj, false, OFF_O>(pf, nx.o, S::H, S::AO, c.gw, po && more);
     }
   } else {
