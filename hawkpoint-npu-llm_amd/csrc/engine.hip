@@ -161,6 +161,9 @@ struct hk_engine {
   // there, judged by next_pos, the position the next launch decodes
   bool xcd_split = false;
   int next_pos = 0;
+  std::vector<uint16_t*> down_x;         // per layer, down_proj regrouped for the split
+  unsigned long long* wpart = nullptr;   // the split's partial down products
+  unsigned long long* xpart = nullptr;
   PersistentLayer* players = nullptr;  // device copy of the layer pointers
   unsigned int spin_limit = kPersistentSpinLimit;
   unsigned int* psync = nullptr;       // per-workgroup epochs
@@ -332,6 +335,8 @@ int launch_persistent(hk_engine* e, bool head) {
   a.ctrl = e->ctrl;
   a.out_tokens = e->out_tokens;
   a.result = e->result;
+  a.wpart = e->wpart;
+  a.xpart = e->xpart;
   a.progress = e->psync;
   a.error = reinterpret_cast<unsigned int*>(e->result + 1);
   a.spin_limit = e->spin_limit;
@@ -357,6 +362,8 @@ int check_persistent(hk_engine* e, const int32_t* result_host) {
   HK_CHECK(hipStreamSynchronize(e->stream));
   HK_CHECK(hipMemset(e->psync, 0, psync_words(e) * sizeof(unsigned int)));
   HK_CHECK(hipMemset(e->ptag, 0, ptag_words(e) * sizeof(uint32_t)));
+  if (e->wpart) HK_CHECK(hipMemset(e->wpart, 0, (size_t)kPersistentGrid * e->d.hidden * 8));
+  if (e->xpart) HK_CHECK(hipMemset(e->xpart, 0, (size_t)8 * e->d.hidden * 8));
   HK_CHECK(hipMemset(e->counters, 0, e->d.q_heads * sizeof(unsigned int)));
   HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
   HK_CHECK(hipDeviceSynchronize());
@@ -423,8 +430,11 @@ void free_engine(hk_engine* e) {
                   e->normed,  e->logits,   e->kcache,   e->vcache,     e->partial,
                   e->counters, e->keys,    e->ctrl,     e->out_tokens, e->result,
                   e->pf_x,    e->pf_h1,    e->pf_xn,    e->pf_qkv,     e->pf_q,
-                  e->pf_att,  e->pf_act,   e->pf_tokens, e->pf_split, e->players, e->psync, e->ptag};
+                  e->pf_att,  e->pf_act,   e->pf_tokens, e->pf_split, e->players, e->psync, e->ptag,
+                  e->wpart,   e->xpart};
   for (void* p : bufs)
+    if (p) (void)hipFree(p);
+  for (uint16_t* p : e->down_x)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
@@ -669,7 +679,24 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
         const hk_layer_weights& lw = e->layers[l];
         pl[l] = {static_cast<const uint16_t*>(lw.qkv),     lw.qkv_bias,
                  static_cast<const uint16_t*>(lw.o_proj),  static_cast<const uint16_t*>(lw.gate_up),
-                 static_cast<const uint16_t*>(lw.down_proj), lw.input_norm, lw.post_attn_norm};
+                 static_cast<const uint16_t*>(lw.down_proj), lw.input_norm, lw.post_attn_norm,
+                 nullptr};
+      }
+      if (e->xcd_split) {
+        // the split fuses down_proj into the gate/up workgroups: a regrouped
+        // copy per layer (H x I bf16 each) and the partial-sum words
+        e->down_x.assign(d.layers, nullptr);
+        for (int l = 0; l < d.layers; ++l) {
+          HK_TRY(dalloc(&e->down_x[l], (size_t)d.hidden * d.intermediate));
+          HK_TRY(launch_regroup_down(static_cast<const uint16_t*>(e->layers[l].down_proj), e->down_x[l],
+                                     d.hidden, d.intermediate, e->stream));
+          pl[l].down_x = e->down_x[l];
+        }
+        HK_TRY(dalloc(&e->wpart, (size_t)kPersistentGrid * d.hidden));
+        HK_CHECK(hipMemset(e->wpart, 0, (size_t)kPersistentGrid * d.hidden * 8));
+        HK_TRY(dalloc(&e->xpart, (size_t)8 * d.hidden));
+        HK_CHECK(hipMemset(e->xpart, 0, (size_t)8 * d.hidden * 8));
+        HK_CHECK(hipStreamSynchronize(e->stream));
       }
       HK_TRY(dalloc(&e->players, d.layers));
       HK_CHECK(hipMemcpy(e->players, pl.data(), d.layers * sizeof(PersistentLayer),

@@ -112,6 +112,11 @@ struct PersistentLayer {
   const uint16_t* down;
   const uint16_t* in_norm;
   const uint16_t* post_norm;
+  // down_proj regrouped for the XCD split (null otherwise): for each group of
+  // four intermediate rows g, [H / 8][8][4] bf16 -- element (c, e, j) is
+  // down[8c + e][4g + j], so one 16-byte chunk holds two outputs of all four
+  // rows (see launch_regroup_down)
+  const uint16_t* down_x;
 };
 
 struct PersistentArgs {
@@ -141,6 +146,10 @@ struct PersistentArgs {
   StepCtrl* ctrl;
   int32_t* out_tokens;
   int32_t* result;
+  // XCD split: per-workgroup and per-XCD partial down products, 64-bit words
+  // (epoch tag << 32) | float bits; zero between launch sequences
+  unsigned long long* wpart;  // [kPersistentGrid][H]
+  unsigned long long* xpart;  // [8][H]
   unsigned int* progress;  // [kPersistentGrid * kFlagStride] last epoch per workgroup
   unsigned int* error;     // nonzero: a wait timed out; the launch was abandoned
   unsigned int spin_limit; // polls before a wait is abandoned
@@ -160,6 +169,8 @@ int persistent_xcd_split(int shape, hipStream_t stream);
 int persistent_split_tasks_max();
 int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream,
                            bool xcd_split = false);
+// down_x for the XCD split from down [H, I] (I a multiple of 4, H of 8).
+int launch_regroup_down(const uint16_t* down, uint16_t* down_x, int H, int I, hipStream_t stream);
 
 // ---- batched prefill (prefill.hip) ----
 

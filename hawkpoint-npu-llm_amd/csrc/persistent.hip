@@ -69,7 +69,9 @@ constexpr int kPartStride = kHeadDim + 2;
 constexpr int kSc1 = 16;                  // buffer-load cache policy: device scope (sc1)
 // Cache policy of hand-offs inside one XCD: loads with sc0|nt miss the CU's
 // L1 and read the XCD's shared L2, which every CU of the XCD writes through
-// to; stores use the default policy (0) and stay in that L2.
+// to; stores use the default policy (0) and stay in that L2.  Data stored
+// with sc1 (written through to memory for other XCDs) is read with sc1 even
+// inside the XCD: an sc0|nt load can keep hitting a stale L2 copy of it.
 constexpr int kLocal = 3;
 // MI355X: 8 XCDs of 32 CUs; workgroup i of a one-per-CU launch runs on XCD
 // i % 8 (the XCD split checks this against the XCC_ID register).
@@ -78,12 +80,6 @@ constexpr int kXcdWg = kPersistentGrid / kXcds;
 static_assert(2 * kChunk == kPT, "two threads per attention slot");
 
 // ---- device-coherent accesses ----
-__device__ __forceinline__ void st_c16(uint16_t* p, uint32_t v) {
-  __hip_atomic_store(p, (uint16_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_c16(const uint16_t* p) {
-  return __hip_atomic_load(const_cast<uint16_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void st_c32(unsigned* p, unsigned v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -107,10 +103,6 @@ __device__ __forceinline__ unsigned long long ld_c64(const unsigned long long* p
 // byte offset, and offsets past `bytes` read zero instead of faulting.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
-// 16 bytes at base + off, device-coherent.
-__device__ __forceinline__ u32x4 ld_c128(const void* base, int bytes, int off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base, bytes), off, 0, kSc1);
 }
 
 
@@ -225,14 +217,17 @@ struct Shape {
   static constexpr PhaseCfg xq = pick_cfg(QKV, H, false, kAW, kPf / 2);
   static constexpr PhaseCfg xo = pick_cfg(H, AO, false, kAW, kPf / 2);
   static constexpr PhaseCfg xg = pick_cfg(I, H, true, kMW, kPf / 2);
-  static constexpr PhaseCfg xd = pick_cfg(H, I, false, kMW, kPf - 2 * xg.nj);
-  static constexpr int xnq = producers(xq, QKV), xno = producers(xo, H);
-  static constexpr int xng = producers(xg, I), xnd = producers(xd, H);
-  // O rows take their residual from the Q stagers' copy of h, down rows from
-  // the gate/up stagers' copy of h1
-  static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr && xd.lpr && xq.nj + xo.nj <= kPf &&
-                             2 * xg.nj + xd.nj <= kPf && xno <= xnq && xnd <= xng &&
-                             xnq <= kXcdWg && xng <= kPersistentGrid - kXcdWg;
+  static constexpr int xnq = producers(xq, QKV), xno = producers(xo, H), xng = producers(xg, I);
+  // down is fused into the gate/up waves: a wave's four act values times
+  // their down_x group, H / 8 output chunks over the 64 lanes (xkd each,
+  // four 16-byte slots per chunk); each workgroup of an XCD then adds up xsl
+  // of the H outputs over the XCD's workgroups
+  static constexpr int xkd = (H / 8 + 63) / 64;
+  static constexpr int xsl = (H + kXcdWg - 1) / kXcdWg;
+  // O rows take their residual from the Q stagers' copy of h
+  static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
+                             2 * xg.nj + 4 * xkd <= kPf && xno <= xnq && xsl <= 64 && H <= kHMax &&
+                             I % 4 == 0 && xnq <= kXcdWg && xng <= kPersistentGrid - kXcdWg;
 };
 
 struct PShared {
@@ -285,18 +280,6 @@ __device__ bool poll_word(const PersistentArgs& a, const uint32_t* p, unsigned t
       out = w;
       return true;
     }
-    if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
-// Poll the 16-byte chunk at byte `off` of a tagged buffer of `bytes` bytes.
-__device__ bool poll_chunk(const PersistentArgs& a, const uint32_t* base, int bytes, int off,
-                           unsigned tag, u32x4& v) {
-  for (unsigned spins = 1;; ++spins) {
-    v = ld_c128(base, bytes, off);
-    if ((v.x >> 16) == tag && (v.y >> 16) == tag && (v.z >> 16) == tag && (v.w >> 16) == tag)
-      return true;
     if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
     __builtin_amdgcn_s_sleep(1);
   }
@@ -959,7 +942,6 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   const unsigned pad = o_pad + c.wg * kPW + c.wave;
   const int row_q = c.gw * (64 / S::q.lpr) + c.lane / S::q.lpr;
   const int row_o = c.gw * (64 / S::o.lpr) + c.lane / S::o.lpr;
-  const int row_g = c.gw * (64 / S::g.lpr) + c.lane / S::g.lpr;
   const int row_d = c.gw * (64 / S::d.lpr) + c.lane / S::d.lpr;
   // first row of this workgroup in each phase and how many of its rows exist
   constexpr int RQ = 64 / S::q.lpr, RO = 64 / S::o.lpr, RG = 64 / S::g.lpr, RD = 64 / S::d.lpr;
@@ -1081,20 +1063,164 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
   lm_head_phase<S>(c, pf, buf, ep_layers, my_flag, p);
 }
 
+// ---- the XCD split's fused down projection ----
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct XShared : PShared {
+  alignas(16) float wsum[kCW][kHMax];  // the compute waves' partial down products
+};
+
+// Partial-sum words: (tag << 32) | float bits; the tag (epoch % (2^32 - 1) + 1)
+// is never 0, the value of cleared memory.  An aligned 8-byte store is seen
+// whole or not at all.
+__device__ __forceinline__ unsigned ptag_of(unsigned e) { return e % 0xffffffffu + 1u; }
+
+// down_x rows of this wave's row group (four intermediate rows): chunk
+// c = lane + 64 k of the group's H / 8 output chunks goes to slots
+// OFF + 4k .. OFF + 4k + 3 (chunks past H / 8 and dead groups read zero).
+template <class S, int OFF>
+__device__ __forceinline__ void prefetch_down_x(u32x4 (&pf)[kPf], const uint16_t* dx, int group, bool live) {
+  constexpr int CC = S::H / 8;
+  const __amdgpu_buffer_rsrc_t r = rsrc(dx, S::I * S::H * 2);
+  const int lane = threadIdx.x & 63;
+  const bool ok = live && group < S::I / 4;
+#pragma unroll
+  for (int k = 0; k < S::xkd; ++k) {
+    const int cc = lane + 64 * k;
+    const unsigned voff = ok && cc < CC ? (unsigned)(group * CC + cc) * 64u : kOutside;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pf[OFF + 4 * k + q] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, q * 16, kNT);
+  }
+}
+
+// This wave's partial down product: act (bf16 bits; lanes 16 s .. 16 s + 15
+// hold row s of the group) times the group's down_x chunks, written to ws[H].
+template <class S, int OFF>
+__device__ __forceinline__ void down_partial(const u32x4 (&pf)[kPf], uint32_t act, float* ws) {
+  constexpr int CC = S::H / 8;
+  const int lane = threadIdx.x & 63;
+  const uint32_t a0 = __shfl(act, 0, 64), a1 = __shfl(act, 16, 64);
+  const uint32_t a2 = __shfl(act, 32, 64), a3 = __shfl(act, 48, 64);
+  const uint32_t A01 = (a0 & 0xffffu) | (a1 << 16), A23 = (a2 & 0xffffu) | (a3 << 16);
+#pragma unroll
+  for (int k = 0; k < S::xkd; ++k) {
+    const int cc = lane + 64 * k;
+    float o[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 w = pf[OFF + 4 * k + q];  // outputs 2q, 2q + 1 of the chunk, rows 0..3 each
+      o[2 * q] = dot2(w.x, A01, dot2(w.y, A23, 0.0f));
+      o[2 * q + 1] = dot2(w.z, A01, dot2(w.w, A23, 0.0f));
+    }
+    if (cc < CC) {
+      reinterpret_cast<float4*>(ws + 8 * cc)[0] = make_float4(o[0], o[1], o[2], o[3]);
+      reinterpret_cast<float4*>(ws + 8 * cc)[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+  }
+}
+
+// Stager wave 0 of MLP workgroup jx of XCD xcd: outputs xsl * jx + lane of
+// the XCD's down product, the sum over its nprod producing workgroups (local
+// index j, in order) of their partials (tag pt), stored to xpart across the
+// device.  False (in every lane) when the launch is abandoned.
+template <class S>
+__device__ bool reduce_xcd(Ctx& c, int xcd, int jx, int nprod, unsigned pt) {
+  const PersistentArgs& a = *c.a;
+  const int e = S::xsl * jx + c.lane;
+  const bool live = c.lane < S::xsl && e < S::H;
+  const __amdgpu_buffer_rsrc_t r = rsrc(a.wpart, kPersistentGrid * S::H * 8);
+  unsigned long long v[kXcdWg];
+  bool ok = true;
+  for (unsigned spins = 1;; ++spins) {
+    bool have = true;
+#pragma unroll
+    for (int j = 0; j < kXcdWg; ++j) {
+      const unsigned off = live && j < nprod ? (unsigned)(((kXcds * j + xcd) * S::H + e) * 8) : kOutside;
+      v[j] = __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kLocal));
+    }
+#pragma unroll
+    for (int j = 0; j < kXcdWg; ++j) have = have && (!live || j >= nprod || (unsigned)(v[j] >> 32) == pt);
+    if (__all(have)) break;
+    if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) {
+      ok = give_up(a);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (ok && live) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kXcdWg; ++j)
+      if (j < nprod) sum += __uint_as_float((unsigned)v[j]);
+    const unsigned long long w = ((unsigned long long)pt << 32) | __float_as_uint(sum);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, w), rsrc(a.xpart, kXcds * S::H * 8),
+                                          (xcd * S::H + e) * 8, 0, kSc1);
+  }
+  return __all(ok);
+}
+
+// Stager wave 0 of XCD-0 workgroup jx: outputs xsl * jx + lane of the layer
+// output h = bf16(bf16(sum over XCDs 1..7 of their partials) + h1), the
+// down_proj epilogue of the undivided step.  Stored three ways: tagged in
+// `local` with the default policy (the next layer's QKV stagers on XCD 0
+// poll it there), tagged in h across the device (the LM head polls it), and
+// as plain bf16.
+template <class S>
+__device__ bool reduce_h(Ctx& c, int jx, unsigned pt, unsigned tag_h1, unsigned tag_h, uint32_t* local) {
+  const PersistentArgs& a = *c.a;
+  const int e = S::xsl * jx + c.lane;
+  const bool live = c.lane < S::xsl && e < S::H;
+  const __amdgpu_buffer_rsrc_t r = rsrc(a.xpart, kXcds * S::H * 8);
+  const __amdgpu_buffer_rsrc_t rh1 = rsrc(a.th1, S::H * 4);
+  unsigned long long v[kXcds - 1];
+  uint32_t h1 = 0;
+  bool ok = true;
+  for (unsigned spins = 1;; ++spins) {
+#pragma unroll
+    for (int x = 1; x < kXcds; ++x)
+      v[x - 1] = __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(
+                                                          r, live ? (unsigned)((x * S::H + e) * 8) : kOutside, 0, kSc1));
+    h1 = __builtin_amdgcn_raw_buffer_load_b32(rh1, live ? (unsigned)e * 4u : kOutside, 0, kSc1);
+    bool have = !live || (h1 >> 16) == tag_h1;
+#pragma unroll
+    for (int x = 0; x < kXcds - 1; ++x) have = have && (!live || (unsigned)(v[x] >> 32) == pt);
+    if (__all(have)) break;
+    if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) {
+      ok = give_up(a);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (ok && live) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int x = 0; x < kXcds - 1; ++x) sum += __uint_as_float((unsigned)v[x]);
+    const uint32_t y = f32_to_bf16(round_bf16(sum) + bf_lo(h1));
+    __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_h), rsrc(local, S::H * 4), e * 4, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_h), rsrc(a.th, S::H * 4), e * 4, 0, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)y, rsrc(a.h, S::H * 2), e * 2, 0, 0);
+  }
+  return __all(ok);
+}
+
 // ---- the step kernel, split by XCD ----
 // The attention block (input RMSNorm, QKV, attention, O + residual) runs on
 // the 32 workgroups of XCD 0 and the MLP (post-attention RMSNorm, gate/up +
-// SwiGLU, down + residual) on the 224 workgroups of the other XCDs.  The
+// SwiGLU, down as partial sums) on the 224 workgroups of the other XCDs;
+// XCD 0 adds the partials and the residual.  The
 // QKV -> attention and attention -> O hand-offs then stay inside one L2
 // (kLocal policy, ~0.5 us against ~1.3 us across XCDs), and each side
 // streams its next layer's weights while the other side computes, so no
-// prefetch queues ahead of a poll.  Epochs, tags and flags are those of
+// prefetch queues ahead of a poll.  down_proj is fused into the gate/up
+// workgroups (split-K over the intermediate rows, reduced per workgroup, per
+// XCD and finally on XCD 0), so act never crosses XCDs; the act buffer holds
+// XCD 0's local copy of h instead.  Epochs, tags and flags are those of
 // decode_step_kernel: launches of the two kernels may alternate.  Data the
 // XCD-local stores leave in XCD 0's L2 is written back at the end of the
 // launch, before another kernel can read it from another XCD.
 template <class S>
 __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args) {
-  __shared__ PShared sm;
+  __shared__ XShared sm;
   Ctx c;
   c.a = &args;
   c.sm = &sm;
@@ -1135,8 +1261,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
   const int rank = attn ? c.wg / kXcds : (c.wg / kXcds) * (kXcds - 1) + c.wg % kXcds - 1;
   c.gw = rank * kCW + c.wave;
 
-  const unsigned o_h = 0, o_h1 = (unsigned)(a.th1 - a.th), o_qkv = (unsigned)(a.tqkv - a.th);
-  const unsigned o_act = (unsigned)(a.tact - a.th), o_pad = (unsigned)(a.pad - a.th);
+  const unsigned o_h1 = (unsigned)(a.th1 - a.th), o_qkv = (unsigned)(a.tqkv - a.th);
+  const unsigned o_pad = (unsigned)(a.pad - a.th);
   const __amdgpu_buffer_rsrc_t tbuf = rsrc(a.th, (int)(o_pad + kPersistentGrid * kPW) * 4);
   const unsigned pad = o_pad + c.wg * kPW + c.wave;
   u32x4 pf[kPf];
@@ -1174,8 +1300,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (stager) {
           if (l == 0)
             stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
-          else
-            ok = stage_wave<S::H, true, true>(c, a.th, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
+          else  // h from XCD 0's own reducers (reduce_h), in its L2
+            ok = stage_wave<S::H, true, true, kLocal>(c, a.tact, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
         }
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
@@ -1213,53 +1339,65 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
       prefetch<O.lpr, O.nj, false, OFF_O>(pf, nx.o, S::H, S::AO, c.gw, po && more);
+      // ---- h = h1 + down(act): this workgroup's outputs, from the MLP XCDs'
+      // partials (the next hand-off barrier reports an abandoned wait) ----
+      if (c.wave == kCW && !reduce_h<S>(c, rank, ptag_of(ep + 4), tag_of(ep + 3), tag_of(ep + 5), a.tact) &&
+          c.lane == 0)
+        sm.abort = 1;
     }
   } else {
-    constexpr PhaseCfg G = S::xg, D = S::xd;
-    constexpr int RG = 64 / G.lpr, RD = 64 / D.lpr, OFF_D = 2 * G.nj;
-    const bool is_g = rank < S::xng, is_d = rank < S::xnd;
-    const int row_d = c.gw * RD + c.lane / D.lpr;
-    const int fg = rank * kCW * RG, fd = rank * kCW * RD;
-    const bool lg = c.lane % G.lpr == 0, ld = c.lane % D.lpr == 0;
-    const int res_d = min(row_d, S::H - 1);
-    const unsigned dst_h = is_d && row_d < S::H ? (unsigned)row_d * 2u : kOutside;
-    const bool pg = is_g && !stager, pd = is_d && !stager;
+    constexpr PhaseCfg G = S::xg;
+    constexpr int OFF_D = 2 * G.nj;
+    const int xcd = c.wg % kXcds, jx = c.wg / kXcds;  // this XCD, and the index within it
+    const bool is_g = rank < S::xng;
+    const bool pg = is_g && !stager;
+    // workgroups of this XCD with gate/up rows: local index j, rank 7 j + xcd - 1
+    int nprod = 0;
+    for (int j = 0; j < kXcdWg; ++j) nprod += (kXcds - 1) * j + xcd - 1 < S::xng ? 1 : 0;
     prefetch<G.lpr, G.nj, true, 0>(pf, sm.layers[0].gate_up, S::I, S::H, c.gw, pg);
-    prefetch<D.lpr, D.nj, false, OFF_D>(pf, sm.layers[0].down, S::H, S::I, c.gw, pd);
+    prefetch_down_x<S, OFF_D>(pf, sm.layers[0].down_x, c.gw, pg);
     for (int l = 0; l < L; ++l) {
       const PersistentLayer& lw = sm.layers[l];
       const unsigned ep = base + 5u * (unsigned)l;
       const bool more = l + 1 < L;
       const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
-      // ---- G: h1 from XCD 0 ----
+      const unsigned pt = ptag_of(ep + 4);
+      // ---- gate/up + SwiGLU on h1 from XCD 0, then this wave's rows of down ----
       if (is_g) {
         bool ok = true;
-        if (stager) ok = stage_wave<S::H, true, true>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], sm.raw_h1);
+        if (stager) ok = stage_wave<S::H, true, false>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], nullptr);
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
+        if (!stager) {
+          dot_group<G.lpr, G.nj, true, 0>(pf, sm.xs[buf], S::H, acc, accu);
+          down_partial<S, OFF_D>(pf, f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), sm.wsum[c.wave]);
+        }
+        __syncthreads();
+        // the workgroup's partial: thread t adds outputs 2t, 2t + 1 over the
+        // compute waves, in order
+        if (threadIdx.x < S::H / 2) {
+          const int t = threadIdx.x;
+          float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+          for (int w = 0; w < kCW; ++w) {
+            s0 += sm.wsum[w][2 * t];
+            s1 += sm.wsum[w][2 * t + 1];
+          }
+          const u32x4 words = {__float_as_uint(s0), pt, __float_as_uint(s1), pt};
+          __builtin_amdgcn_raw_buffer_store_b128(words, rsrc(a.wpart, kPersistentGrid * S::H * 8),
+                                                 (c.wg * S::H + 2 * t) * 8, 0, 0);
+        }
+        buf ^= 1;
       }
-      if (!stager) {
-        dot_group<G.lpr, G.nj, true, 0>(pf, sm.xs[buf], S::H, acc, accu);
-        publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
-                         lg, tbuf, o_act + fg, S::I - fg, pad, false);
-      }
-      if (is_g) buf ^= 1;
-      // ---- D: h to XCD 0 (and to the LM head after the last layer) ----
-      if (is_d) {
+      // ---- this workgroup's outputs of the XCD's sum (stager wave 0); the
+      // barrier keeps the next weight loads behind its polls ----
+      {
         bool ok = true;
-        if (stager) ok = stage_wave<S::I, false, false>(c, a.tact, tag_of(ep + 4), nullptr, sm.xs[buf], nullptr);
+        if (c.wave == kCW) ok = reduce_xcd<S>(c, xcd, jx, nprod, pt);
         if (!handoff(ok)) return;
       }
-      if (!stager) {
-        dot_group<D.lpr, D.nj, false, OFF_D>(pf, sm.xs[buf], S::I, acc, accu);
-        const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
-        publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, tbuf, o_h + fd, S::H - fd, pad, true);
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)y, rsrc(a.h, S::H * 2), dst_h, 0, 0);
-      }
-      if (is_d) buf ^= 1;
-      // the next layer's MLP weights stream while XCD 0 runs its attention block
       prefetch<G.lpr, G.nj, true, 0>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
-      prefetch<D.lpr, D.nj, false, OFF_D>(pf, nx.down, S::H, S::I, c.gw, pd && more);
+      prefetch_down_x<S, OFF_D>(pf, nx.down_x, c.gw, pg && more);
     }
   }
   const unsigned ep_layers = base + 5u * (unsigned)L;
@@ -1381,6 +1519,29 @@ int persistent_xcd_split(int shape, hipStream_t stream) {
 }
 
 int persistent_split_tasks_max() { return kXcdWg; }
+
+namespace {
+// down_x[((g * (H / 8) + c) * 8 + e) * 4 + j] = down[(8 c + e) * I + 4 g + j]
+__global__ void regroup_down_kernel(const uint16_t* __restrict__ down, uint16_t* __restrict__ dx, int H, int I) {
+  const size_t n = (size_t)H * I;
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < n; o += (size_t)gridDim.x * blockDim.x) {
+    const int j = (int)(o & 3);
+    const int e = (int)((o >> 2) & 7);
+    const size_t gc = o >> 5;  // g * (H / 8) + c
+    const int c = (int)(gc % (size_t)(H / 8));
+    const int g = (int)(gc / (size_t)(H / 8));
+    dx[o] = down[(size_t)(8 * c + e) * I + 4 * g + j];
+  }
+}
+}  // namespace
+
+int launch_regroup_down(const uint16_t* down, uint16_t* down_x, int H, int I, hipStream_t stream) {
+  if (!down || !down_x || H <= 0 || I <= 0 || H % 8 != 0 || I % 4 != 0)
+    return fail("regroup_down: bad arguments");
+  hipLaunchKernelGGL(regroup_down_kernel, dim3(1024), dim3(256), 0, stream, down, down_x, H, I);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "regroup_down launch");
+}
 
 int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream, bool xcd_split) {
   if (a.layers <= 0 || a.layers > kPersistentMaxLayers) return fail("persistent step: layer count out of range");
