@@ -621,7 +621,10 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   }
   if (__syncthreads_or(!ok)) return false;
 
-  const float scale = 1.0f / 8.0f;  // head_dim ** -0.5 for head_dim 64 (exact)
+  // scores in base 2: head_dim ** -0.5 (1/8 for head_dim 64) times log2(e),
+  // so every exponential below is one v_exp_f32 (2^x); the split-KV maxima
+  // are kept in the same base
+  const float scale = 0.125f * 1.44269504088896341f;
   float dot = 0.0f;
   {
     const float* qh = qs + half * kHalf;
@@ -659,21 +662,19 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   dot += __shfl_xor(dot, 1, 64);  // the two halves of the slot
   const bool live = si < n;
   const float sc = live ? dot * scale : -INFINITY;
-  float m = wave_max64(sc);
-  if (c.lane == 0) c.sm->red[0][c.wave] = m;
-  __syncthreads();
-  m = c.sm->red[0][0];
-#pragma unroll
-  for (int w = 1; w < kPW; ++w) m = fmaxf(m, c.sm->red[0][w]);
-  const float e = live ? expf(sc - m) : 0.0f;
-  float sum = wave_sum<64>(half == 0 ? e : 0.0f);  // each slot once
-  if (c.lane == 0) c.sm->red[1][c.wave] = sum;
-  __syncthreads();
-  sum = c.sm->red[1][0];
-#pragma unroll
-  for (int w = 1; w < kPW; ++w) sum += c.sm->red[1][w];
-  if (half == 0) pr[si] = nsplit == 1 ? e / sum : e;  // a single chunk normalises first, as NumPy does
-  __syncthreads();
+  // Softmax and P @ V per wave, flash-style: a wave's 32 slots are exactly
+  // those of its two P @ V groups (gi = 2 wave, 2 wave + 1), so its max,
+  // exponentials, sum and partial P @ V need no workgroup barrier; one
+  // barrier then merges the eight waves by log-sum-exp.  (A wave without
+  // live slots has max -inf and contributes exp(-inf) = 0; every chunk has a
+  // live slot, so the merged max is finite.)
+  const float mw = wave_max64(sc);
+  const float e = live ? __builtin_amdgcn_exp2f(sc - mw) : 0.0f;
+  const float sw = wave_sum<64>(half == 0 ? e : 0.0f);  // each slot once
+  if (half == 0) pr[si] = e;
+  // the P @ V reads below take probabilities written by other lanes of this
+  // wave only; a wave's LDS accesses complete in order
+  __builtin_amdgcn_wave_barrier();
 
   // probabilities of slots past the chunk's live ones are zero, and so are
   // their value words, so the loop needs no bounds test; the four 16-byte
@@ -696,12 +697,27 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   }
   acc[gi * kHeadDim + 2 * dp] = o0;
   acc[gi * kHeadDim + 2 * dp + 1] = o1;
+  if (c.lane == 0) {
+    c.sm->red[0][c.wave] = mw;
+    c.sm->red[1][c.wave] = sw;
+  }
   __syncthreads();
+  float m = c.sm->red[0][0];
+#pragma unroll
+  for (int w = 1; w < kPW; ++w) m = fmaxf(m, c.sm->red[0][w]);
+  float fw[kPW], sum = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kPW; ++w) {
+    fw[w] = __builtin_amdgcn_exp2f(c.sm->red[0][w] - m);
+    sum = fmaf(c.sm->red[1][w], fw[w], sum);
+  }
+  constexpr int kGroupsPerWave = 64 / kHalf;
   float o = 0.0f;
   if (tid < kHeadDim) {
 #pragma unroll
-    for (int k = 0; k < kGroupsPV; ++k) o += acc[k * kHeadDim + tid];
+    for (int k = 0; k < kGroupsPV; ++k) o = fmaf(acc[k * kHeadDim + tid], fw[k / kGroupsPerWave], o);
   }
+  if (nsplit == 1) o = o / sum;  // a single chunk normalises here
   uint32_t* out = a.tattn + (size_t)h * kHeadDim;
   // the head's output words; XCD-local stores go through a buffer resource
   auto store_out = [&](uint32_t v) {
@@ -737,7 +753,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     float lsum = 0.0f, r = 0.0f;
     for (int j = 0; j < nsplit; ++j) {
       const float* pj = base + (size_t)j * kPartStride;
-      const float f = expf(ld_cf(pj + kHeadDim) - mx);
+      const float f = __builtin_amdgcn_exp2f(ld_cf(pj + kHeadDim) - mx);
       lsum = fmaf(ld_cf(pj + kHeadDim + 1), f, lsum);
       r = fmaf(ld_cf(pj + tid), f, r);
     }
