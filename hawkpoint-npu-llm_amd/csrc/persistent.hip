@@ -174,8 +174,8 @@ constexpr PhaseCfg pick_cfg(int M, int K, bool pair, int waves, int budget) {
 }
 
 // producers of a phase: workgroups whose compute waves own row groups
-constexpr int producers(PhaseCfg c, int M) {
-  return ((M + 64 / c.lpr - 1) / (64 / c.lpr) + kCW - 1) / kCW;
+constexpr int producers(PhaseCfg c, int M, int waves_per_wg = kCW) {
+  return ((M + 64 / c.lpr - 1) / (64 / c.lpr) + waves_per_wg - 1) / waves_per_wg;
 }
 
 template <int H_, int I_, int HQ_, int HKV_>
@@ -212,20 +212,31 @@ struct Shape {
                 "residual copies need nested producer sets");
   // XCD split (decode_step_xa_kernel): the attention block runs on the
   // kXcdWg workgroups of XCD 0 (QKV rows in slots 0.., O rows after them),
-  // the MLP on the other XCDs (gate/up pairs in slots 0.., down rows after)
-  static constexpr int kAW = kXcdWg * kCW, kMW = (kPersistentGrid - kXcdWg) * kCW;
+  // the MLP on the other XCDs (gate/up pairs in slots 0.., down rows after).
+  // On XCD 0 all kPW waves of a workgroup take QKV and O rows (the stagers
+  // are idle during those dot products), so the rows fit on the lowest
+  // workgroups and the attention tasks go to workgroups without rows, whose
+  // K/V loads then go out at the start of the layer; O uses no more
+  // workgroups than QKV (their stagers keep h for the residual)
+  static constexpr int kAW = kXcdWg * kPW, kMW = (kPersistentGrid - kXcdWg) * kCW;
   static constexpr PhaseCfg xq = pick_cfg(QKV, H, false, kAW, kPf / 2);
-  static constexpr PhaseCfg xo = pick_cfg(H, AO, false, kAW, kPf / 2);
+  static constexpr int xnq = producers(xq, QKV, kPW);
+  static constexpr PhaseCfg xo = pick_cfg(H, AO, false, xnq * kPW, kPf / 2);
   static constexpr PhaseCfg xg = pick_cfg(I, H, true, kMW, kPf / 2);
-  static constexpr int xnq = producers(xq, QKV), xno = producers(xo, H), xng = producers(xg, I);
+  static constexpr int xno = producers(xo, H, kPW), xng = producers(xg, I);
   // down is fused into the gate/up waves: a wave's four act values times
   // their down_x group, H / 8 output chunks over the 64 lanes (xkd each,
   // four 16-byte slots per chunk); each workgroup of an XCD then adds up xsl
   // of the H outputs over the XCD's workgroups
   static constexpr int xkd = (H / 8 + 63) / 64;
   static constexpr int xsl = (H + kXcdWg - 1) / kXcdWg;
+  // XCD 0 adds the XCD partials on the stager waves of its workgroups
+  // without QKV/O rows (no weight prefetch queues ahead of their polls):
+  // slices of xhs outputs, xhn of them
+  static constexpr int xhs = 32, xhn = (H + xhs - 1) / xhs;
   // O rows take their residual from the Q stagers' copy of h
   static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
+                             xnq + HQ <= kXcdWg && xhn <= (kXcdWg - xnq) * kSW &&
                              2 * xg.nj + 4 * xkd <= kPf && xno <= xnq && xsl <= 64 && H <= kHMax &&
                              I % 4 == 0 && xnq <= kXcdWg && xng <= kPersistentGrid - kXcdWg;
 };
@@ -775,11 +786,11 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
 // gathered store has been issued before it goes on to issue weight loads:
 // the CU's memory pipeline is in order, so the store must not queue behind
 // tens of kilobytes of prefetch.
-template <int RPW, int POL = kSc1>
+template <int RPW, int POL = kSc1, int NW = kCW>
 __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t word, bool row_lead,
                                              __amdgpu_buffer_rsrc_t tagged_buf, unsigned first,
                                              int valid_rows, unsigned pad, bool then_load) {
-  static_assert(kCW * RPW <= kCW * 16, "gather buffer too small");
+  static_assert(NW * RPW <= kCW * 16, "gather buffer too small");
   // word offsets into the tagged-activation buffer (a buffer store with a
   // 32-bit offset holds fewer registers than a 64-bit address)
   unsigned dst = pad;
@@ -790,7 +801,7 @@ __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t wor
     if (row_lead) c.sm->out_val[c.wave * RPW + sub] = word;
     if (c.lane == 0) old = atomicAdd(&c.sm->out_count, 1u);
     old = __shfl(old, 0, 64);
-    if (old % kCW == kCW - 1 && c.lane < kCW * RPW && c.lane < valid_rows) {
+    if (old % NW == NW - 1 && c.lane < NW * RPW && c.lane < valid_rows) {
       v = c.sm->out_val[c.lane];
       dst = first + c.lane;
     }
@@ -798,8 +809,8 @@ __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t wor
   // device-coherent (sc1) like st_c32, or XCD-local (the default policy)
   __builtin_amdgcn_raw_buffer_store_b32(v, tagged_buf, dst * 4u, 0, POL == kSc1 ? kSc1 : 0);
   if (!producer) return;
-  const unsigned done = old - old % kCW + kCW;
-  if (old % kCW == kCW - 1) {
+  const unsigned done = old - old % NW + NW;
+  if (old % NW == NW - 1) {
     if (c.lane == 0) __hip_atomic_store(&c.sm->out_stored, done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   } else if (then_load) {
     // the last wave is at most a few hundred cycles behind; the bound only
@@ -1175,17 +1186,17 @@ __device__ bool reduce_xcd(Ctx& c, int xcd, int jx, int nprod, unsigned pt) {
   return __all(ok);
 }
 
-// Stager wave 0 of XCD-0 workgroup jx: outputs xsl * jx + lane of the layer
+// A stager wave of XCD 0: outputs xhs * slice + lane of the layer
 // output h = bf16(bf16(sum over XCDs 1..7 of their partials) + h1), the
 // down_proj epilogue of the undivided step.  Stored three ways: tagged in
 // `local` with the default policy (the next layer's QKV stagers on XCD 0
 // poll it there), tagged in h across the device (the LM head polls it), and
 // as plain bf16.
 template <class S>
-__device__ bool reduce_h(Ctx& c, int jx, unsigned pt, unsigned tag_h1, unsigned tag_h, uint32_t* local) {
+__device__ bool reduce_h(Ctx& c, int slice, unsigned pt, unsigned tag_h1, unsigned tag_h, uint32_t* local) {
   const PersistentArgs& a = *c.a;
-  const int e = S::xsl * jx + c.lane;
-  const bool live = c.lane < S::xsl && e < S::H;
+  const int e = S::xhs * slice + c.lane;
+  const bool live = c.lane < S::xhs && e < S::H;
   const __amdgpu_buffer_rsrc_t r = rsrc(a.xpart, kXcds * S::H * 8);
   const __amdgpu_buffer_rsrc_t rh1 = rsrc(a.th1, S::H * 4);
   unsigned long long v[kXcds - 1];
@@ -1275,7 +1286,9 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
   const bool attn = c.wg % kXcds == 0;
   // rank of the workgroup within its side, and its compute waves' indices
   const int rank = attn ? c.wg / kXcds : (c.wg / kXcds) * (kXcds - 1) + c.wg % kXcds - 1;
-  c.gw = rank * kCW + c.wave;
+  // row-group index of this wave: all kPW waves on XCD 0, the kCW compute
+  // waves on the MLP side (a stager's index there is never live)
+  c.gw = rank * (attn ? kPW : kCW) + c.wave;
 
   const unsigned o_h1 = (unsigned)(a.th1 - a.th), o_qkv = (unsigned)(a.tqkv - a.th);
   const unsigned o_pad = (unsigned)(a.pad - a.th);
@@ -1295,12 +1308,13 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     constexpr int RQ = 64 / Q.lpr, RO = 64 / O.lpr, OFF_O = Q.nj;
     const bool is_q = rank < S::xnq, is_o = rank < S::xno;
     const int row_q = c.gw * RQ + c.lane / Q.lpr, row_o = c.gw * RO + c.lane / O.lpr;
-    const int fq = rank * kCW * RQ, fo = rank * kCW * RO;
+    const int fq = rank * kPW * RQ, fo = rank * kPW * RO;
     const bool lq = c.lane % Q.lpr == 0, lo = c.lane % O.lpr == 0;
     const int res_o = min(row_o, S::H - 1);
-    const unsigned bias_off = is_q && !stager && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
-    const bool pq = is_q && !stager, po = is_o && !stager;
+    const unsigned bias_off = is_q && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
+    const bool pq = is_q, po = is_o;
     const int tasks = S::HQ * (p / kChunk + 1);
+    const int hslice = rank >= S::xnq ? (rank - S::xnq) * kSW + (c.wave - kCW) : S::xhn;
     prefetch<Q.lpr, Q.nj, false, 0>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
     prefetch<O.lpr, O.nj, false, OFF_O>(pf, sm.layers[0].o, S::H, S::AO, c.gw, po);
     float bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
@@ -1322,13 +1336,14 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
       }
-      if (!stager) {
+      {  // all eight waves
         dot_group<Q.lpr, Q.nj, false, 0>(pf, sm.xs[buf], S::H, acc, accu);
         const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
-        publish_rows<RQ, kLocal>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, S::QKV - fq, pad, true);
+        publish_rows<RQ, kLocal, kPW>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, S::QKV - fq, pad,
+                                      true);
       }
       if (is_q) buf ^= 1;
-      // ---- A: tasks on the highest ranks ----
+      // ---- A: tasks on the highest ranks, which hold no QKV or O rows ----
       for (int t = kXcdWg - 1 - rank; t < tasks; t += kXcdWg) {
         __syncthreads();  // LDS reuse
         if (!attention_task<S, kLocal>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2)))
@@ -1341,10 +1356,10 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
           ok = stage_wave<S::AO, false, false, kLocal>(c, a.tattn, tag_of(ep + 2), nullptr, sm.xs[buf], nullptr);
         if (!handoff(ok)) return;
       }
-      if (!stager) {
+      {  // all eight waves
         dot_group<O.lpr, O.nj, false, OFF_O>(pf, sm.xs[buf], S::AO, acc, accu);
-        publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
-                         lo, tbuf, o_h1 + fo, S::H - fo, pad, true);
+        publish_rows<RO, kSc1, kPW>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
+                                    lo, tbuf, o_h1 + fo, S::H - fo, pad, true);
       }
       if (is_o) buf ^= 1;
       // the next layer's QKV and O rows go out once this layer's attention
@@ -1355,10 +1370,11 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
       prefetch<O.lpr, O.nj, false, OFF_O>(pf, nx.o, S::H, S::AO, c.gw, po && more);
-      // ---- h = h1 + down(act): this workgroup's outputs, from the MLP XCDs'
-      // partials (the next hand-off barrier reports an abandoned wait) ----
-      if (c.wave == kCW && !reduce_h<S>(c, rank, ptag_of(ep + 4), tag_of(ep + 3), tag_of(ep + 5), a.tact) &&
-          c.lane == 0)
+      // ---- h = h1 + down(act) from the MLP XCDs' partials, on the stager
+      // waves of the workgroups without rows (an abandoned wait ends every
+      // later wait of the launch through the error word) ----
+      if (stager && hslice < S::xhn &&
+          !reduce_h<S>(c, hslice, ptag_of(ep + 4), tag_of(ep + 3), tag_of(ep + 5), a.tact) && c.lane == 0)
         sm.abort = 1;
     }
   } else {
