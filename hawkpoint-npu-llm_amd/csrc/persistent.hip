@@ -1308,7 +1308,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     constexpr int RQ = 64 / Q.lpr, RO = 64 / O.lpr, OFF_O = Q.nj;
     const bool is_q = rank < S::xnq, is_o = rank < S::xno;
     const int row_q = c.gw * RQ + c.lane / Q.lpr, row_o = c.gw * RO + c.lane / O.lpr;
-    const int fq = rank * kPW * RQ, fo = rank * kPW * RO;
+    const int fo = rank * kPW * RO;
     const bool lq = c.lane % Q.lpr == 0, lo = c.lane % O.lpr == 0;
     const int res_o = min(row_o, S::H - 1);
     const unsigned bias_off = is_q && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
@@ -1336,11 +1336,13 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
       }
-      {  // all eight waves
+      {  // all eight waves; the rows go straight to XCD 0's L2 (only the
+         // attention tasks there poll them): each row's first lane stores it,
+         // the other lanes the wave's pad word, one store per wave
         dot_group<Q.lpr, Q.nj, false, 0>(pf, sm.xs[buf], S::H, acc, accu);
         const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
-        publish_rows<RQ, kLocal, kPW>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, S::QKV - fq, pad,
-                                      true);
+        const unsigned dst = is_q && lq && row_q < S::QKV ? o_qkv + (unsigned)row_q : pad;
+        __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_of(ep + 1)), tbuf, dst * 4u, 0, 0);
       }
       if (is_q) buf ^= 1;
       // ---- A: tasks on the highest ranks, which hold no QKV or O rows ----
