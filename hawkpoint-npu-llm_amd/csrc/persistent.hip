@@ -556,9 +556,9 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   const int nsplit = p / kChunk + 1;
   const bool holds_new = (s == nsplit - 1);
   const int tid = threadIdx.x;
-  float* qs = reinterpret_cast<float*>(c.sm->xs[0]);  // [64]
-  float* knew = qs + kHeadDim;          // [64]
-  float* pr = knew + kHeadDim;          // [kChunk]
+  uint16_t* qs = c.sm->xs[0];           // [64] rotated q, bf16
+  uint16_t* knew = qs + kHeadDim;       // [64] rotated new key, bf16
+  float* pr = reinterpret_cast<float*>(knew + kHeadDim);  // [kChunk]
   float* acc = pr + kChunk;             // [kGroupsPV][64]
   const size_t head_base = ((size_t)l * S::HKV + g) * a.max_ctx;
   // this head's cache rows [0, p): slots p and beyond read as zero
@@ -615,9 +615,9 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     const float x1 = bf_lo(w1), x2 = bf_lo(w2);
     const uint32_t r1 = f32_to_bf16(x1 * cs - x2 * sn);
     const uint32_t r2 = f32_to_bf16(x2 * cs + x1 * sn);
-    float* dst = is_k ? knew : qs;
-    dst[j] = bf16_to_f32(r1);
-    dst[j + kHalf] = bf16_to_f32(r2);
+    uint16_t* dst = is_k ? knew : qs;
+    dst[j] = (uint16_t)r1;
+    dst[j + kHalf] = (uint16_t)r2;
     if (is_k && holds_new && h % S::QPK == 0 && ok) {
       uint32_t v1 = 0, v2 = 0;
       ok = poll_word<POL>(a, tq + vr + j, tag_q, v1, tqr, (vr + j) * 4) &&
@@ -636,39 +636,25 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   // so every exponential below is one v_exp_f32 (2^x); the split-KV maxima
   // are kept in the same base
   const float scale = 0.125f * 1.44269504088896341f;
-  float dot = 0.0f;
+  float dot;
   {
-    const float* qh = qs + half * kHalf;
-    if (slot == p) {
-      // the new key (bf16 values held as f32) packed like a cached row
-      const float4* kh = reinterpret_cast<const float4*>(knew + half * kHalf);
+    // q and k are bf16: v_dot2 on packed pairs, exact products, float sums
+    const u32x4* qh = reinterpret_cast<const u32x4*>(qs + half * kHalf);
+    if (slot == p) {  // the new key, packed like a cached row
+      const u32x4* kh = reinterpret_cast<const u32x4*>(knew + half * kHalf);
 #pragma unroll
-      for (int ch = 0; ch < kHeadDim / 16; ++ch) {
-        const float4 a0 = kh[2 * ch], a1 = kh[2 * ch + 1];
-        krow[ch] = u32x4{(__float_as_uint(a0.x) >> 16) | (__float_as_uint(a0.y) & 0xffff0000u),
-                         (__float_as_uint(a0.z) >> 16) | (__float_as_uint(a0.w) & 0xffff0000u),
-                         (__float_as_uint(a1.x) >> 16) | (__float_as_uint(a1.y) & 0xffff0000u),
-                         (__float_as_uint(a1.z) >> 16) | (__float_as_uint(a1.w) & 0xffff0000u)};
-      }
+      for (int ch = 0; ch < kHeadDim / 16; ++ch) krow[ch] = kh[ch];
     }
-    {
+    float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-      for (int ch = 0; ch < kHeadDim / 16; ++ch) {
-        // eight q values per step: keeps the LDS reads from being hoisted
-        // into many live registers
-        const float4 q0 = reinterpret_cast<const float4*>(qh)[2 * ch];
-        const float4 q1 = reinterpret_cast<const float4*>(qh)[2 * ch + 1];
-        dot = fmaf(q0.x, bf_lo(krow[ch].x), dot);
-        dot = fmaf(q0.y, bf_hi(krow[ch].x), dot);
-        dot = fmaf(q0.z, bf_lo(krow[ch].y), dot);
-        dot = fmaf(q0.w, bf_hi(krow[ch].y), dot);
-        dot = fmaf(q1.x, bf_lo(krow[ch].z), dot);
-        dot = fmaf(q1.y, bf_hi(krow[ch].z), dot);
-        dot = fmaf(q1.z, bf_lo(krow[ch].w), dot);
-        dot = fmaf(q1.w, bf_hi(krow[ch].w), dot);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int ch = 0; ch < kHeadDim / 16; ++ch) {
+      const u32x4 q = qh[ch];
+      d0 = dot2(krow[ch].x, q.x, d0);
+      d1 = dot2(krow[ch].y, q.y, d1);
+      d0 = dot2(krow[ch].z, q.z, d0);
+      d1 = dot2(krow[ch].w, q.w, d1);
     }
+    dot = d0 + d1;
   }
   dot += __shfl_xor(dot, 1, 64);  // the two halves of the slot
   const bool live = si < n;
@@ -728,7 +714,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
 #pragma unroll
     for (int k = 0; k < kGroupsPV; ++k) o = fmaf(acc[k * kHeadDim + tid], fw[k / kGroupsPerWave], o);
   }
-  if (nsplit == 1) o = o / sum;  // a single chunk normalises here
+  if (nsplit == 1) o *= __builtin_amdgcn_rcpf(sum);  // a single chunk normalises here
   uint32_t* out = a.tattn + (size_t)h * kHeadDim;
   // the head's output words; XCD-local stores go through a buffer resource
   auto store_out = [&](uint32_t v) {
