@@ -297,12 +297,17 @@ int launch_part(hk_engine* e, int part, int l) {
   }
 }
 
-// Whether a persistent launch at `position` runs split by XCD.
-bool split_at(const hk_engine* e, int position) {
-  return e->xcd_split &&
-         e->d.q_heads * (position / kPersistentChunk + 1) <= persistent_split_tasks_max();
+// The form of a persistent launch at `position`: split by XCD with the
+// attention tasks on XCD 0 while they fit its workgroups, on the MLP
+// workgroups while they fit those, else undivided.
+int form_at(const hk_engine* e, int position) {
+  if (!e->xcd_split) return kStepUndivided;
+  const int tasks = e->d.q_heads * (position / kPersistentChunk + 1);
+  if (tasks <= persistent_split_tasks_max(false)) return kStepSplit;
+  if (tasks <= persistent_split_tasks_max(true)) return kStepSplitLong;
+  return kStepUndivided;
 }
-bool split_step(const hk_engine* e) { return split_at(e, e->next_pos); }
+int step_form(const hk_engine* e) { return form_at(e, e->next_pos); }
 
 int launch_persistent(hk_engine* e, bool head) {
   const hk_model_desc& d = e->d;
@@ -340,7 +345,7 @@ int launch_persistent(hk_engine* e, bool head) {
   a.progress = e->psync;
   a.error = reinterpret_cast<unsigned int*>(e->result + 1);
   a.spin_limit = e->spin_limit;
-  return launch_persistent_step(e->pshape, a, e->stream, split_step(e));
+  return launch_persistent_step(e->pshape, a, e->stream, step_form(e));
 }
 
 size_t psync_words(const hk_engine*) { return (size_t)kPersistentGrid * kFlagStride; }
@@ -847,7 +852,7 @@ int hk_engine_launch_part_repeat(hk_engine* e, int32_t part, int32_t count) {
   HK_CHECK(hipSetDevice(e->device));
   if (part >= HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
   const long long key = (long long)part << 32 | (unsigned)count |
-                        (part == HK_PART_STEP && e->pshape >= 0 && split_step(e) ? 1LL << 62 : 0);
+                        (part == HK_PART_STEP && e->pshape >= 0 ? (long long)step_form(e) << 60 : 0);
   auto it = e->repeat_graphs.find(key);
   if (it == e->repeat_graphs.end()) {
     hipGraph_t graph = nullptr;
@@ -923,7 +928,8 @@ int hk_engine_step_kind(hk_engine* e, int32_t position, int32_t* kind_out) {
   if (!e || !kind_out) return fail("hk_engine_step_kind: null argument");
   if (position < 0 || position >= e->d.max_context)
     return fail("position outside the " + std::to_string(e->d.max_context) + "-token context");
-  *kind_out = e->pshape < 0 ? HK_STEP_KERNELS : split_at(e, position) ? HK_STEP_XCD_SPLIT : HK_STEP_PERSISTENT;
+  static const int32_t kinds[] = {HK_STEP_PERSISTENT, HK_STEP_XCD_SPLIT, HK_STEP_XCD_SPLIT_LONG};
+  *kind_out = e->pshape < 0 ? HK_STEP_KERNELS : kinds[form_at(e, position)];
   return HK_OK;
 }
 

@@ -163,12 +163,15 @@ int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bo
 // XCD 0, MLP on the others) on the current device; else 0 with the reason in
 // hk_last_error().  Runs a small probe kernel on `stream` and waits for it.
 int persistent_xcd_split(int shape, hipStream_t stream);
-// Attention tasks per layer up to which the XCD split keeps one task per
-// workgroup of XCD 0 (query heads x 256-slot chunks); beyond it the split is
-// correct but slower than the undivided step.
-int persistent_split_tasks_max();
+// Forms of the persistent step.  kStepSplit runs a layer's attention tasks
+// (query heads x 256-slot chunks) on XCD 0, kStepSplitLong on the MLP
+// workgroups of the other XCDs; each is correct for any position, and
+// persistent_split_tasks_max(long_form) is the task count up to which it
+// keeps one task per workgroup.
+enum StepForm : int { kStepUndivided = 0, kStepSplit = 1, kStepSplitLong = 2 };
+int persistent_split_tasks_max(bool long_form);
 int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream,
-                           bool xcd_split = false);
+                           int form = kStepUndivided);
 // down_x for the XCD split from down [H, I] (I a multiple of 4, H of 8).
 int launch_regroup_down(const uint16_t* down, uint16_t* down_x, int H, int I, hipStream_t stream);
 

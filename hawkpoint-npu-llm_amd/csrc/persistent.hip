@@ -1231,7 +1231,12 @@ __device__ bool reduce_h(Ctx& c, int slice, unsigned pt, unsigned tag_h1, unsign
 // decode_step_kernel: launches of the two kernels may alternate.  Data the
 // XCD-local stores leave in XCD 0's L2 is written back at the end of the
 // launch, before another kernel can read it from another XCD.
-template <class S>
+// LONG: the long-context form.  A layer's attention tasks (heads x 256-slot
+// chunks) then outnumber XCD 0's row-free workgroups, so they run on the MLP
+// workgroups (one task each up to 224 tasks), which sit idle during the
+// attention block anyway; the QKV -> attention and attention -> O hand-offs
+// then cross XCDs (sc1), the rest is unchanged.
+template <class S, bool LONG>
 __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args) {
   __shared__ XShared sm;
   Ctx c;
@@ -1327,12 +1332,17 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
          // the other lanes the wave's pad word, one store per wave
         dot_group<Q.lpr, Q.nj, false, 0>(pf, sm.xs[buf], S::H, acc, accu);
         const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
-        const unsigned dst = is_q && lq && row_q < S::QKV ? o_qkv + (unsigned)row_q : pad;
-        __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_of(ep + 1)), tbuf, dst * 4u, 0, 0);
+        if constexpr (LONG) {  // to the MLP workgroups: gathered, one writer per workgroup
+          publish_rows<RQ, kSc1, kPW>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + rank * kPW * RQ,
+                                      S::QKV - rank * kPW * RQ, pad, true);
+        } else {
+          const unsigned dst = is_q && lq && row_q < S::QKV ? o_qkv + (unsigned)row_q : pad;
+          __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_of(ep + 1)), tbuf, dst * 4u, 0, 0);
+        }
       }
       if (is_q) buf ^= 1;
       // ---- A: tasks on the highest ranks, which hold no QKV or O rows ----
-      for (int t = kXcdWg - 1 - rank; t < tasks; t += kXcdWg) {
+      for (int t = kXcdWg - 1 - rank; !LONG && t < tasks; t += kXcdWg) {
         __syncthreads();  // LDS reuse
         if (!attention_task<S, kLocal>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2)))
           return;
@@ -1341,7 +1351,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       if (is_o) {
         bool ok = true;
         if (stager)
-          ok = stage_wave<S::AO, false, false, kLocal>(c, a.tattn, tag_of(ep + 2), nullptr, sm.xs[buf], nullptr);
+          ok = stage_wave<S::AO, false, false, LONG ? kSc1 : kLocal>(c, a.tattn, tag_of(ep + 2), nullptr,
+                                                                     sm.xs[buf], nullptr);
         if (!handoff(ok)) return;
       }
       {  // all eight waves
@@ -1374,6 +1385,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     // workgroups of this XCD with gate/up rows: local index j, rank 7 j + xcd - 1
     int nprod = 0;
     for (int j = 0; j < kXcdWg; ++j) nprod += (kXcds - 1) * j + xcd - 1 < S::xng ? 1 : 0;
+    const int tasks_l = S::HQ * (p / kChunk + 1);
     prefetch<G.lpr, G.nj, true, 0>(pf, sm.layers[0].gate_up, S::I, S::H, c.gw, pg);
     prefetch_down_x<S, OFF_D>(pf, sm.layers[0].down_x, c.gw, pg);
     for (int l = 0; l < L; ++l) {
@@ -1382,6 +1394,19 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       const bool more = l + 1 < L;
       const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
       const unsigned pt = ptag_of(ep + 4);
+      if constexpr (LONG) {
+        // ---- attention tasks (q/k/v from XCD 0, outputs back to it); the
+        // next layer's MLP weights go out after them, not ahead of their
+        // K/V loads and polls ----
+        for (int t = rank; t < tasks_l; t += kPersistentGrid - kXcdWg) {
+          __syncthreads();  // LDS reuse
+          if (!attention_task<S, kSc1>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2))) return;
+        }
+        if (l > 0) {
+          prefetch<G.lpr, G.nj, true, 0>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
+          prefetch_down_x<S, OFF_D>(pf, lw.down_x, c.gw, pg);
+        }
+      }
       // ---- gate/up + SwiGLU on h1 from XCD 0, then this wave's rows of down ----
       if (is_g) {
         bool ok = true;
@@ -1416,8 +1441,10 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (c.wave == kCW) ok = reduce_xcd<S>(c, xcd, jx, nprod, pt);
         if (!handoff(ok)) return;
       }
-      prefetch<G.lpr, G.nj, true, 0>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
-      prefetch_down_x<S, OFF_D>(pf, nx.down_x, c.gw, pg && more);
+      if constexpr (!LONG) {
+        prefetch<G.lpr, G.nj, true, 0>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
+        prefetch_down_x<S, OFF_D>(pf, nx.down_x, c.gw, pg && more);
+      }
     }
   }
   const unsigned ep_layers = base + 5u * (unsigned)L;
@@ -1437,11 +1464,14 @@ bool matches(int hidden, int intermediate, int q_heads, int kv_heads) {
 }
 
 template <class S>
-int launch_shape(const PersistentArgs& a, hipStream_t stream, bool xcd_split) {
-  if (xcd_split) {
-    if constexpr (S::xa)
-      hipLaunchKernelGGL(decode_step_xa_kernel<S>, dim3(kPersistentGrid), dim3(kPT), 0, stream, a);
-    else
+int launch_shape(const PersistentArgs& a, hipStream_t stream, int form) {
+  if (form != kStepUndivided) {
+    if constexpr (S::xa) {
+      if (form == kStepSplitLong)
+        hipLaunchKernelGGL((decode_step_xa_kernel<S, true>), dim3(kPersistentGrid), dim3(kPT), 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_step_xa_kernel<S, false>), dim3(kPersistentGrid), dim3(kPT), 0, stream, a);
+    } else
       return fail("persistent step: no XCD split for this model shape");
   } else {
     hipLaunchKernelGGL(decode_step_kernel<S>, dim3(kPersistentGrid), dim3(kPT), 0, stream, a);
@@ -1500,7 +1530,7 @@ int xcd_layout_ok(hipStream_t stream) {
 template <class S>
 int xcd_split_ok(hipStream_t stream) {
   if constexpr (S::xa) {
-    if (!occupancy_of(decode_step_xa_kernel<S>)) {
+    if (!occupancy_of(decode_step_xa_kernel<S, false>) || !occupancy_of(decode_step_xa_kernel<S, true>)) {
       set_error("XCD split: the split step kernel cannot keep one workgroup per CU");
       return 0;
     }
@@ -1538,7 +1568,7 @@ int persistent_xcd_split(int shape, hipStream_t stream) {
   }
 }
 
-int persistent_split_tasks_max() { return kXcdWg; }
+int persistent_split_tasks_max(bool long_form) { return long_form ? kPersistentGrid - kXcdWg : kXcdWg; }
 
 namespace {
 // down_x[((g * (H / 8) + c) * 8 + e) * 4 + j] = down[(8 c + e) * I + 4 g + j]
@@ -1563,12 +1593,12 @@ int launch_regroup_down(const uint16_t* down, uint16_t* down_x, int H, int I, hi
   return err == hipSuccess ? 0 : hip_fail(err, "regroup_down launch");
 }
 
-int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream, bool xcd_split) {
+int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream, int form) {
   if (a.layers <= 0 || a.layers > kPersistentMaxLayers) return fail("persistent step: layer count out of range");
   if (a.max_splits < (a.max_ctx + kChunk - 1) / kChunk) return fail("persistent step: partials too small");
   switch (shape) {
-    case 0: return launch_shape<SmolShape>(a, stream, xcd_split);
-    case 1: return launch_shape<QwenShape>(a, stream, xcd_split);
+    case 0: return launch_shape<SmolShape>(a, stream, form);
+    case 1: return launch_shape<QwenShape>(a, stream, form);
     default: return fail("persistent step: unsupported model shape");
   }
 }

@@ -150,13 +150,14 @@ class QwenDecoderEngine:
     def stream(self):
         return self._lib.hk_engine_stream(self._engine)
 
-    STEP_KINDS = {0: "kernels", 1: "persistent", 2: "xcd_split"}
+    STEP_KINDS = {0: "kernels", 1: "persistent", 2: "xcd_split", 3: "xcd_split_long"}
 
     def step_kind(self, position):
         """How a decode step at `position` runs: "kernels" (one kernel per
-        part, replayed as a hipGraph), "persistent" (one launch over all CUs)
-        or "xcd_split" (one launch, attention block on XCD 0, MLP on the
-        other XCDs)."""
+        part, replayed as a hipGraph), "persistent" (one launch over all CUs),
+        "xcd_split" (one launch, attention block on XCD 0, MLP on the other
+        XCDs) or "xcd_split_long" (the same with the attention tasks on the
+        MLP XCDs, for longer contexts)."""
         kind = ctypes.c_int32()
         hip.check(self._lib.hk_engine_step_kind(self._live(), int(position), ctypes.byref(kind)),
                   "hk_engine_step_kind")

@@ -170,14 +170,16 @@ int hk_engine_reset(hk_engine* engine);
 
 /* How a decode step at `position` runs, written to `kind_out`:
  * HK_STEP_KERNELS (one kernel per part, replayed as a hipGraph),
- * HK_STEP_PERSISTENT (one persistent launch over all CUs) or
+ * HK_STEP_PERSISTENT (one persistent launch over all CUs),
  * HK_STEP_XCD_SPLIT (one persistent launch with the attention block on XCD 0
- * and the MLP on the other XCDs; short contexts).  HK_ERR_INVALID for a
- * position outside the context.  No reference counterpart (the NPU engine
- * has one dispatch form). */
+ * and the MLP on the other XCDs; short contexts) or HK_STEP_XCD_SPLIT_LONG
+ * (the same with the attention tasks on the MLP XCDs; contexts up to 4096 for
+ * Qwen2.5-0.5B).  HK_ERR_INVALID for a position outside the context.  No
+ * reference counterpart (the NPU engine has one dispatch form). */
 #define HK_STEP_KERNELS 0
 #define HK_STEP_PERSISTENT 1
 #define HK_STEP_XCD_SPLIT 2
+#define HK_STEP_XCD_SPLIT_LONG 3
 int hk_engine_step_kind(hk_engine* engine, int32_t position, int32_t* kind_out);
 
 /* The engine's HIP stream (hipStream_t), for timing with events. */

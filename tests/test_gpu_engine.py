@@ -149,9 +149,10 @@ def test_long_context_split_kv():
 
 def test_xcd_split_is_selected_by_context():
     """On MI355X (8 XCDs, workgroup i on XCD i % 8) the Qwen step runs split
-    by XCD while the attention tasks of a layer (14 query heads x 256-slot
-    chunks) fit the 32 workgroups of XCD 0, i.e. below position 512, and as
-    one undivided launch beyond; HK_XCD_SPLIT=0 turns the split off, and
+    by XCD: with the attention tasks of a layer (14 query heads x 256-slot
+    chunks) on XCD 0 while they fit its 32 workgroups (below position 512),
+    on the 224 MLP workgroups while they fit those (below 4096), and as one
+    undivided launch beyond; HK_XCD_SPLIT=0 turns the split off, and
     HK_XCD_SPLIT=1 makes engine creation fail (with the reason) where the
     device cannot run it."""
     from runtime.qwen_engine import QwenDecoderEngine
@@ -162,15 +163,15 @@ def test_xcd_split_is_selected_by_context():
         if required:
             os.environ["HK_XCD_SPLIT"] = required
         try:
-            engine = QwenDecoderEngine(model, context_length=1024)
+            engine = QwenDecoderEngine(model, context_length=4100)
         finally:
             os.environ.pop("HK_XCD_SPLIT", None)
         try:
-            kinds = [engine.step_kind(p) for p in (0, 40, 511, 512, 1023)]
+            kinds = [engine.step_kind(p) for p in (0, 40, 511, 512, 4095, 4096, 4099)]
             announce(f"  kinds {kinds}")
-            assert kinds == ["xcd_split"] * 3 + ["persistent"] * 2
+            assert kinds == ["xcd_split"] * 3 + ["xcd_split_long"] * 2 + ["persistent"] * 2
             with pytest.raises(ValueError):
-                engine.step_kind(1024)
+                engine.step_kind(4100)
         finally:
             engine.close()
     os.environ["HK_XCD_SPLIT"] = "0"
@@ -192,6 +193,14 @@ def test_undivided_step_short_context(monkeypatch):
     _check_decode(model, _prompt(151936, 40, 12), 32, 72, label="qwen-4L-undivided")
 
 
+def test_undivided_step_long_context(monkeypatch):
+    """The undivided persistent step (HK_XCD_SPLIT=0) at positions past 256,
+    where its split-KV attention merges several chunks."""
+    monkeypatch.setenv("HK_XCD_SPLIT", "0")
+    model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
+    _check_decode(model, _prompt(151936, 600, 14), 8, 4096, label="qwen2-layer-ctx4096-undivided")
+
+
 def test_xcd_split_two_chunk_attention():
     """Positions 256..511 give each head two 256-slot chunks, merged by
     log-sum-exp, all on XCD 0 under the split."""
@@ -202,9 +211,10 @@ def test_xcd_split_two_chunk_attention():
 def test_xcd_split_agrees_with_undivided_step(monkeypatch):
     """The split and undivided kernels sum the QKV and O rows over different
     lane groups (8 lanes per row against 16 and 64), so they agree to float
-    tolerance; the greedy ids agree up to a near-tie.  The second engine also
-    alternates the two kernels (the split below 512, undivided above), which
-    share tags, epochs and flags from launch to launch."""
+    tolerance; the greedy ids agree up to a near-tie.  The second run also
+    alternates the two split forms (attention on XCD 0 below 512, on the MLP
+    XCDs above), which share tags, epochs and flags with each other and with
+    the undivided kernel from launch to launch."""
     from runtime.qwen_engine import QwenDecoderEngine
 
     announce("split vs undivided step")
@@ -235,7 +245,7 @@ def test_xcd_split_agrees_with_undivided_step(monkeypatch):
 
     l_split, g_split, g2_split, k_split = run(True)
     l_flat, g_flat, g2_flat, k_flat = run(False)
-    assert k_split == ("xcd_split", "persistent") and k_flat == ("persistent", "persistent")
+    assert k_split == ("xcd_split", "xcd_split_long") and k_flat == ("persistent", "persistent")
     errs = [rel_l2(a, b) for a, b in zip(l_split, l_flat)]
     announce(f"  rel-L2 split vs undivided {max(errs):.3e}; ids equal {g_split == g_flat}, {g2_split == g2_flat}")
     assert max(errs) <= 1e-2
