@@ -89,9 +89,6 @@ __device__ __forceinline__ unsigned ld_c32(const unsigned* p) {
 __device__ __forceinline__ void st_cf(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_cf(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void st_c64(unsigned long long* p, unsigned long long v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -743,16 +740,38 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
                                                __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (c.sm->ticket != nsplit - 1) return true;
+  // merge (wave 0, lane d = output d): the chunks' maxima spread over the
+  // lanes, then each lane folds its output over the chunks in order, kMergeBatch
+  // chunks at a time.  Device-coherent buffer loads, not atomics, so a batch
+  // goes out together instead of one round trip per load.
   if (tid < kHeadDim) {
-    const float* base = a.partial + (size_t)h * a.max_splits * kPartStride;
+    constexpr int kMergeBatch = 8;
+    const __amdgpu_buffer_rsrc_t pr =
+        rsrc(a.partial + (size_t)h * a.max_splits * kPartStride, nsplit * kPartStride * 4);
+    auto ldp = [&](int j, int k) {  // word k of chunk j's partial (zero past the chunks)
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           pr, j < nsplit ? (unsigned)(j * kPartStride + k) * 4u : kOutside, 0, kSc1));
+    };
     float mx = -INFINITY;
-    for (int j = 0; j < nsplit; ++j) mx = fmaxf(mx, ld_cf(base + (size_t)j * kPartStride + kHeadDim));
+    for (int j = tid; j < nsplit; j += kHeadDim) mx = fmaxf(mx, ldp(j, kHeadDim));
+    mx = wave_max64(mx);
     float lsum = 0.0f, r = 0.0f;
-    for (int j = 0; j < nsplit; ++j) {
-      const float* pj = base + (size_t)j * kPartStride;
-      const float f = __builtin_amdgcn_exp2f(ld_cf(pj + kHeadDim) - mx);
-      lsum = fmaf(ld_cf(pj + kHeadDim + 1), f, lsum);
-      r = fmaf(ld_cf(pj + tid), f, r);
+    for (int j0 = 0; j0 < nsplit; j0 += kMergeBatch) {
+      float mj[kMergeBatch], sj[kMergeBatch], oj[kMergeBatch];
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        mj[k] = ldp(j0 + k, kHeadDim);
+        sj[k] = ldp(j0 + k, kHeadDim + 1);
+        oj[k] = ldp(j0 + k, tid);
+      }
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        if (j0 + k < nsplit) {
+          const float f = __builtin_amdgcn_exp2f(mj[k] - mx);
+          lsum = fmaf(sj[k], f, lsum);
+          r = fmaf(oj[k], f, r);
+        }
+      }
     }
     store_out(tagged(f32_to_bf16(r / lsum), tag_a));
   }
