@@ -335,7 +335,7 @@ int launch_persistent(hk_engine* e, bool head) {
   a.pad = a.tact + d.intermediate;
   a.logits = e->logits;
   a.keys = e->keys;
-  a.partial = e->partial;
+  a.partial = reinterpret_cast<unsigned long long*>(e->partial);
   a.counters = e->counters;
   a.ctrl = e->ctrl;
   a.out_tokens = e->out_tokens;
@@ -349,6 +349,8 @@ int launch_persistent(hk_engine* e, bool head) {
 }
 
 size_t psync_words(const hk_engine*) { return (size_t)kPersistentGrid * kFlagStride; }
+
+size_t partial_floats(const hk_engine* e) { return (size_t)e->d.q_heads * e->max_splits * (kHeadDim + 2) * 2; }
 
 size_t ptag_words(const hk_engine* e) {
   const hk_model_desc& d = e->d;
@@ -369,6 +371,7 @@ int check_persistent(hk_engine* e, const int32_t* result_host) {
   HK_CHECK(hipMemset(e->ptag, 0, ptag_words(e) * sizeof(uint32_t)));
   if (e->wpart) HK_CHECK(hipMemset(e->wpart, 0, (size_t)kPersistentGrid * e->d.hidden * 8));
   if (e->xpart) HK_CHECK(hipMemset(e->xpart, 0, (size_t)8 * e->d.hidden * 8));
+  HK_CHECK(hipMemset(e->partial, 0, partial_floats(e) * sizeof(float)));
   HK_CHECK(hipMemset(e->counters, 0, e->d.q_heads * sizeof(unsigned int)));
   HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
   HK_CHECK(hipDeviceSynchronize());
@@ -652,7 +655,10 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     const size_t kv = (size_t)d.layers * kv_layer_elems(e);
     HK_TRY(dalloc(&e->kcache, kv));
     HK_TRY(dalloc(&e->vcache, kv));
-    HK_TRY(dalloc(&e->partial, (size_t)d.q_heads * e->max_splits * (kHeadDim + 2)));
+    // split-KV partials: floats for the per-kernel attention, 64-bit tagged
+    // words for the persistent step (twice the floats), zero to start
+    HK_TRY(dalloc(&e->partial, partial_floats(e)));
+    HK_CHECK(hipMemset(e->partial, 0, partial_floats(e) * sizeof(float)));
     HK_TRY(dalloc(&e->counters, d.q_heads));
     HK_TRY(dalloc(&e->keys, kMaxPartialKeys));
     HK_TRY(dalloc(&e->ctrl, 1));

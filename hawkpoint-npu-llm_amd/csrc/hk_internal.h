@@ -141,7 +141,9 @@ struct PersistentArgs {
   uint32_t* pad;    // [kPersistentGrid * 8] per-wave sink for stores of rows a wave does not own
   float* logits;             // [vocab + kPersistentGrid * 8]: the tail is a per-wave sink
   unsigned long long* keys;  // [kPersistentGrid]
-  float* partial;            // [Hq, max_splits, 66]
+  // [Hq, max_splits, 66] split-KV partials as (tag << 32) | float words;
+  // zero between launch sequences
+  unsigned long long* partial;
   unsigned int* counters;    // [Hq], zero between launches
   StepCtrl* ctrl;
   int32_t* out_tokens;

@@ -86,9 +86,6 @@ __device__ __forceinline__ void st_c32(unsigned* p, unsigned v) {
 __device__ __forceinline__ unsigned ld_c32(const unsigned* p) {
   return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_cf(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void st_c64(unsigned long long* p, unsigned long long v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -111,6 +108,18 @@ __device__ __forceinline__ bool reached(unsigned v, unsigned target) {
 __device__ __forceinline__ unsigned tag_of(unsigned e) { return e % 65535u + 1u; }
 
 __device__ __forceinline__ uint32_t tagged(uint32_t bf16, unsigned tag) { return (tag << 16) | bf16; }
+
+// Partial-sum words: (tag << 32) | float bits; the tag (epoch % (2^32 - 1) + 1)
+// is never 0, the value of cleared memory.  An aligned 8-byte store is seen
+// whole or not at all.
+__device__ __forceinline__ unsigned ptag_of(unsigned e) { return e % 0xffffffffu + 1u; }
+__device__ __forceinline__ unsigned long long pword(float v, unsigned t) {
+  return ((unsigned long long)t << 32) | __float_as_uint(v);
+}
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned long long ld_p64(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kSc1));
+}
 
 // ---- cross-lane sums with DPP ----
 // Within a 16-lane row DPP moves take a few cycles, against an LDS round trip
@@ -543,9 +552,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // ---- attention task: query head h, slots [s * kChunk, ...] of layer l ----
 // POL: cache policy of the q/k/v polls and the output store (kSc1 across
 // the device, kLocal when producers and consumers share an XCD).
-template <class S, int POL = kSc1>
+// ptag tags the split-KV partial words (ptag_of of the attention epoch); the
+// merging task loads MB chunks' words per round trip (a register budget).
+template <class S, int POL = kSc1, int MB = 8>
 __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_q,
-                               unsigned tag_a) {
+                               unsigned tag_a, unsigned ptag) {
   const PersistentArgs& a = *c.a;
   const int g = h / S::QPK;
   const int t0 = s * kChunk;
@@ -725,59 +736,73 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     return true;
   }
 
-  // split-KV: publish this chunk's (p @ V, max, sum); the last task of the
-  // head (ticket) merges all chunks with log-sum-exp rescaling
-  float* mine = a.partial + ((size_t)h * a.max_splits + s) * kPartStride;
-  if (tid < kHeadDim) st_cf(mine + tid, o);
-  if (tid == 0) {
-    st_cf(mine + kHeadDim, m);
-    st_cf(mine + kHeadDim + 1, sum);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0)
-    c.sm->ticket = (int)__hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (c.sm->ticket != nsplit - 1) return true;
-  // merge (wave 0, lane d = output d): the chunks' maxima spread over the
-  // lanes, then each lane folds its output over the chunks in order, kMergeBatch
-  // chunks at a time.  Device-coherent buffer loads, not atomics, so a batch
-  // goes out together instead of one round trip per load.
-  if (tid < kHeadDim) {
-    constexpr int kMergeBatch = 8;
-    const __amdgpu_buffer_rsrc_t pr =
-        rsrc(a.partial + (size_t)h * a.max_splits * kPartStride, nsplit * kPartStride * 4);
-    auto ldp = [&](int j, int k) {  // word k of chunk j's partial (zero past the chunks)
-      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                           pr, j < nsplit ? (unsigned)(j * kPartStride + k) * 4u : kOutside, 0, kSc1));
-    };
-    float mx = -INFINITY;
-    for (int j = tid; j < nsplit; j += kHeadDim) mx = fmaxf(mx, ldp(j, kHeadDim));
-    mx = wave_max64(mx);
-    float lsum = 0.0f, r = 0.0f;
-    for (int j0 = 0; j0 < nsplit; j0 += kMergeBatch) {
-      float mj[kMergeBatch], sj[kMergeBatch], oj[kMergeBatch];
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) {
-        mj[k] = ldp(j0 + k, kHeadDim);
-        sj[k] = ldp(j0 + k, kHeadDim + 1);
-        oj[k] = ldp(j0 + k, tid);
-      }
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) {
-        if (j0 + k < nsplit) {
-          const float f = __builtin_amdgcn_exp2f(mj[k] - mx);
-          lsum = fmaf(sj[k], f, lsum);
-          r = fmaf(oj[k], f, r);
-        }
-      }
+  // split-KV: every chunk but the last publishes its (P @ V, max, sum) as
+  // tagged 64-bit words and is done; the task of the last chunk (which holds
+  // slot p and has the fewest live slots) polls them and merges by
+  // log-sum-exp, chunks in order.  No completion wait or ticket: each word
+  // carries the epoch.
+  const __amdgpu_buffer_rsrc_t prs =
+      rsrc(a.partial + (size_t)h * a.max_splits * kPartStride, a.max_splits * kPartStride * 8);
+  if (s != nsplit - 1) {
+    if (tid < kPartStride) {
+      const float v = tid < kHeadDim ? o : tid == kHeadDim ? m : sum;
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, pword(v, ptag)), prs,
+                                            (s * kPartStride + tid) * 8, 0, kSc1);
     }
-    store_out(tagged(f32_to_bf16(r / lsum), tag_a));
+    return true;
   }
-  if (tid == 0)
-    (void)__hip_atomic_exchange(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return true;
+  // (ok is true here: the q/k/v polls succeeded)
+  if (tid < kHeadDim) {
+    constexpr int kMergeBatch = MB;
+    const int others = nsplit - 1;
+    // one pass over the chunks in order with a running maximum (each chunk
+    // has live slots, so its maximum is finite): a batch of chunks per round
+    // trip, no separate pass for the maxima
+    float mx = -INFINITY, lsum = 0.0f, r = 0.0f;
+    auto fold = [&](float mj, float sj, float oj) {
+      const float nm = fmaxf(mx, mj);
+      const float keep = __builtin_amdgcn_exp2f(mx - nm), f = __builtin_amdgcn_exp2f(mj - nm);
+      lsum = fmaf(sj, f, lsum * keep);
+      r = fmaf(oj, f, r * keep);
+      mx = nm;
+    };
+    // a batch of kMergeBatch chunks per round trip: lane k loads chunk
+    // j0 + k's (max, sum) pair (one 16-byte load), every lane its own output
+    // word of each chunk; readlane hands the pairs to the whole wave
+    static_assert(kMergeBatch <= 64, "one (max, sum) pair per lane");
+    for (int j0 = 0; ok && j0 < others; j0 += kMergeBatch) {
+      unsigned long long ow[kMergeBatch];
+      u32x4 ms;
+      for (unsigned spins = 1;; ++spins) {
+        const int jm = j0 + (int)tid;
+        ms = __builtin_amdgcn_raw_buffer_load_b128(
+            prs, (int)tid < kMergeBatch && jm < others ? (unsigned)(jm * kPartStride + kHeadDim) * 8u : kOutside, 0,
+            kSc1);
+        bool have = (int)tid >= kMergeBatch || jm >= others || (ms.y == ptag && ms.w == ptag);
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+          const int j = j0 + k;
+          ow[k] = ld_p64(prs, j < others ? (unsigned)(j * kPartStride + tid) * 8u : kOutside);
+          have = have && (j >= others || (unsigned)(ow[k] >> 32) == ptag);
+        }
+        if (__all(have)) break;
+        if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) {
+          ok = give_up(a);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k)
+        if (j0 + k < others)
+          fold(__uint_as_float((unsigned)__builtin_amdgcn_readlane((int)ms.x, k)),
+               __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)ms.z, k)),
+               __uint_as_float((unsigned)ow[k]));
+    }
+    fold(m, sum, o);  // this task's own chunk, the last
+    if (ok) store_out(tagged(f32_to_bf16(r / lsum), tag_a));
+  }
+  return !__syncthreads_or(!ok);
 }
 
 // Publish one GEMV phase's outputs.  Each compute wave parks its rows'
@@ -1031,7 +1056,8 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     // are not held across attention)
     for (int t = kPersistentGrid - 1 - c.wg; t < tasks; t += kPersistentGrid) {
       __syncthreads();  // LDS reuse
-      if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2))) return;
+      if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2), ptag_of(ep + 2)))
+        return;
     }
     prefetch<S::o.lpr, S::o.nj, false, S::off_o>(pf, lw.o, S::H, S::AO, c.gw, po);
     prefetch<S::g.lpr, S::g.nj, true, S::off_g>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
@@ -1096,16 +1122,10 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
 }
 
 // ---- the XCD split's fused down projection ----
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
 struct XShared : PShared {
   alignas(16) float wsum[kCW][kHMax];  // the compute waves' partial down products
 };
 
-// Partial-sum words: (tag << 32) | float bits; the tag (epoch % (2^32 - 1) + 1)
-// is never 0, the value of cleared memory.  An aligned 8-byte store is seen
-// whole or not at all.
-__device__ __forceinline__ unsigned ptag_of(unsigned e) { return e % 0xffffffffu + 1u; }
 
 // down_x rows of this wave's row group (four intermediate rows): chunk
 // c = lane + 64 k of the group's H / 8 output chunks goes to slots
@@ -1363,7 +1383,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       // ---- A: tasks on the highest ranks, which hold no QKV or O rows ----
       for (int t = kXcdWg - 1 - rank; !LONG && t < tasks; t += kXcdWg) {
         __syncthreads();  // LDS reuse
-        if (!attention_task<S, kLocal>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2)))
+        if (!attention_task<S, kLocal, 4>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2),
+                                          ptag_of(ep + 2)))
           return;
       }
       // ---- O: h1 to the MLP side ----
@@ -1419,7 +1440,9 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         // K/V loads and polls ----
         for (int t = rank; t < tasks_l; t += kPersistentGrid - kXcdWg) {
           __syncthreads();  // LDS reuse
-          if (!attention_task<S, kSc1>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2))) return;
+          if (!attention_task<S, kSc1, 16>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2),
+                                           ptag_of(ep + 2)))
+            return;
         }
         if (l > 0) {
           prefetch<G.lpr, G.nj, true, 0>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
