@@ -1610,7 +1610,10 @@ int persistent_xcd_split(int shape, hipStream_t stream) {
   }
 }
 
-int persistent_split_tasks_max(bool long_form) { return long_form ? kPersistentGrid - kXcdWg : kXcdWg; }
+// The short form runs up to 1.5 tasks per XCD-0 workgroup on average: measured
+// at 42 tasks (position 700) it is 6% faster than the long form, at 56 tasks
+// (position 960) level with it.
+int persistent_split_tasks_max(bool long_form) { return long_form ? kPersistentGrid - kXcdWg : kXcdWg + kXcdWg / 2; }
 
 namespace {
 // down_x[((g * (H / 8) + c) * 8 + e) * 4 + j] = down[(8 c + e) * I + 4 g + j]

@@ -150,8 +150,8 @@ def test_long_context_split_kv():
 def test_xcd_split_is_selected_by_context():
     """On MI355X (8 XCDs, workgroup i on XCD i % 8) the Qwen step runs split
     by XCD: with the attention tasks of a layer (14 query heads x 256-slot
-    chunks) on XCD 0 while they fit its 32 workgroups (below position 512),
-    on the 224 MLP workgroups while they fit those (below 4096), and as one
+    chunks) on XCD 0 while there are at most 48 (below position 768), on the
+    224 MLP workgroups while they fit those (below 4096), and as one
     undivided launch beyond; HK_XCD_SPLIT=0 turns the split off, and
     HK_XCD_SPLIT=1 makes engine creation fail (with the reason) where the
     device cannot run it."""
@@ -167,7 +167,7 @@ def test_xcd_split_is_selected_by_context():
         finally:
             os.environ.pop("HK_XCD_SPLIT", None)
         try:
-            kinds = [engine.step_kind(p) for p in (0, 40, 511, 512, 4095, 4096, 4099)]
+            kinds = [engine.step_kind(p) for p in (0, 40, 767, 768, 4095, 4096, 4099)]
             announce(f"  kinds {kinds}")
             assert kinds == ["xcd_split"] * 3 + ["xcd_split_long"] * 2 + ["persistent"] * 2
             with pytest.raises(ValueError):
@@ -212,7 +212,7 @@ def test_xcd_split_agrees_with_undivided_step(monkeypatch):
     """The split and undivided kernels sum the QKV and O rows over different
     lane groups (8 lanes per row against 16 and 64), so they agree to float
     tolerance; the greedy ids agree up to a near-tie.  The second run also
-    alternates the two split forms (attention on XCD 0 below 512, on the MLP
+    alternates the two split forms (attention on XCD 0 below 768, on the MLP
     XCDs above), which share tags, epochs and flags with each other and with
     the undivided kernel from launch to launch."""
     from runtime.qwen_engine import QwenDecoderEngine
@@ -235,10 +235,10 @@ def test_xcd_split_agrees_with_undivided_step(monkeypatch):
                     logits.append(lg.copy())
             first = int(np.argmax(logits[-1]))
             gen = engine.generate(first, len(prompt), 12)
-            # cross position 512 within one device-driven run: 505..520
-            engine.prefill(_prompt(151936, 505 - len(prompt) - 12, 18), len(prompt) + 12)
-            gen2 = engine.generate(gen[-1], 505, 16)
-            kinds = (engine.step_kind(505), engine.step_kind(520))
+            # cross position 768 within one device-driven run: 760..775
+            engine.prefill(_prompt(151936, 760 - len(prompt) - 12, 18), len(prompt) + 12)
+            gen2 = engine.generate(gen[-1], 760, 16)
+            kinds = (engine.step_kind(760), engine.step_kind(775))
             return logits, gen, gen2, kinds
         finally:
             engine.close()
