@@ -42,6 +42,16 @@
 // * Cross-workgroup data is written and read with device-coherent (sc1)
 //   accesses: the eight XCDs have separate L2 caches, and sc1 accesses bypass
 //   their incoherent state without whole-cache write-back or invalidate fences.
+//   Hand-offs between workgroups of one XCD may instead use its shared L2
+//   (kLocal): plain stores, sc0|nt loads.
+// * Two kernels share this protocol (tags, epochs, flags), so launches may
+//   alternate.  decode_step_kernel (above) spreads every phase over all 256
+//   workgroups.  decode_step_xa_kernel splits the step by XCD: the attention
+//   block on XCD 0, with its QKV -> attention -> O hand-offs inside that
+//   XCD's L2, and the MLP with down_proj fused in as split-K partials on the
+//   other seven.  Its long form moves the attention tasks to the MLP
+//   workgroups for contexts whose tasks outnumber XCD 0's.  The engine
+//   picks the kernel and form per launch from the position.
 // * Every wait is bounded: after spin_limit polls, or once another workgroup
 //   has flagged an error, the workgroup records the error and leaves; all
 //   later waits then end at once, so the launch always drains.  The host
