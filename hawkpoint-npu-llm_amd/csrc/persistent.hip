@@ -179,8 +179,8 @@ struct PhaseCfg {
 // Lanes per row (64, 32, 16 or 8) so that a wave owns at most one row group of
 // the phase at `waves` waves in the grid, with the group's chunks fitting in
 // `budget` prefetch registers.
-constexpr PhaseCfg pick_cfg(int M, int K, bool pair, int waves, int budget) {
-  for (int lpr = 64; lpr >= 8; lpr /= 2) {
+constexpr PhaseCfg pick_cfg(int M, int K, bool pair, int waves, int budget, int max_lpr = 64) {
+  for (int lpr = max_lpr; lpr >= 8; lpr /= 2) {
     const int rpw = 64 / lpr;
     const int groups = (M + rpw - 1) / rpw;
     const int nj = (K / 8 + lpr - 1) / lpr;
@@ -235,10 +235,12 @@ struct Shape {
   // K/V loads then go out at the start of the layer; O uses no more
   // workgroups than QKV (their stagers keep h for the residual)
   static constexpr int kAW = kXcdWg * kPW, kMW = (kPersistentGrid - kXcdWg) * kCW;
-  static constexpr PhaseCfg xq = pick_cfg(QKV, H, false, kAW, kPf / 2);
+  // (8 lanes per row: QKV on as few workgroups as the register budget allows)
+  static constexpr PhaseCfg xq = pick_cfg(QKV, H, false, kAW, kPf / 2, 8);
   static constexpr int xnq = producers(xq, QKV, kPW);
   static constexpr PhaseCfg xo = pick_cfg(H, AO, false, xnq * kPW, kPf / 2);
-  static constexpr PhaseCfg xg = pick_cfg(I, H, true, kMW, kPf / 2);
+  // (at most 16 lanes per row: the fused down takes four rows per wave)
+  static constexpr PhaseCfg xg = pick_cfg(I, H, true, kMW, kPf / 2, 16);
   static constexpr int xno = producers(xo, H, kPW), xng = producers(xg, I);
   // down is fused into the gate/up waves: a wave's four act values times
   // their down_x group, H / 8 output chunks over the 64 lanes (xkd each,
