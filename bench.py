@@ -58,6 +58,20 @@ def step_bytes(meta, position):
     return meta["layers"] * per_layer + head + 2 * h + kv_slot * (position + 1) + kv_slot
 
 
+def w8_step_bytes(meta, position):
+    """Algorithmic HBM bytes of one W8 decode step: int8 layer projections
+    with a float32 scale per output row, the bf16 LM head, qkv bias, norm
+    gains, the embedding row and the KV traffic of ``step_bytes``."""
+    h, i = meta["hidden_size"], meta["intermediate_size"]
+    nq, nkv, d = meta["attention_heads"], meta["kv_heads"], meta["head_dim"]
+    qkv = (nq + 2 * nkv) * d
+    rows = qkv + h + 2 * i + h
+    per_layer = (qkv * h + h * nq * d + 2 * i * h + h * i) + 4 * rows + 4 * qkv + 2 * 2 * h
+    head = 2 * meta["vocab_size"] * h + 2 * h
+    kv_slot = meta["layers"] * 2 * nkv * d * 2
+    return meta["layers"] * per_layer + head + 2 * h + kv_slot * (position + 1) + kv_slot
+
+
 def layer_params(meta):
     """Projection weights that every token multiplies (all layers, no head)."""
     h, i = meta["hidden_size"], meta["intermediate_size"]
@@ -316,6 +330,34 @@ def main():
     # which step kernel ran at the timed positions (both share one contract)
     split = engine.step_kind(end_pos) == "xcd_split"
     engine.close()
+
+    # the W8 decoder: int8 layer projections with per-row float32 scales and
+    # the bf16 LM head; the same 40-token prompt in one batched prefill, then
+    # 31 greedy steps (32 tokens), median of 5 runs
+    log("building the W8 engine (per-row int8 quantisation of the same weights)")
+    w8 = QwenDecoderEngine(model, context_length=4096, w8=True)
+    w8_first, w8_ttft = timed(lambda: w8.prefill(prompt, 0, want_logits_array=False)[0], 3)
+    w8.generate(w8_first, PROMPT, RUN)  # captures the step graph
+    w8_runs = []
+    for _ in range(5):
+        hip.check(lib.hk_stream_sync(w8.stream), "sync")
+        t0 = time.perf_counter()
+        w8.generate(w8_first, PROMPT, RUN)
+        w8_runs.append(RUN / (time.perf_counter() - t0))
+    w8_tok_s = sorted(w8_runs)[len(w8_runs) // 2]
+    w8_kind = w8.step_kind(PROMPT)
+    w8_kernel_us = None
+    if not args.no_parts:  # the W8 step kernel alone, as for the bf16 one above
+        ev0, ev1 = hip.Event(), hip.Event()
+        hip.check(lib.hk_engine_launch_part_repeat(w8._engine, hip.PART_STEP, n), "W8 step repeat")
+        ev0.record(w8.stream)
+        hip.check(lib.hk_engine_launch_part_repeat(w8._engine, hip.PART_STEP, n), "W8 step repeat")
+        ev1.record(w8.stream)
+        w8_kernel_us = ev0.elapsed_ms(ev1) * 1e3 / n
+    w8.close()
+    w8_gbs = w8_step_bytes(meta, mean_pos) * w8_tok_s / 1e9
+    log(f"W8 decode: {w8_tok_s:.1f} tok/s ({w8_kind} step), {w8_gbs:.0f} GB/s whole step, "
+        f"TTFT {w8_ttft * 1e3:.2f} ms, step kernel {w8_kernel_us} us")
     if split:
         kernel_name = "decode_step_xa_kernel (attention block on XCD 0, MLP on XCDs 1-7)"
         tfile = ROOT / "profiles" / "traffic_decode_step_xcd_split_qwen05b.json"
@@ -364,6 +406,19 @@ def main():
             "prefill_mfma_frac_of_bf16_dense": round(long_flops / t_long / BF16_PEAK, 4),
             "decode_tok_s": round(long_decode, 1),
             "decode_positions": [long_n, long_n + RUN - 1],
+        },
+        "w8_decode": {
+            "workload": "the same decoder with W8 layer projections (int8, per-output-row float32 "
+            "scale), bf16 activations, KV cache and LM head; 40-token prompt, 32 greedy tokens",
+            "tok_s": round(w8_tok_s, 1),
+            "step": w8_kind,
+            "ttft_ms": round(w8_ttft * 1e3, 3),
+            "step_bytes": int(w8_step_bytes(meta, mean_pos)),
+            "step_hbm_gbs": round(w8_gbs, 1),
+            "step_hbm_frac": round(w8_gbs / HBM_PEAK_GBS, 4),
+            "step_kernel_us": None if w8_kernel_us is None else round(w8_kernel_us, 2),
+            "step_kernel_gbs": None if w8_kernel_us is None else
+            round(w8_step_bytes(meta, end_pos) / (w8_kernel_us * 1e-6) / 1e9, 1),
         },
         "step_hbm_gbs": round(step_gbs, 1),
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),

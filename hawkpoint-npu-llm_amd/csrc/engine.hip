@@ -680,7 +680,9 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     // HK_XCD_SPLIT: 0 off, 1 required (creation fails with the reason when
     // the device cannot run it), unset: on where the device allows it
     const char* split = getenv("HK_XCD_SPLIT");
-    if (e->pshape >= 0 && !(split && split[0] == '0')) {
+    if (e->pshape >= 0 && w8 && split && split[0] == '1')
+      return fail("hk_engine_create: the XCD split step runs bf16 layer weights only");
+    if (e->pshape >= 0 && !w8 && !(split && split[0] == '0')) {
       e->xcd_split = persistent_xcd_split(e->pshape, e->stream) == 1;
       if (!e->xcd_split && split && split[0] == '1') return HK_ERR_INVALID;
     }
@@ -691,7 +693,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
         pl[l] = {static_cast<const uint16_t*>(lw.qkv),     lw.qkv_bias,
                  static_cast<const uint16_t*>(lw.o_proj),  static_cast<const uint16_t*>(lw.gate_up),
                  static_cast<const uint16_t*>(lw.down_proj), lw.input_norm, lw.post_attn_norm,
-                 nullptr};
+                 nullptr, lw.qkv_scale, lw.o_scale, lw.gate_up_scale, lw.down_scale};
       }
       if (e->xcd_split) {
         // the split fuses down_proj into the gate/up workgroups: a regrouped

@@ -104,6 +104,10 @@ constexpr int kPersistentChunk = 256;    // attention slots per task
 constexpr int kFlagStride = 32;          // uint32 words between flags (one 128-byte line each)
 constexpr int kPersistentMaxLayers = 128;
 
+// Layer weights of the persistent step.  For a W8 model the four projection
+// pointers hold int8 [rows, cols] and the *_scale pointers the float32 scale
+// of each output row (gate_up_scale: 2 I, gate rows first); for bf16 they
+// hold bf16 and the scales are null.
 struct PersistentLayer {
   const uint16_t* qkv;
   const float* qkv_bias;  // null when the model has none
@@ -117,6 +121,10 @@ struct PersistentLayer {
   // down[8c + e][4g + j], so one 16-byte chunk holds two outputs of all four
   // rows (see launch_regroup_down)
   const uint16_t* down_x;
+  const float* qkv_scale;
+  const float* o_scale;
+  const float* gate_up_scale;
+  const float* down_scale;
 };
 
 struct PersistentArgs {
@@ -159,7 +167,9 @@ struct PersistentArgs {
 
 constexpr unsigned kPersistentSpinLimit = 1u << 20;
 
-// Model shapes the persistent step is compiled for (-1: use the per-kernel step).
+// Model shapes the persistent step is compiled for: 0 SmolLM2-135M, 1
+// Qwen2.5-0.5B, 2 and 3 the same with W8 layer projections (-1: use the
+// per-kernel step).
 int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bool w8);
 // 1 when the step of this shape can also run split by XCD (attention block on
 // XCD 0, MLP on the others) on the current device; else 0 with the reason in

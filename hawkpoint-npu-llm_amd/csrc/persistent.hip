@@ -177,13 +177,13 @@ struct PhaseCfg {
 };
 
 // Lanes per row (64, 32, 16 or 8) so that a wave owns at most one row group of
-// the phase at `waves` waves in the grid, with the group's chunks fitting in
-// `budget` prefetch registers.
-constexpr PhaseCfg pick_cfg(int M, int K, bool pair, int waves, int budget, int max_lpr = 64) {
+// the phase at `waves` waves in the grid, with the group's 16-byte chunks
+// (`eb` bytes per weight) fitting in `budget` prefetch registers.
+constexpr PhaseCfg pick_cfg(int M, int K, bool pair, int waves, int budget, int max_lpr = 64, int eb = 2) {
   for (int lpr = max_lpr; lpr >= 8; lpr /= 2) {
     const int rpw = 64 / lpr;
     const int groups = (M + rpw - 1) / rpw;
-    const int nj = (K / 8 + lpr - 1) / lpr;
+    const int nj = (K * eb / 16 + lpr - 1) / lpr;
     if (groups <= waves && nj * (pair ? 2 : 1) <= budget) return {lpr, nj};
   }
   return {0, 0};
@@ -194,17 +194,21 @@ constexpr int producers(PhaseCfg c, int M, int waves_per_wg = kCW) {
   return ((M + 64 / c.lpr - 1) / (64 / c.lpr) + waves_per_wg - 1) / waves_per_wg;
 }
 
-template <int H_, int I_, int HQ_, int HKV_>
+// W8: the four layer projections are int8 with a float32 scale per output
+// row (16 weights per 16-byte chunk); the LM head stays bf16.
+template <int H_, int I_, int HQ_, int HKV_, bool W8_ = false>
 struct Shape {
   static constexpr int H = H_, I = I_, HQ = HQ_, HKV = HKV_;
+  static constexpr bool W8 = W8_;
+  static constexpr int EB = W8 ? 1 : 2;  // bytes per layer weight
   static constexpr int QPK = HQ / HKV;
   static constexpr int QKV = (HQ + 2 * HKV) * kHeadDim;
   static constexpr int AO = HQ * kHeadDim;
   static constexpr int kWaves = kPersistentGrid * kCW;
-  static constexpr PhaseCfg q = pick_cfg(QKV, H, false, kWaves, 4);
-  static constexpr PhaseCfg o = pick_cfg(H, AO, false, kWaves, 4);
-  static constexpr PhaseCfg d = pick_cfg(H, I, false, kWaves, 12);
-  static constexpr PhaseCfg g = pick_cfg(I, H, true, kWaves, kPf - o.nj - d.nj);
+  static constexpr PhaseCfg q = pick_cfg(QKV, H, false, kWaves, 4, 64, EB);
+  static constexpr PhaseCfg o = pick_cfg(H, AO, false, kWaves, 4, 64, EB);
+  static constexpr PhaseCfg d = pick_cfg(H, I, false, kWaves, 12, 64, EB);
+  static constexpr PhaseCfg g = pick_cfg(I, H, true, kWaves, kPf - o.nj - d.nj, 64, EB);
   // register slots: O and gate/up are requested together after attention;
   // down, and the next layer's QKV in the O slots, once O has been computed
   static constexpr int off_o = 0, off_g = o.nj, off_d = o.nj + 2 * g.nj, off_q = 0;
@@ -219,6 +223,7 @@ struct Shape {
   static_assert((I / 4 + 63) / 64 <= 32 && (H / 4 + 63) / 64 <= 32 && (AO / 4 + 63) / 64 <= 32,
                 "stager chunk mask is 32 bits");
   static_assert(H % 8 == 0 && I % 8 == 0 && AO % 8 == 0, "rows are read in 16-byte chunks");
+  static_assert(!W8 || (H % 16 == 0 && I % 16 == 0 && AO % 16 == 0), "int8 rows are read in 16-byte chunks");
   // residual rows are fetched by workgroups that have just seen the whole
   // source vector: O rows by Q producers, down rows by gate/up producers
   // the stager of an O-row workgroup saw all of h (Q phase), of a down-row
@@ -253,7 +258,7 @@ struct Shape {
   // slices of xhs outputs, xhn of them
   static constexpr int xhs = 32, xhn = (H + xhs - 1) / xhs;
   // O rows take their residual from the Q stagers' copy of h
-  static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
+  static constexpr bool xa = !W8 && xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
                              xnq + HQ <= kXcdWg && xhn <= (kXcdWg - xnq) * kSW &&
                              2 * xg.nj + 4 * xkd <= kPf && xno <= xnq && xsl <= 64 && H <= kHMax &&
                              I % 4 == 0 && xnq <= kXcdWg && xng <= kPersistentGrid - kXcdWg;
@@ -484,25 +489,35 @@ __device__ __forceinline__ void normalise_staged(Ctx& c, uint16_t* xs, float eps
 constexpr unsigned kOutside = 0x7ffffff0u;  // byte offset beyond every resource
 constexpr int kNT = 2;                      // buffer-load cache policy: non-temporal
 
-template <int LPR, int NJ, bool PAIR, int OFF>
-__device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const uint16_t* W, int M, int K,
+template <int LPR, int NJ, bool PAIR, int OFF, int EB = 2>
+__device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const void* W, int M, int K,
                                          int group, bool live_wg) {
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
   const int l = lane % LPR, sub = lane / LPR;
   const int row = group * RPW + sub;
   const bool live = live_wg && row < M;
-  const __amdgpu_buffer_rsrc_t r = rsrc(W, (PAIR ? 2 : 1) * M * K * 2);
+  const __amdgpu_buffer_rsrc_t r = rsrc(W, (PAIR ? 2 : 1) * M * K * EB);
   // one VGPR per lane: the chunk stride and the gate/up distance go in the
   // scalar offset.  Chunks past the row end read the next row (ignored by
   // dot_group) or, past the matrix, zero.
-  const unsigned voff = live ? (unsigned)row * (unsigned)K * 2u + (unsigned)l * 16u : kOutside;
+  const unsigned voff = live ? (unsigned)row * (unsigned)K * (unsigned)EB + (unsigned)l * 16u : kOutside;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     pf[OFF + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, j * LPR * 16, kNT);
     if constexpr (PAIR)
-      pf[OFF + NJ + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, M * K * 2 + j * LPR * 16, kNT);
+      pf[OFF + NJ + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, M * K * EB + j * LPR * 16, kNT);
   }
+}
+
+// Per-row float32 scale of a W8 phase, for the row prefetch() gives this lane
+// (1.0 for a row outside the matrix or a lane that takes no row).
+template <int LPR>
+__device__ __forceinline__ float row_scale(const float* scale, int M, int group, bool live_wg) {
+  const int row = group * (64 / LPR) + (threadIdx.x & 63) / LPR;
+  const unsigned off = live_wg && row < M ? (unsigned)row * 4u : kOutside;
+  const float s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(scale, M * 4), off, 0, 0));
+  return off == kOutside ? 1.0f : s;
 }
 
 // Eight bf16 products of a weight chunk and an x chunk, into two float32
@@ -528,9 +543,62 @@ __device__ __forceinline__ void fma8(const u32x4 w, const u32x4 x, float& a0, fl
 // first (a chunk past the row reads inside the staging buffer and is zeroed
 // by a select, not a branch), so the reads overlap instead of each paying
 // the LDS latency in turn.
-template <int LPR, int NJ, bool PAIR, int OFF>
+// Sixteen int8 weights (a 16-byte chunk) times sixteen bf16 x values: each
+// int8 becomes a float exactly, two of them one packed bf16 pair (integers up
+// to 127 need 7 significant bits: exact in bf16), then v_dot2 as for bf16
+// weights; the row scale is applied to the finished sum.
+__device__ __forceinline__ uint32_t i8pair_bf16(uint32_t w, int lo) {
+  const float f0 = (float)(int)(int8_t)(w >> (8 * lo));
+  const float f1 = (float)(int)(int8_t)(w >> (8 * lo + 8));
+  // bytes 2, 3 of f0 low, bytes 2, 3 of f1 high: one v_perm_b32
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
+}
+__device__ __forceinline__ void fma16_i8(const u32x4 w, const u32x4 x0, const u32x4 x1, float& a0, float& a1) {
+  a0 = dot2(i8pair_bf16(w.x, 0), x0.x, a0);
+  a1 = dot2(i8pair_bf16(w.x, 2), x0.y, a1);
+  a0 = dot2(i8pair_bf16(w.y, 0), x0.z, a0);
+  a1 = dot2(i8pair_bf16(w.y, 2), x0.w, a1);
+  a0 = dot2(i8pair_bf16(w.z, 0), x1.x, a0);
+  a1 = dot2(i8pair_bf16(w.z, 2), x1.y, a1);
+  a0 = dot2(i8pair_bf16(w.w, 0), x1.z, a0);
+  a1 = dot2(i8pair_bf16(w.w, 2), x1.w, a1);
+}
+
+template <int LPR, int NJ, bool PAIR, int OFF, int EB = 2>
 __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t* xs, int K,
                                           float& acc, float& accu) {
+  if constexpr (EB == 1) {
+    // chunk j of this lane: columns 16 (l + j LPR) .. + 15
+    static_assert((64 + (NJ - 1) * LPR) * 16 <= kXMax, "x reads stay inside the staging buffer");
+    const int l = (threadIdx.x & 63) % LPR;
+    const int CH = K / 16;
+    u32x4 xv[NJ][2];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      xv[j][0] = *reinterpret_cast<const u32x4*>(xs + (l + j * LPR) * 16);
+      xv[j][1] = *reinterpret_cast<const u32x4*>(xs + (l + j * LPR) * 16 + 8);
+    }
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      xv[j][0] = l + j * LPR < CH ? xv[j][0] : zero;
+      xv[j][1] = l + j * LPR < CH ? xv[j][1] : zero;
+    }
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      fma16_i8(pf[OFF + j], xv[j][0], xv[j][1], a0, a1);
+      if constexpr (PAIR) fma16_i8(pf[OFF + NJ + j], xv[j][0], xv[j][1], b0, b1);
+    }
+    if constexpr (LPR >= 16) {
+      acc = wave_sum<LPR>(a0 + a1);
+      accu = PAIR ? wave_sum<LPR>(b0 + b1) : 0.0f;
+    } else {
+      acc = group_sum<LPR>(a0 + a1);
+      accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
+    }
+    return;
+  }
   static_assert((64 + (NJ - 1) * LPR) * 8 <= kXMax, "x reads stay inside the staging buffer");
   const int l = (threadIdx.x & 63) % LPR;
   const int CH = K / 8;
@@ -1029,8 +1097,13 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
 
   u32x4 pf[kPf];
   float acc, accu, bias_q = 0.0f;
+  // W8 row scales of this lane's rows (QKV, O, gate, up, down)
+  float sq = 1.0f, so = 1.0f, sg = 1.0f, su = 1.0f, sd = 1.0f;
   int buf = 0;  // LDS staging buffer of the next GEMV phase
-  prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
+  // (a W8 scale is requested ahead of its rows: loads complete in order, so
+  // the wait for a scale issued later would also wait for later prefetches)
+  if constexpr (S::W8) sq = row_scale<S::q.lpr>(sm.layers[0].qkv_scale, S::QKV, c.gw, pq);
+  prefetch<S::q.lpr, S::q.nj, false, S::off_q, S::EB>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
   bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                          bias_rsrc<S>(sm.layers[0].qkv_bias), bias_off, 0, 0));
 
@@ -1058,7 +1131,8 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
       normalise_staged<S::H>(c, sm.xs[buf], a.eps);
     }
     if (!stager) {
-      dot_group<S::q.lpr, S::q.nj, false, S::off_q>(pf, sm.xs[buf], S::H, acc, accu);
+      dot_group<S::q.lpr, S::q.nj, false, S::off_q, S::EB>(pf, sm.xs[buf], S::H, acc, accu);
+      if constexpr (S::W8) acc *= sq;
       const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
       publish_rows<RQ>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + fq, nvq, pad, true);
     }
@@ -1071,8 +1145,13 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
       if (!attention_task<S>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2), ptag_of(ep + 2)))
         return;
     }
-    prefetch<S::o.lpr, S::o.nj, false, S::off_o>(pf, lw.o, S::H, S::AO, c.gw, po);
-    prefetch<S::g.lpr, S::g.nj, true, S::off_g>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
+    if constexpr (S::W8) {
+      so = row_scale<S::o.lpr>(lw.o_scale, S::H, c.gw, po);
+      sg = row_scale<S::g.lpr>(lw.gate_up_scale, S::I, c.gw, pg);
+      su = row_scale<S::g.lpr>(lw.gate_up_scale + S::I, S::I, c.gw, pg);
+    }
+    prefetch<S::o.lpr, S::o.nj, false, S::off_o, S::EB>(pf, lw.o, S::H, S::AO, c.gw, po);
+    prefetch<S::g.lpr, S::g.nj, true, S::off_g, S::EB>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
     // ---- O ----
     if (is_o) {
       bool ok = true;
@@ -1080,7 +1159,8 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
       if (!handoff(ok)) return;
     }
     if (!stager) {
-      dot_group<S::o.lpr, S::o.nj, false, S::off_o>(pf, sm.xs[buf], S::AO, acc, accu);
+      dot_group<S::o.lpr, S::o.nj, false, S::off_o, S::EB>(pf, sm.xs[buf], S::AO, acc, accu);
+      if constexpr (S::W8) acc *= so;
       publish_rows<RO>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
                        lo, tbuf, o_h1 + fo, nvo, pad, true);
     }
@@ -1088,10 +1168,14 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
     // issued there, they would queue in this CU's memory pipeline ahead of the
     // stagers' polls for the down input, the largest one of the layer
     {
-      prefetch<S::d.lpr, S::d.nj, false, S::off_d>(pf, lw.down, S::H, S::I, c.gw, pd);
       const bool more = l + 1 < L;
       const PersistentLayer& nx = sm.layers[more ? l + 1 : l];
-      prefetch<S::q.lpr, S::q.nj, false, S::off_q>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      if constexpr (S::W8) {
+        sd = row_scale<S::d.lpr>(lw.down_scale, S::H, c.gw, pd);
+        sq = row_scale<S::q.lpr>(nx.qkv_scale, S::QKV, c.gw, pq && more);
+      }
+      prefetch<S::d.lpr, S::d.nj, false, S::off_d, S::EB>(pf, lw.down, S::H, S::I, c.gw, pd);
+      prefetch<S::q.lpr, S::q.nj, false, S::off_q, S::EB>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
       bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
     }
@@ -1104,7 +1188,11 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
       normalise_staged<S::H>(c, sm.xs[buf], a.eps);
     }
     if (!stager) {
-      dot_group<S::g.lpr, S::g.nj, true, S::off_g>(pf, sm.xs[buf], S::H, acc, accu);
+      dot_group<S::g.lpr, S::g.nj, true, S::off_g, S::EB>(pf, sm.xs[buf], S::H, acc, accu);
+      if constexpr (S::W8) {
+        acc *= sg;
+        accu *= su;
+      }
       publish_rows<RG>(c, is_g, tagged(f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), tag_of(ep + 4)),
                        lg, tbuf, o_act + fg, nvg, pad, false);
     }
@@ -1116,7 +1204,8 @@ __global__ __launch_bounds__(kPT) void decode_step_kernel(PersistentArgs args) {
       if (!handoff(ok)) return;
     }
     if (!stager) {
-      dot_group<S::d.lpr, S::d.nj, false, S::off_d>(pf, sm.xs[buf], S::I, acc, accu);
+      dot_group<S::d.lpr, S::d.nj, false, S::off_d, S::EB>(pf, sm.xs[buf], S::I, acc, accu);
+      if constexpr (S::W8) acc *= sd;
       const uint32_t y = f32_to_bf16(round_bf16(acc) + sm.raw_h1[res_d]);
       publish_rows<RD>(c, is_d, tagged(y, tag_of(ep + 5)), ld, tbuf, o_h + fd, nvd, pad, false);
       // plain copy: the final hidden for hk_engine_final_hidden
@@ -1511,6 +1600,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
 
 using SmolShape = Shape<576, 1536, 9, 3>;
 using QwenShape = Shape<896, 4864, 14, 2>;
+using SmolShapeW8 = Shape<576, 1536, 9, 3, true>;
+using QwenShapeW8 = Shape<896, 4864, 14, 2, true>;
 
 template <class S>
 bool matches(int hidden, int intermediate, int q_heads, int kv_heads) {
@@ -1598,7 +1689,6 @@ int xcd_split_ok(hipStream_t stream) {
 }  // namespace
 
 int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bool w8) {
-  if (w8) return -1;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
@@ -1606,9 +1696,9 @@ int persistent_shape(int hidden, int intermediate, int q_heads, int kv_heads, bo
   // one resident workgroup per CU is what keeps every wait finite
   if (cus < kPersistentGrid) return -1;
   if (matches<QwenShape>(hidden, intermediate, q_heads, kv_heads))
-    return occupancy_ok<QwenShape>() ? 1 : -1;
+    return w8 ? (occupancy_ok<QwenShapeW8>() ? 3 : -1) : (occupancy_ok<QwenShape>() ? 1 : -1);
   if (matches<SmolShape>(hidden, intermediate, q_heads, kv_heads))
-    return occupancy_ok<SmolShape>() ? 0 : -1;
+    return w8 ? (occupancy_ok<SmolShapeW8>() ? 2 : -1) : (occupancy_ok<SmolShape>() ? 0 : -1);
   return -1;
 }
 
@@ -1616,6 +1706,9 @@ int persistent_xcd_split(int shape, hipStream_t stream) {
   switch (shape) {
     case 0: return xcd_split_ok<SmolShape>(stream);
     case 1: return xcd_split_ok<QwenShape>(stream);
+    case 2: case 3:
+      set_error("XCD split: bf16 layer weights only");
+      return 0;
     default:
       set_error("XCD split: no persistent step for this model shape");
       return 0;
@@ -1656,6 +1749,8 @@ int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t strea
   switch (shape) {
     case 0: return launch_shape<SmolShape>(a, stream, form);
     case 1: return launch_shape<QwenShape>(a, stream, form);
+    case 2: return launch_shape<SmolShapeW8>(a, stream, form);
+    case 3: return launch_shape<QwenShapeW8>(a, stream, form);
     default: return fail("persistent step: unsupported model shape");
   }
 }

@@ -140,6 +140,44 @@ def test_qwen_4_layer_w8_decode_within_1e2():
     _check_decode(model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen2.5-0.5b-4L-w8")
 
 
+def test_w8_step_is_persistent():
+    """W8 layer weights (int8 rows, float32 row scale applied to the finished
+    sum) run the undivided persistent step at every position; the XCD split
+    is bf16-only, and HK_XCD_SPLIT=1 makes a W8 engine fail to create."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("W8 step kind")
+    for meta in (QWEN25_05B, SMOLLM2_135M):
+        model = SyntheticModel(meta, seed=1, layers=1)
+        engine = QwenDecoderEngine(model, context_length=1100, w8=True)
+        try:
+            assert [engine.step_kind(p) for p in (0, 767, 1099)] == ["persistent"] * 3
+        finally:
+            engine.close()
+    os.environ["HK_XCD_SPLIT"] = "1"
+    try:
+        with pytest.raises(ValueError, match="bf16 layer weights only"):
+            QwenDecoderEngine(SyntheticModel(QWEN25_05B, seed=1, layers=1), context_length=64, w8=True)
+    finally:
+        os.environ.pop("HK_XCD_SPLIT", None)
+
+
+def test_smollm_4_layer_w8_decode_within_1e2():
+    model = SyntheticModel(SMOLLM2_135M, seed=0, layers=4)
+    _check_decode(model, _prompt(49152, 35, 15), 16, 64, w8=True, label="smollm2-4L-w8")
+
+
+def test_w8_long_context_split_kv():
+    model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
+    _check_decode(model, _prompt(151936, 600, 16), 8, 4096, w8=True, label="qwen-2L-ctx4096-w8")
+
+
+def test_per_kernel_path_w8_decode(monkeypatch):
+    monkeypatch.setenv("HK_PERSISTENT", "0")
+    model = SyntheticModel(QWEN25_05B, seed=0, layers=4)
+    _check_decode(model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen-4L-w8-per-kernel")
+
+
 def test_long_context_split_kv():
     """Positions past 256 take the split-KV attention path (several chunks
     merged by log-sum-exp); 2-layer model keeps the oracle quick."""
