@@ -680,9 +680,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     // HK_XCD_SPLIT: 0 off, 1 required (creation fails with the reason when
     // the device cannot run it), unset: on where the device allows it
     const char* split = getenv("HK_XCD_SPLIT");
-    if (e->pshape >= 0 && w8 && split && split[0] == '1')
-      return fail("hk_engine_create: the XCD split step runs bf16 layer weights only");
-    if (e->pshape >= 0 && !w8 && !(split && split[0] == '0')) {
+    if (e->pshape >= 0 && !(split && split[0] == '0')) {
       e->xcd_split = persistent_xcd_split(e->pshape, e->stream) == 1;
       if (!e->xcd_split && split && split[0] == '1') return HK_ERR_INVALID;
     }
@@ -697,12 +695,13 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
       }
       if (e->xcd_split) {
         // the split fuses down_proj into the gate/up workgroups: a regrouped
-        // copy per layer (H x I bf16 each) and the partial-sum words
+        // copy per layer (H x I weights each, bf16 or int8) and the
+        // partial-sum words
         e->down_x.assign(d.layers, nullptr);
         for (int l = 0; l < d.layers; ++l) {
-          HK_TRY(dalloc(&e->down_x[l], (size_t)d.hidden * d.intermediate));
-          HK_TRY(launch_regroup_down(static_cast<const uint16_t*>(e->layers[l].down_proj), e->down_x[l],
-                                     d.hidden, d.intermediate, e->stream));
+          HK_TRY(dalloc(&e->down_x[l], (size_t)d.hidden * d.intermediate / (w8 ? 2 : 1)));
+          HK_TRY(launch_regroup_down(e->layers[l].down_proj, e->down_x[l], d.hidden, d.intermediate, w8,
+                                     e->stream));
           pl[l].down_x = e->down_x[l];
         }
         HK_TRY(dalloc(&e->wpart, (size_t)kPersistentGrid * d.hidden));

@@ -117,9 +117,9 @@ struct PersistentLayer {
   const uint16_t* in_norm;
   const uint16_t* post_norm;
   // down_proj regrouped for the XCD split (null otherwise): for each group of
-  // four intermediate rows g, [H / 8][8][4] bf16 -- element (c, e, j) is
-  // down[8c + e][4g + j], so one 16-byte chunk holds two outputs of all four
-  // rows (see launch_regroup_down)
+  // four intermediate rows g, [H / R][R][4] -- element (c, e, j) is
+  // down[R c + e][4g + j], so one 16-byte chunk holds R / 4 outputs of all
+  // four rows (R = 8 for bf16, 16 for int8; see launch_regroup_down)
   const uint16_t* down_x;
   const float* qkv_scale;
   const float* o_scale;
@@ -184,8 +184,9 @@ enum StepForm : int { kStepUndivided = 0, kStepSplit = 1, kStepSplitLong = 2 };
 int persistent_split_tasks_max(bool long_form);
 int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t stream,
                            int form = kStepUndivided);
-// down_x for the XCD split from down [H, I] (I a multiple of 4, H of 8).
-int launch_regroup_down(const uint16_t* down, uint16_t* down_x, int H, int I, hipStream_t stream);
+// down_x for the XCD split from down [H, I] (bf16, or int8 when w8; I a
+// multiple of 4, H of 8, or of 16 for int8).
+int launch_regroup_down(const void* down, void* down_x, int H, int I, bool w8, hipStream_t stream);
 
 // ---- batched prefill (prefill.hip) ----
 

@@ -241,24 +241,25 @@ struct Shape {
   // workgroups than QKV (their stagers keep h for the residual)
   static constexpr int kAW = kXcdWg * kPW, kMW = (kPersistentGrid - kXcdWg) * kCW;
   // (8 lanes per row: QKV on as few workgroups as the register budget allows)
-  static constexpr PhaseCfg xq = pick_cfg(QKV, H, false, kAW, kPf / 2, 8);
+  static constexpr PhaseCfg xq = pick_cfg(QKV, H, false, kAW, kPf / 2, 8, EB);
   static constexpr int xnq = producers(xq, QKV, kPW);
-  static constexpr PhaseCfg xo = pick_cfg(H, AO, false, xnq * kPW, kPf / 2);
+  static constexpr PhaseCfg xo = pick_cfg(H, AO, false, xnq * kPW, kPf / 2, 64, EB);
   // (at most 16 lanes per row: the fused down takes four rows per wave)
-  static constexpr PhaseCfg xg = pick_cfg(I, H, true, kMW, kPf / 2, 16);
+  static constexpr PhaseCfg xg = pick_cfg(I, H, true, kMW, kPf / 2, 16, EB);
   static constexpr int xno = producers(xo, H, kPW), xng = producers(xg, I);
   // down is fused into the gate/up waves: a wave's four act values times
-  // their down_x group, H / 8 output chunks over the 64 lanes (xkd each,
-  // four 16-byte slots per chunk); each workgroup of an XCD then adds up xsl
-  // of the H outputs over the XCD's workgroups
-  static constexpr int xkd = (H / 8 + 63) / 64;
+  // their down_x group, xdc output chunks (8 outputs each, 16 for W8) over
+  // the 64 lanes (xkd each, four 16-byte slots per chunk); each workgroup of
+  // an XCD then adds up xsl of the H outputs over the XCD's workgroups
+  static constexpr int xdo = 16 / EB, xdc = H / xdo;
+  static constexpr int xkd = (xdc + 63) / 64;
   static constexpr int xsl = (H + kXcdWg - 1) / kXcdWg;
   // XCD 0 adds the XCD partials on the stager waves of its workgroups
   // without QKV/O rows (no weight prefetch queues ahead of their polls):
   // slices of xhs outputs, xhn of them
   static constexpr int xhs = 32, xhn = (H + xhs - 1) / xhs;
   // O rows take their residual from the Q stagers' copy of h
-  static constexpr bool xa = !W8 && xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
+  static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
                              xnq + HQ <= kXcdWg && xhn <= (kXcdWg - xnq) * kSW &&
                              2 * xg.nj + 4 * xkd <= kPf && xno <= xnq && xsl <= 64 && H <= kHMax &&
                              I % 4 == 0 && xnq <= kXcdWg && xng <= kPersistentGrid - kXcdWg;
@@ -1229,12 +1230,12 @@ struct XShared : PShared {
 
 
 // down_x rows of this wave's row group (four intermediate rows): chunk
-// c = lane + 64 k of the group's H / 8 output chunks goes to slots
-// OFF + 4k .. OFF + 4k + 3 (chunks past H / 8 and dead groups read zero).
+// c = lane + 64 k of the group's xdc output chunks goes to slots
+// OFF + 4k .. OFF + 4k + 3 (chunks past xdc and dead groups read zero).
 template <class S, int OFF>
 __device__ __forceinline__ void prefetch_down_x(u32x4 (&pf)[kPf], const uint16_t* dx, int group, bool live) {
-  constexpr int CC = S::H / 8;
-  const __amdgpu_buffer_rsrc_t r = rsrc(dx, S::I * S::H * 2);
+  constexpr int CC = S::xdc;
+  const __amdgpu_buffer_rsrc_t r = rsrc(dx, S::I * S::H * S::EB);
   const int lane = threadIdx.x & 63;
   const bool ok = live && group < S::I / 4;
 #pragma unroll
@@ -1248,13 +1249,37 @@ __device__ __forceinline__ void prefetch_down_x(u32x4 (&pf)[kPf], const uint16_t
 
 // This wave's partial down product: act (bf16 bits; lanes 16 s .. 16 s + 15
 // hold row s of the group) times the group's down_x chunks, written to ws[H].
+// For W8 (unscaled int8 down rows; the row scale is applied to the finished
+// sum in reduce_h) a chunk holds 16 outputs: slot q outputs 4q .. 4q + 3,
+// each as the four rows' int8 weights.
 template <class S, int OFF>
 __device__ __forceinline__ void down_partial(const u32x4 (&pf)[kPf], uint32_t act, float* ws) {
-  constexpr int CC = S::H / 8;
+  constexpr int CC = S::xdc;
   const int lane = threadIdx.x & 63;
   const uint32_t a0 = __shfl(act, 0, 64), a1 = __shfl(act, 16, 64);
   const uint32_t a2 = __shfl(act, 32, 64), a3 = __shfl(act, 48, 64);
   const uint32_t A01 = (a0 & 0xffffu) | (a1 << 16), A23 = (a2 & 0xffffu) | (a3 << 16);
+  if constexpr (S::W8) {
+#pragma unroll
+    for (int k = 0; k < S::xkd; ++k) {
+      const int cc = lane + 64 * k;
+      float o[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 w = pf[OFF + 4 * k + q];
+        o[4 * q] = dot2(i8pair_bf16(w.x, 0), A01, dot2(i8pair_bf16(w.x, 2), A23, 0.0f));
+        o[4 * q + 1] = dot2(i8pair_bf16(w.y, 0), A01, dot2(i8pair_bf16(w.y, 2), A23, 0.0f));
+        o[4 * q + 2] = dot2(i8pair_bf16(w.z, 0), A01, dot2(i8pair_bf16(w.z, 2), A23, 0.0f));
+        o[4 * q + 3] = dot2(i8pair_bf16(w.w, 0), A01, dot2(i8pair_bf16(w.w, 2), A23, 0.0f));
+      }
+      if (cc < CC) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          reinterpret_cast<float4*>(ws + 16 * cc)[q] = make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < S::xkd; ++k) {
     const int cc = lane + 64 * k;
@@ -1319,10 +1344,16 @@ __device__ bool reduce_xcd(Ctx& c, int xcd, int jx, int nprod, unsigned pt) {
 // poll it there), tagged in h across the device (the LM head polls it), and
 // as plain bf16.
 template <class S>
-__device__ bool reduce_h(Ctx& c, int slice, unsigned pt, unsigned tag_h1, unsigned tag_h, uint32_t* local) {
+__device__ bool reduce_h(Ctx& c, int slice, unsigned pt, unsigned tag_h1, unsigned tag_h, uint32_t* local,
+                         const float* dscale) {
   const PersistentArgs& a = *c.a;
   const int e = S::xhs * slice + c.lane;
   const bool live = c.lane < S::xhs && e < S::H;
+  // W8: the down row scale of output e, for the finished sum
+  float sd = 1.0f;
+  if constexpr (S::W8)
+    sd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                       rsrc(dscale, S::H * 4), live ? (unsigned)e * 4u : kOutside, 0, 0));
   const __amdgpu_buffer_rsrc_t r = rsrc(a.xpart, kXcds * S::H * 8);
   const __amdgpu_buffer_rsrc_t rh1 = rsrc(a.th1, S::H * 4);
   unsigned long long v[kXcds - 1];
@@ -1348,6 +1379,7 @@ __device__ bool reduce_h(Ctx& c, int slice, unsigned pt, unsigned tag_h1, unsign
     float sum = 0.0f;
 #pragma unroll
     for (int x = 0; x < kXcds - 1; ++x) sum += __uint_as_float((unsigned)v[x]);
+    if constexpr (S::W8) sum *= sd;
     const uint32_t y = f32_to_bf16(round_bf16(sum) + bf_lo(h1));
     __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_h), rsrc(local, S::H * 4), e * 4, 0, 0);
     __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_h), rsrc(a.th, S::H * 4), e * 4, 0, kSc1);
@@ -1446,8 +1478,14 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     const bool pq = is_q, po = is_o;
     const int tasks = S::HQ * (p / kChunk + 1);
     const int hslice = rank >= S::xnq ? (rank - S::xnq) * kSW + (c.wave - kCW) : S::xhn;
-    prefetch<Q.lpr, Q.nj, false, 0>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
-    prefetch<O.lpr, O.nj, false, OFF_O>(pf, sm.layers[0].o, S::H, S::AO, c.gw, po);
+    // W8 row scales, requested ahead of their rows (loads complete in order)
+    float sq = 1.0f, so = 1.0f;
+    if constexpr (S::W8) {
+      sq = row_scale<Q.lpr>(sm.layers[0].qkv_scale, S::QKV, c.gw, pq);
+      so = row_scale<O.lpr>(sm.layers[0].o_scale, S::H, c.gw, po);
+    }
+    prefetch<Q.lpr, Q.nj, false, 0, S::EB>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
+    prefetch<O.lpr, O.nj, false, OFF_O, S::EB>(pf, sm.layers[0].o, S::H, S::AO, c.gw, po);
     float bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                  bias_rsrc<S>(sm.layers[0].qkv_bias), bias_off, 0, 0));
     for (int l = 0; l < L; ++l) {
@@ -1470,7 +1508,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       {  // all eight waves; the rows go straight to XCD 0's L2 (only the
          // attention tasks there poll them): each row's first lane stores it,
          // the other lanes the wave's pad word, one store per wave
-        dot_group<Q.lpr, Q.nj, false, 0>(pf, sm.xs[buf], S::H, acc, accu);
+        dot_group<Q.lpr, Q.nj, false, 0, S::EB>(pf, sm.xs[buf], S::H, acc, accu);
+        if constexpr (S::W8) acc *= sq;
         const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
         if constexpr (LONG) {  // to the MLP workgroups: gathered, one writer per workgroup
           publish_rows<RQ, kSc1, kPW>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + rank * kPW * RQ,
@@ -1497,7 +1536,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
       }
       {  // all eight waves
-        dot_group<O.lpr, O.nj, false, OFF_O>(pf, sm.xs[buf], S::AO, acc, accu);
+        dot_group<O.lpr, O.nj, false, OFF_O, S::EB>(pf, sm.xs[buf], S::AO, acc, accu);
+        if constexpr (S::W8) acc *= so;
         publish_rows<RO, kSc1, kPW>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
                                     lo, tbuf, o_h1 + fo, S::H - fo, pad, true);
       }
@@ -1506,15 +1546,20 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       // block is done, while the MLP side computes: issued earlier, they
       // would queue in this CU's memory pipeline ahead of the attention
       // task's K/V loads and the O stagers' polls
-      prefetch<Q.lpr, Q.nj, false, 0>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      if constexpr (S::W8) {
+        sq = row_scale<Q.lpr>(nx.qkv_scale, S::QKV, c.gw, pq && more);
+        so = row_scale<O.lpr>(nx.o_scale, S::H, c.gw, po && more);
+      }
+      prefetch<Q.lpr, Q.nj, false, 0, S::EB>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
       bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
-      prefetch<O.lpr, O.nj, false, OFF_O>(pf, nx.o, S::H, S::AO, c.gw, po && more);
+      prefetch<O.lpr, O.nj, false, OFF_O, S::EB>(pf, nx.o, S::H, S::AO, c.gw, po && more);
       // ---- h = h1 + down(act) from the MLP XCDs' partials, on the stager
       // waves of the workgroups without rows (an abandoned wait ends every
       // later wait of the launch through the error word) ----
       if (stager && hslice < S::xhn &&
-          !reduce_h<S>(c, hslice, ptag_of(ep + 4), tag_of(ep + 3), tag_of(ep + 5), a.tact) && c.lane == 0)
+          !reduce_h<S>(c, hslice, ptag_of(ep + 4), tag_of(ep + 3), tag_of(ep + 5), a.tact, lw.down_scale) &&
+          c.lane == 0)
         sm.abort = 1;
     }
   } else {
@@ -1527,7 +1572,15 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     int nprod = 0;
     for (int j = 0; j < kXcdWg; ++j) nprod += (kXcds - 1) * j + xcd - 1 < S::xng ? 1 : 0;
     const int tasks_l = S::HQ * (p / kChunk + 1);
-    prefetch<G.lpr, G.nj, true, 0>(pf, sm.layers[0].gate_up, S::I, S::H, c.gw, pg);
+    float sg = 1.0f, su = 1.0f;  // W8 row scales of this lane's gate and up rows
+    auto scales_g = [&](const PersistentLayer& w, bool live) {
+      if constexpr (S::W8) {
+        sg = row_scale<G.lpr>(w.gate_up_scale, S::I, c.gw, live);
+        su = row_scale<G.lpr>(w.gate_up_scale + S::I, S::I, c.gw, live);
+      }
+    };
+    scales_g(sm.layers[0], pg);
+    prefetch<G.lpr, G.nj, true, 0, S::EB>(pf, sm.layers[0].gate_up, S::I, S::H, c.gw, pg);
     prefetch_down_x<S, OFF_D>(pf, sm.layers[0].down_x, c.gw, pg);
     for (int l = 0; l < L; ++l) {
       const PersistentLayer& lw = sm.layers[l];
@@ -1546,7 +1599,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
             return;
         }
         if (l > 0) {
-          prefetch<G.lpr, G.nj, true, 0>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
+          scales_g(lw, pg);
+          prefetch<G.lpr, G.nj, true, 0, S::EB>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
           prefetch_down_x<S, OFF_D>(pf, lw.down_x, c.gw, pg);
         }
       }
@@ -1557,7 +1611,11 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
         if (!stager) {
-          dot_group<G.lpr, G.nj, true, 0>(pf, sm.xs[buf], S::H, acc, accu);
+          dot_group<G.lpr, G.nj, true, 0, S::EB>(pf, sm.xs[buf], S::H, acc, accu);
+          if constexpr (S::W8) {
+            acc *= sg;
+            accu *= su;
+          }
           down_partial<S, OFF_D>(pf, f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), sm.wsum[c.wave]);
         }
         __syncthreads();
@@ -1585,7 +1643,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
       }
       if constexpr (!LONG) {
-        prefetch<G.lpr, G.nj, true, 0>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
+        scales_g(nx, pg && more);
+        prefetch<G.lpr, G.nj, true, 0, S::EB>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
         prefetch_down_x<S, OFF_D>(pf, nx.down_x, c.gw, pg && more);
       }
     }
@@ -1706,9 +1765,8 @@ int persistent_xcd_split(int shape, hipStream_t stream) {
   switch (shape) {
     case 0: return xcd_split_ok<SmolShape>(stream);
     case 1: return xcd_split_ok<QwenShape>(stream);
-    case 2: case 3:
-      set_error("XCD split: bf16 layer weights only");
-      return 0;
+    case 2: return xcd_split_ok<SmolShapeW8>(stream);
+    case 3: return xcd_split_ok<QwenShapeW8>(stream);
     default:
       set_error("XCD split: no persistent step for this model shape");
       return 0;
@@ -1721,24 +1779,31 @@ int persistent_xcd_split(int shape, hipStream_t stream) {
 int persistent_split_tasks_max(bool long_form) { return long_form ? kPersistentGrid - kXcdWg : kXcdWg + kXcdWg / 2; }
 
 namespace {
-// down_x[((g * (H / 8) + c) * 8 + e) * 4 + j] = down[(8 c + e) * I + 4 g + j]
-__global__ void regroup_down_kernel(const uint16_t* __restrict__ down, uint16_t* __restrict__ dx, int H, int I) {
+// down_x[((g * (H / R) + c) * R + e) * 4 + j] = down[(R c + e) * I + 4 g + j]
+// with R outputs per 16-byte chunk group: 8 for bf16, 16 for int8
+template <class T, int R>
+__global__ void regroup_down_kernel(const T* __restrict__ down, T* __restrict__ dx, int H, int I) {
   const size_t n = (size_t)H * I;
   for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < n; o += (size_t)gridDim.x * blockDim.x) {
     const int j = (int)(o & 3);
-    const int e = (int)((o >> 2) & 7);
-    const size_t gc = o >> 5;  // g * (H / 8) + c
-    const int c = (int)(gc % (size_t)(H / 8));
-    const int g = (int)(gc / (size_t)(H / 8));
-    dx[o] = down[(size_t)(8 * c + e) * I + 4 * g + j];
+    const int e = (int)((o >> 2) % R);
+    const size_t gc = o / (4 * R);  // g * (H / R) + c
+    const int c = (int)(gc % (size_t)(H / R));
+    const int g = (int)(gc / (size_t)(H / R));
+    dx[o] = down[(size_t)(R * c + e) * I + 4 * g + j];
   }
 }
 }  // namespace
 
-int launch_regroup_down(const uint16_t* down, uint16_t* down_x, int H, int I, hipStream_t stream) {
-  if (!down || !down_x || H <= 0 || I <= 0 || H % 8 != 0 || I % 4 != 0)
+int launch_regroup_down(const void* down, void* down_x, int H, int I, bool w8, hipStream_t stream) {
+  if (!down || !down_x || H <= 0 || I <= 0 || H % (w8 ? 16 : 8) != 0 || I % 4 != 0)
     return fail("regroup_down: bad arguments");
-  hipLaunchKernelGGL(regroup_down_kernel, dim3(1024), dim3(256), 0, stream, down, down_x, H, I);
+  if (w8)
+    hipLaunchKernelGGL((regroup_down_kernel<int8_t, 16>), dim3(1024), dim3(256), 0, stream,
+                       static_cast<const int8_t*>(down), static_cast<int8_t*>(down_x), H, I);
+  else
+    hipLaunchKernelGGL((regroup_down_kernel<uint16_t, 8>), dim3(1024), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(down), static_cast<uint16_t*>(down_x), H, I);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "regroup_down launch");
 }

@@ -140,26 +140,36 @@ def test_qwen_4_layer_w8_decode_within_1e2():
     _check_decode(model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen2.5-0.5b-4L-w8")
 
 
-def test_w8_step_is_persistent():
+def test_w8_step_forms():
     """W8 layer weights (int8 rows, float32 row scale applied to the finished
-    sum) run the undivided persistent step at every position; the XCD split
-    is bf16-only, and HK_XCD_SPLIT=1 makes a W8 engine fail to create."""
+    sum; the split's fused down scales each output after the cross-XCD sum)
+    take the same step forms by position as bf16: split by XCD below 4096,
+    undivided beyond, and undivided everywhere with HK_XCD_SPLIT=0."""
     from runtime.qwen_engine import QwenDecoderEngine
 
-    announce("W8 step kind")
-    for meta in (QWEN25_05B, SMOLLM2_135M):
-        model = SyntheticModel(meta, seed=1, layers=1)
-        engine = QwenDecoderEngine(model, context_length=1100, w8=True)
-        try:
-            assert [engine.step_kind(p) for p in (0, 767, 1099)] == ["persistent"] * 3
-        finally:
-            engine.close()
-    os.environ["HK_XCD_SPLIT"] = "1"
+    announce("W8 step kinds")
+    model = SyntheticModel(QWEN25_05B, seed=1, layers=1)
+    engine = QwenDecoderEngine(model, context_length=4100, w8=True)
     try:
-        with pytest.raises(ValueError, match="bf16 layer weights only"):
-            QwenDecoderEngine(SyntheticModel(QWEN25_05B, seed=1, layers=1), context_length=64, w8=True)
+        kinds = [engine.step_kind(p) for p in (0, 767, 768, 4095, 4096)]
+        assert kinds == ["xcd_split"] * 2 + ["xcd_split_long"] * 2 + ["persistent"]
+    finally:
+        engine.close()
+    smol = QwenDecoderEngine(SyntheticModel(SMOLLM2_135M, seed=1, layers=1), context_length=4100, w8=True)
+    try:
+        # 9 query heads: 153 attention tasks at position 4099, within the long form's 224
+        assert [smol.step_kind(p) for p in (0, 4099)] == ["xcd_split", "xcd_split_long"]
+    finally:
+        smol.close()
+    os.environ["HK_XCD_SPLIT"] = "0"
+    try:
+        flat = QwenDecoderEngine(model, context_length=1100, w8=True)
     finally:
         os.environ.pop("HK_XCD_SPLIT", None)
+    try:
+        assert [flat.step_kind(p) for p in (0, 1099)] == ["persistent"] * 2
+    finally:
+        flat.close()
 
 
 def test_smollm_4_layer_w8_decode_within_1e2():
@@ -246,7 +256,8 @@ def test_xcd_split_two_chunk_attention():
     _check_decode(model, _prompt(151936, 300, 16), 8, 512, label="qwen-2L-split-two-chunks")
 
 
-def test_xcd_split_agrees_with_undivided_step(monkeypatch):
+@pytest.mark.parametrize("w8", [False, True], ids=["bf16", "w8"])
+def test_xcd_split_agrees_with_undivided_step(monkeypatch, w8):
     """The split and undivided kernels sum the QKV and O rows over different
     lane groups (8 lanes per row against 16 and 64), so they agree to float
     tolerance; the greedy ids agree up to a near-tie.  The second run also
@@ -255,7 +266,7 @@ def test_xcd_split_agrees_with_undivided_step(monkeypatch):
     the undivided kernel from launch to launch."""
     from runtime.qwen_engine import QwenDecoderEngine
 
-    announce("split vs undivided step")
+    announce(f"split vs undivided step, w8={w8}")
     model = SyntheticModel(QWEN25_05B, seed=9, layers=4)
     prompt = _prompt(151936, 24, 17)
 
@@ -264,7 +275,7 @@ def test_xcd_split_agrees_with_undivided_step(monkeypatch):
             monkeypatch.delenv("HK_XCD_SPLIT", raising=False)
         else:
             monkeypatch.setenv("HK_XCD_SPLIT", "0")
-        engine = QwenDecoderEngine(model, context_length=1024)
+        engine = QwenDecoderEngine(model, context_length=1024, w8=w8)
         try:
             logits = []
             for pos, tok in enumerate(prompt):
