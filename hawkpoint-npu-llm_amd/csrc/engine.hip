@@ -497,6 +497,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     q.A = e->pf_xn;
     q.lda = H;
     q.W = static_cast<const uint16_t*>(lw.qkv);
+    q.scale = e->w8 ? lw.qkv_scale : nullptr;
     q.bias = lw.qkv_bias;
     q.Y = e->pf_qkv;
     q.ldy = e->qkv_rows;
@@ -527,6 +528,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     o.A = e->pf_att;
     o.lda = QD;
     o.W = static_cast<const uint16_t*>(lw.o_proj);
+    o.scale = e->w8 ? lw.o_scale : nullptr;
     o.resid = e->pf_x;
     o.ldr = H;
     o.Y = e->pf_h1;
@@ -543,6 +545,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     g.A = e->pf_xn;
     g.lda = H;
     g.W = static_cast<const uint16_t*>(lw.gate_up);
+    g.scale = e->w8 ? lw.gate_up_scale : nullptr;
     g.Y = e->pf_act;
     g.ldy = I;
     g.M = n;
@@ -556,6 +559,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     dn.A = e->pf_act;
     dn.lda = I;
     dn.W = static_cast<const uint16_t*>(lw.down_proj);
+    dn.scale = e->w8 ? lw.down_scale : nullptr;
     dn.resid = e->pf_h1;
     dn.ldr = H;
     dn.Y = e->pf_x;
@@ -796,8 +800,8 @@ int hk_engine_prefill(hk_engine* e, const int32_t* tokens_host, int32_t n, int32
     if (tokens_host[i] < 0 || tokens_host[i] >= e->d.vocab) return fail("token id outside the vocabulary");
   HK_CHECK(hipSetDevice(e->device));
   const bool want = logits_host != nullptr || next_token_host != nullptr;
-  if (e->w8 || (e->d.hidden % 32) || (e->d.intermediate % 32) || ((e->d.q_heads * kHeadDim) % 32)) {
-    // int8 weights and shapes off the MFMA tile use the decode step per position
+  if ((e->d.hidden % 32) || (e->d.intermediate % 32) || ((e->d.q_heads * kHeadDim) % 32)) {
+    // shapes off the MFMA tile use the decode step per position
     for (int i = 0; i < n; ++i) {
       const bool last = want && i == n - 1;
       HK_TRY(set_ctrl(e, tokens_host[i], start + i, 0));

@@ -70,6 +70,22 @@ __device__ __forceinline__ u32x4 load_stream16(const void* p) {
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *(global_u32x4*)p; }
 
+// Two int8 weights (bytes lo, lo + 1 of w) as one packed bf16 pair: each
+// becomes a float exactly, and integers up to 127 need 7 significant bits,
+// so the float's high half is the exact bf16; v_perm_b32 takes both halves.
+__device__ __forceinline__ uint32_t i8pair_bf16(uint32_t w, int lo) {
+  const float f0 = (float)(int)(int8_t)(w >> (8 * lo));
+  const float f1 = (float)(int)(int8_t)(w >> (8 * lo + 8));
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
+}
+
+// Eight int8 weights (one streaming 8-byte load) as eight bf16 values, in order.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4 load_stream_i8_bf16(const void* p) {
+  const u32x2_t q = __builtin_nontemporal_load((__attribute__((address_space(1))) const u32x2_t*)p);
+  return u32x4{i8pair_bf16(q.x, 0), i8pair_bf16(q.x, 2), i8pair_bf16(q.y, 0), i8pair_bf16(q.y, 2)};
+}
+
 // Butterfly sum over groups of `width` adjacent lanes (width a power of two).
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {

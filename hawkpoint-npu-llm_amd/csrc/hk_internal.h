@@ -194,6 +194,9 @@ struct PrefillGemmArgs {
   const uint16_t* A;      // [M, lda] bf16 activations (tokens x K)
   const uint16_t* W;      // [N, K] bf16 weights (SwiGLU: [2N, K], gate rows then up rows)
   const float* bias;      // [N] (EPI_BIAS)
+  // W8: W holds int8 [N, K] (SwiGLU [2N, K]) and scale the float32 scale of
+  // each weight row, applied to the finished sum; null for bf16 weights
+  const float* scale;
   const uint16_t* resid;  // [M, ldr] (EPI_RESID)
   uint16_t* Y;            // [M, ldy] bf16 output
   int M, N, K, lda, ldr, ldy;

@@ -544,16 +544,9 @@ __device__ __forceinline__ void fma8(const u32x4 w, const u32x4 x, float& a0, fl
 // first (a chunk past the row reads inside the staging buffer and is zeroed
 // by a select, not a branch), so the reads overlap instead of each paying
 // the LDS latency in turn.
-// Sixteen int8 weights (a 16-byte chunk) times sixteen bf16 x values: each
-// int8 becomes a float exactly, two of them one packed bf16 pair (integers up
-// to 127 need 7 significant bits: exact in bf16), then v_dot2 as for bf16
-// weights; the row scale is applied to the finished sum.
-__device__ __forceinline__ uint32_t i8pair_bf16(uint32_t w, int lo) {
-  const float f0 = (float)(int)(int8_t)(w >> (8 * lo));
-  const float f1 = (float)(int)(int8_t)(w >> (8 * lo + 8));
-  // bytes 2, 3 of f0 low, bytes 2, 3 of f1 high: one v_perm_b32
-  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
-}
+// Sixteen int8 weights (a 16-byte chunk) times sixteen bf16 x values: exact
+// bf16 pairs (i8pair_bf16), then v_dot2 as for bf16 weights; the row scale is
+// applied to the finished sum.
 __device__ __forceinline__ void fma16_i8(const u32x4 w, const u32x4 x0, const u32x4 x1, float& a0, float& a1) {
   a0 = dot2(i8pair_bf16(w.x, 0), x0.x, a0);
   a1 = dot2(i8pair_bf16(w.x, 2), x0.y, a1);

@@ -38,7 +38,9 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return (g / (1.0f + expf(-clipped))) * u;
 }
 
-template <bool PAIR>
+// W8: int8 weight rows, converted exactly to bf16 as they are loaded; the
+// row scale multiplies the finished sum in the epilogue.
+template <bool PAIR, bool W8 = false>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[kTM][kLdsRow];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[kTN][kLdsRow];
@@ -74,8 +76,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
   int arow = a_ok ? m0 + lr : 0;
   if (grouped) arow = a.a_rows ? a.a_rows[row_off + (a_ok ? m0 + lr : 0)] : row_off + arow;
   const uint16_t* a_src = a.A + (size_t)arow * a.lda + lk;
-  const uint16_t* w_src = Wb + (size_t)(w_ok ? n0 + lr : 0) * a.K + lk;
-  const uint16_t* u_src = Wb + (size_t)(w_ok ? n0 + lr + a.N : 0) * a.K + lk;
+  const size_t w_off = (size_t)(w_ok ? n0 + lr : 0) * a.K + lk;
+  const size_t u_off = (size_t)(w_ok ? n0 + lr + a.N : 0) * a.K + lk;
+  auto wload = [&](size_t off) -> u32x4 {
+    if constexpr (W8)
+      return load_stream_i8_bf16(reinterpret_cast<const int8_t*>(Wb) + off);
+    else
+      return load_stream16(Wb + off);
+  };
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
   f32x4 acc[2][2], accu[2][2];
@@ -92,9 +100,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
 
   for (int k0 = 0; k0 < a.K; k0 += kTK) {
     const u32x4 av = a_ok ? load16(a_src + k0) : zero;
-    const u32x4 wv = w_ok ? load_stream16(w_src + k0) : zero;
+    const u32x4 wv = w_ok ? wload(w_off + k0) : zero;
     u32x4 uv = zero;
-    if constexpr (PAIR) uv = w_ok ? load_stream16(u_src + k0) : zero;
+    if constexpr (PAIR) uv = w_ok ? wload(u_off + k0) : zero;
     __syncthreads();
     *reinterpret_cast<u32x4*>(&As[lr][lk]) = av;
     *reinterpret_cast<u32x4*>(&Ws[lr][lk]) = wv;
@@ -129,7 +137,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
         const int n = n0 + wn + j * 16 + (lane & 15);
         if (mt >= M || n >= a.N) continue;
         const int m = row_off + mt;
-        const float v = acc[i][j][r];
+        float v = acc[i][j][r], u = accu[i][j][r];
+        if constexpr (W8) {
+          v *= a.scale[n];
+          if constexpr (PAIR) u *= a.scale[a.N + n];
+        }
         uint16_t* y = a.Y + (size_t)m * a.ldy + n;
         switch (a.epi) {
           case EPI_BF16:
@@ -142,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
             *y = (uint16_t)f32_to_bf16(round_bf16(v) + bf16_to_f32(a.resid[(size_t)m * a.ldr + n]));
             break;
           case EPI_SWIGLU:
-            *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(v), round_bf16(accu[i][j][r])));
+            *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(v), round_bf16(u)));
             break;
           default:
             break;
@@ -234,7 +246,7 @@ constexpr int kBRow = kBK + 8;  // bf16 per LDS row (rows 144 B apart: no bank c
 // (token tiles varying fastest) and the y-th of gridDim.y runs of K steps,
 // and stores float32 partial sums to split_ws[y][m][outputs] (SwiGLU: up
 // outputs at N + n) for split_reduce_kernel.
-template <int BM, int BN, bool PAIR, bool SPLIT>
+template <int BM, int BN, bool PAIR, bool SPLIT, bool W8 = false>
 __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
   constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
   constexpr int MB = BM / 32;             // 16-row blocks per wave
@@ -278,14 +290,18 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
     a_ok[i] = m < a.M;
     a_src[i] = a.A + (size_t)(a_ok[i] ? m : 0) * a.lda + pk;
   }
-  const uint16_t* w_src[WL];
+  const void* w_src[WL];  // bf16, or int8 (W8) at the same element offset
   bool w_ok[WL];
 #pragma unroll
   for (int i = 0; i < WL; ++i) {
     const int r = pr + 32 * i;  // tile row: gate rows first, then up rows
     const int n = n0 + (PAIR ? r % BN : r);
     w_ok[i] = n < a.N;
-    w_src[i] = a.W + (size_t)((w_ok[i] ? n : 0) + (PAIR && r >= BN ? a.N : 0)) * a.K + pk;
+    const size_t off = (size_t)((w_ok[i] ? n : 0) + (PAIR && r >= BN ? a.N : 0)) * a.K + pk;
+    if constexpr (W8)
+      w_src[i] = reinterpret_cast<const int8_t*>(a.W) + off;
+    else
+      w_src[i] = a.W + off;
   }
 
   u32x4 av[AL], wv[WL];
@@ -293,7 +309,12 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
 #pragma unroll
     for (int i = 0; i < AL; ++i) av[i] = a_ok[i] ? load16(a_src[i] + k0) : zero;
 #pragma unroll
-    for (int i = 0; i < WL; ++i) wv[i] = w_ok[i] ? load_stream16(w_src[i] + k0) : zero;
+    for (int i = 0; i < WL; ++i) {
+      if constexpr (W8)
+        wv[i] = w_ok[i] ? load_stream_i8_bf16(static_cast<const int8_t*>(w_src[i]) + k0) : zero;
+      else
+        wv[i] = w_ok[i] ? load_stream16(static_cast<const uint16_t*>(w_src[i]) + k0) : zero;
+    }
   };
   auto store = [&](int b) {
 #pragma unroll
@@ -352,13 +373,19 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
         const int m = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
         const int n = n0 + wn + 16 * j + fr;
         if (m >= a.M || n >= a.N) continue;
-        const float v = acc[i][j][r];
+        float v = acc[i][j][r];
         if constexpr (SPLIT) {
           const int outs = PAIR ? 2 * a.N : a.N;
           float* part = a.split_ws + ((size_t)blockIdx.y * a.M + m) * outs;
           part[n] = v;
           if constexpr (PAIR) part[a.N + n] = accu[i][j][r];
           continue;
+        }
+        float u = 0.0f;
+        if constexpr (PAIR) u = accu[i][j][r];
+        if constexpr (W8) {
+          v *= a.scale[n];
+          if constexpr (PAIR) u *= a.scale[a.N + n];
         }
         uint16_t* y = a.Y + (size_t)m * a.ldy + n;
         switch (a.epi) {
@@ -372,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
             *y = (uint16_t)f32_to_bf16(round_bf16(v) + bf16_to_f32(a.resid[(size_t)m * a.ldr + n]));
             break;
           case EPI_SWIGLU:
-            if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(v), round_bf16(accu[i][j][r])));
+            if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(v), round_bf16(u)));
             break;
           default:
             break;
@@ -393,6 +420,10 @@ __global__ __launch_bounds__(kThreads) void split_reduce_kernel(PrefillGemmArgs 
     const float* part = a.split_ws + ((size_t)s * a.M + m) * outs;
     v += part[n];
     if (pair) u += part[a.N + n];
+  }
+  if (a.scale) {  // W8: the row scales, on the finished sums
+    v *= a.scale[n];
+    if (pair) u *= a.scale[a.N + n];
   }
   uint16_t* y = a.Y + (size_t)m * a.ldy + n;
   switch (a.epi) {
@@ -609,10 +640,9 @@ size_t split_ws_need(int M, int N, int K, bool pair) {
   return parts > 1 ? (size_t)parts * M * (pair ? 2 * N : N) : 0;
 }
 
-int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
-  if (a.M <= 0 || a.N <= 0 || a.K <= 0) return fail("prefill gemm: sizes must be positive");
-  if (a.K % kTK != 0) return fail("prefill gemm: K must be a multiple of 32");
-  if (a.lda % 8 != 0) return fail("prefill gemm: lda must be a multiple of 8");
+namespace {
+template <bool W8>
+int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   dim3 grid((a.N + kTN - 1) / kTN, (a.M + kTM - 1) / kTM);
   if (a.grp_count != nullptr) {
     if (a.max_groups <= 0 || a.max_rows <= 0 || a.n_groups == nullptr || a.grp_expert == nullptr ||
@@ -629,13 +659,13 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     const dim3 g(gemm_tiles(a.M, a.N), parts);
     if (split_bm(a.M) == 64) {
       if (pair)
-        hipLaunchKernelGGL((gemm_big_kernel<64, 64, true, true>), g, dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL((gemm_big_kernel<64, 64, true, true, W8>), g, dim3(kThreads), 0, stream, a);
       else
-        hipLaunchKernelGGL((gemm_big_kernel<64, 64, false, true>), g, dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL((gemm_big_kernel<64, 64, false, true, W8>), g, dim3(kThreads), 0, stream, a);
     } else if (pair) {
-      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, true, true>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, true, true, W8>), g, dim3(kThreads), 0, stream, a);
     } else {
-      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, false, true>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, false, true, W8>), g, dim3(kThreads), 0, stream, a);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "split gemm launch");
@@ -651,18 +681,27 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     const int bn = wide ? 128 : 64;
     const dim3 g(8 * ((mt * ((a.N + bn - 1) / bn) + 7) / 8));
     if (pair)
-      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, true, false>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, true, false, W8>), g, dim3(kThreads), 0, stream, a);
     else if (wide)
-      hipLaunchKernelGGL((gemm_big_kernel<kBM, 128, false, false>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 128, false, false, W8>), g, dim3(kThreads), 0, stream, a);
     else
-      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, false, false>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_big_kernel<kBM, 64, false, false, W8>), g, dim3(kThreads), 0, stream, a);
   } else if (pair) {
-    hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<true, W8>), grid, dim3(kThreads), 0, stream, a);
   } else {
-    hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<false, W8>), grid, dim3(kThreads), 0, stream, a);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "prefill gemm launch");
+}
+}  // namespace
+
+int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0) return fail("prefill gemm: sizes must be positive");
+  if (a.K % kTK != 0) return fail("prefill gemm: K must be a multiple of 32");
+  if (a.lda % 8 != 0) return fail("prefill gemm: lda must be a multiple of 8");
+  if (a.scale && a.grp_count) return fail("prefill gemm: int8 weights in grouped mode are not supported");
+  return a.scale ? launch_gemm<true>(a, stream) : launch_gemm<false>(a, stream);
 }
 
 int launch_embed_rows(const int32_t* tokens, int n, int vocab, const uint16_t* table, int H,

@@ -61,13 +61,13 @@ def test_gemm_bf16_matches_oracle(hk_lib, m, n, k, epi):
     check_bf16(y, ref, bound)
 
 
-def _prefill_case(model, prompt, new_tokens, context, tol, label):
+def _prefill_case(model, prompt, new_tokens, context, tol, label, w8=False):
     from runtime.qwen_engine import QwenDecoderEngine
 
-    announce(f"prefill parity {label}: prompt {len(prompt)} ctx {context}")
-    oracle = OracleDecoder(model, context)
+    announce(f"prefill parity {label}: prompt {len(prompt)} ctx {context} w8={w8}")
+    oracle = OracleDecoder(model, context, w8=w8)
     ref_tokens, ref_logits = oracle.generate_greedy(prompt, new_tokens)
-    engine = QwenDecoderEngine(model, context_length=context)
+    engine = QwenDecoderEngine(model, context_length=context, w8=w8)
     try:
         tok, logits = engine.prefill(prompt, 0)
         err = rel_l2(logits, ref_logits[0])
@@ -168,20 +168,20 @@ def test_prefill_continues_from_cached_prefix():
         engine.close()
 
 
-def test_prefill_w8_uses_step_path():
-    from runtime.qwen_engine import QwenDecoderEngine
+def test_prefill_w8_qwen_4_layer():
+    """W8 prefill on the MFMA GEMMs: int8 weight tiles converted exactly to
+    bf16 on load, the row scale applied to the finished sums (40 tokens: the
+    split-K GEMM and its reduce)."""
+    model = SyntheticModel(QWEN25_05B, seed=3, layers=4)
+    _prefill_case(model, _prompt(151936, 40, 16), 8, 72, 1e-2, "qwen-4L-w8", w8=True)
 
-    announce("prefill W8 (per-position path)")
-    model = SyntheticModel(QWEN25_05B, seed=3, layers=2)
-    prompt = _prompt(151936, 12, 16)
-    engine = QwenDecoderEngine(model, context_length=32, w8=True)
-    try:
-        t1, l1 = engine.prefill(prompt, 0)
-        engine.reset()
-        for pos, tok in enumerate(prompt[:-1]):
-            engine.step_token(tok, pos, logits=False)
-        t2, l2 = engine.step_token(prompt[-1], len(prompt) - 1)
-        assert t1 == t2
-        np.testing.assert_array_equal(l1, l2)
-    finally:
-        engine.close()
+
+def test_prefill_w8_smollm_4_layer():
+    model = SyntheticModel(SMOLLM2_135M, seed=3, layers=4)
+    _prefill_case(model, _prompt(49152, 35, 17), 8, 64, 1e-2, "smollm-4L-w8", w8=True)
+
+
+def test_prefill_w8_long_prompt():
+    """600 tokens: the 128-token-tile W8 GEMMs (no K split)."""
+    model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
+    _prefill_case(model, _prompt(151936, 600, 18), 4, 1024, 1e-2, "qwen-2L-600-w8", w8=True)
