@@ -60,6 +60,17 @@ __global__ void set_ctrl_kernel(StepCtrl* ctrl, int32_t token, int32_t position,
 
 __global__ void store_i32_kernel(int32_t* dst, int32_t value) { *dst = value; }
 
+// Zero n 32-bit words (a kernel rather than hipMemsetAsync, so that a
+// captured step graph can hold it).
+__global__ void clear_words_kernel(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Advance every workgroup's epoch of the persistent step by `count`.
+__global__ void skip_epochs_kernel(unsigned int* progress, int n, int stride, unsigned int count) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) progress[(size_t)i * stride] += count;
+}
+
 // Scratch shared by the single-operation entry points on one device.
 struct OpScratch {
   int device = -1;
@@ -168,6 +179,10 @@ struct hk_engine {
   unsigned int spin_limit = kPersistentSpinLimit;
   unsigned int* psync = nullptr;       // per-workgroup epochs
   uint32_t* ptag = nullptr;            // tagged activations: h, h1, qkv, attn, act
+  // a split launch ran since the last undivided one: the split never writes
+  // act[H..I), so those words may hold tags of an old undivided launch that
+  // recur after the 16-bit tags wrap; the next undivided launch clears act first
+  bool act_stale = false;
   hipGraphExec_t graph[2] = {nullptr, nullptr};
   std::map<long long, hipGraphExec_t> repeat_graphs;  // timing graphs by (part, count)
   bool use_graph = true;
@@ -345,7 +360,15 @@ int launch_persistent(hk_engine* e, bool head) {
   a.progress = e->psync;
   a.error = reinterpret_cast<unsigned int*>(e->result + 1);
   a.spin_limit = e->spin_limit;
-  return launch_persistent_step(e->pshape, a, e->stream, step_form(e));
+  const int form = step_form(e);
+  if (form != kStepUndivided) {
+    e->act_stale = true;
+  } else if (e->act_stale) {
+    hipLaunchKernelGGL(clear_words_kernel, dim3(8), dim3(256), 0, e->stream, a.tact, (int)d.intermediate);
+    HK_CHECK(hipGetLastError());
+    e->act_stale = false;
+  }
+  return launch_persistent_step(e->pshape, a, e->stream, form);
 }
 
 size_t psync_words(const hk_engine*) { return (size_t)kPersistentGrid * kFlagStride; }
@@ -929,6 +952,25 @@ int hk_engine_reset(hk_engine* e) {
   const size_t kv = (size_t)e->d.layers * kv_layer_elems(e) * sizeof(uint16_t);
   HK_CHECK(hipMemsetAsync(e->kcache, 0, kv, e->stream));
   HK_CHECK(hipMemsetAsync(e->vcache, 0, kv, e->stream));
+  // the persistent step's tagged words start over too: zero never matches a
+  // tag, so no word written before the reset can satisfy a later poll
+  if (e->ptag) HK_CHECK(hipMemsetAsync(e->ptag, 0, ptag_words(e) * sizeof(uint32_t), e->stream));
+  if (e->wpart) HK_CHECK(hipMemsetAsync(e->wpart, 0, (size_t)kPersistentGrid * e->d.hidden * 8, e->stream));
+  if (e->xpart) HK_CHECK(hipMemsetAsync(e->xpart, 0, (size_t)8 * e->d.hidden * 8, e->stream));
+  HK_CHECK(hipMemsetAsync(e->partial, 0, partial_floats(e) * sizeof(float), e->stream));
+  e->act_stale = false;
+  HK_CHECK(hipStreamSynchronize(e->stream));
+  return 0;
+}
+
+int hk_engine_skip_epochs(hk_engine* e, uint32_t count) {
+  if (!e) return fail("hk_engine_skip_epochs: null engine");
+  std::lock_guard<std::mutex> lock(e->mu);
+  if (e->pshape < 0) return 0;
+  HK_CHECK(hipSetDevice(e->device));
+  hipLaunchKernelGGL(skip_epochs_kernel, dim3(1), dim3(256), 0, e->stream, e->psync, kPersistentGrid,
+                     kFlagStride, (unsigned int)count);
+  HK_CHECK(hipGetLastError());
   HK_CHECK(hipStreamSynchronize(e->stream));
   return 0;
 }

@@ -45,7 +45,17 @@ from runtime.sampling import GREEDY, Sampler, SamplingParams
 from runtime.stopping import StopMatcher, log_softmax, normalize_logprobs, normalize_stop
 from runtime.tokenizer import StreamDetokenizer
 
-__all__ = ["NPUDecoder"]
+__all__ = ["NPUDecoder", "default_system_prompt"]
+
+QWEN2_SYSTEM = "You are Qwen, created by Alibaba Cloud. You are a helpful assistant."
+SMOLLM_SYSTEM = "You are a helpful AI assistant named SmolLM."
+
+
+def default_system_prompt(model_family):
+    """System turn the chat template adds when the messages carry none: Qwen's
+    own for ``model_family == "qwen2"``, SmolLM's otherwise
+    (npu_llm/runtime/generate.py:47-51)."""
+    return QWEN2_SYSTEM if model_family == "qwen2" else SMOLLM_SYSTEM
 
 
 def _load_model(model):
@@ -90,7 +100,7 @@ class NPUDecoder:
         if isinstance(model_dir, (str, os.PathLike)) and (Path(model_dir) / "tokenizer.json").exists():
             from runtime.tokenizer import SmolLMTokenizer
 
-            self.tokenizer = SmolLMTokenizer(model_dir)
+            self.tokenizer = SmolLMTokenizer(model_dir, default_system=default_system_prompt(self.model_family))
         self._qwen_embedding_cache = OrderedDict()
 
     # -- step ------------------------------------------------------------------

@@ -98,6 +98,7 @@ _SIGNATURES = {
     "hk_engine_launch_part_repeat": (ctypes.c_int, [_vp, _i32, _i32]),
     "hk_gemv_repeat": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "hk_engine_reset": (ctypes.c_int, [_vp]),
+    "hk_engine_skip_epochs": (ctypes.c_int, [_vp, ctypes.c_uint32]),
     "hk_engine_stream": (_vp, [_vp]),
     "hk_engine_step_kind": (ctypes.c_int, [_vp, _i32, ctypes.POINTER(_i32)]),
     "hk_engine_destroy": (None, [_vp]),

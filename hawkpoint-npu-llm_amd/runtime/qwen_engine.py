@@ -171,6 +171,11 @@ class QwenDecoderEngine:
     def reset(self):
         hip.check(self._lib.hk_engine_reset(self._live()), "hk_engine_reset")
 
+    def skip_epochs(self, count):
+        """Test hook: advance the persistent step's epoch counter by ``count``
+        (see hk_engine_skip_epochs)."""
+        hip.check(self._lib.hk_engine_skip_epochs(self._live(), int(count)), "hk_engine_skip_epochs")
+
     def step(self, embedding, position, logits=True):
         """Run every layer for one token given its bf16 embedding row (uint16
         bits, [H]) and return its float32 logits (None with ``logits=False``).

@@ -165,8 +165,15 @@ int hk_gemv_repeat(const void* const* weights, const float* const* scales, int32
                    const uint16_t* x, float* y_f32, int32_t M, int32_t K, int32_t count,
                    void* stream);
 
-/* Zero the KV cache (QwenDecoderEngine.reset, qwen_engine.py:65-66). */
+/* Zero the KV cache (QwenDecoderEngine.reset, qwen_engine.py:65-66), and the
+ * persistent step's tagged activations and partial sums. */
 int hk_engine_reset(hk_engine* engine);
+
+/* Test hook: advance the persistent step's epoch counter by `count`, as if
+ * that many epochs (about 121 per Qwen2.5-0.5B step) had passed with no
+ * launch, so tests can put a launch at any residue of the 16-bit activation
+ * tags.  No effect on the per-kernel step.  No reference counterpart. */
+int hk_engine_skip_epochs(hk_engine* engine, uint32_t count);
 
 /* How a decode step at `position` runs, written to `kind_out`:
  * HK_STEP_KERNELS (one kernel per part, replayed as a hipGraph),

@@ -20,6 +20,7 @@ generate.py:215-223, 832 embed   ``OracleDecoder.decode_token``
 generate.py:709-730 argmax       ``decode_result``
 generate.py:830-846 CPU step     ``OracleDecoder.decode_token``
 generate.py:1110-1158 loop       ``OracleDecoder.generate_greedy``
+generate.py:1110-1125 prefill    ``OracleDecoder.prefill`` (rows at once)
 ===============================  =========================================
 
 BF16 tensors are carried as uint16 bit patterns because ``ml_dtypes`` is not
@@ -55,6 +56,7 @@ import time
 import numpy as np
 
 from oracle.bf16 import from_bits, round_f32, to_bits
+from oracle.quant import project_w8
 
 __all__ = ["CPUDecoderStage", "OracleDecoder", "decode_result", "rope_inv_frequency"]
 
@@ -110,19 +112,38 @@ class CPUDecoderStage:
     def project(self, name, activation):
         """``bf16(W_f32 @ f32(bf16(x)))`` or, in W8 mode for layer weights,
         ``bf16((f32(q) @ f32(bf16(x))) * scale)``."""
-        x = round_f32(activation)
         if self.w8 and name != "lm_head":
-            if name not in self._quant:
-                self._quant[name] = self.model.quantized(name)
-            q = self._quant[name]
-            acc = np.asarray(q.weight, dtype=np.float32) @ x
+            q = self.quantized(name)
+            return project_w8(q.weight, q.scale, activation)
+        return round_f32(from_bits(self.weight(name)) @ round_f32(activation))
+
+    def quantized(self, name):
+        if name not in self._quant:
+            self._quant[name] = self.model.quantized(name)
+        return self._quant[name]
+
+    def project_rows(self, name, rows):
+        """``project`` applied to every row of ``rows`` [n, K] at once: one
+        matrix product instead of n matrix-vector products, so only the
+        float32 summation order differs from calling ``project`` per row."""
+        x = round_f32(rows)
+        if self.w8 and name != "lm_head":
+            q = self.quantized(name)
+            acc = x @ np.asarray(q.weight, dtype=np.float32).T
             return round_f32(acc * np.asarray(q.scale, dtype=np.float32))
-        return round_f32(from_bits(self.weight(name)) @ x)
+        return round_f32(x @ from_bits(self.weight(name)).T)
 
     def norm(self, activation, gamma_name):
         """``bf16((v * inv) * gamma)`` with ``inv = 1/sqrt(mean(v*v) + eps)``."""
         value = round_f32(activation)
         inverse_rms = 1.0 / np.sqrt(np.mean(value * value, dtype=np.float32) + self.epsilon)
+        return round_f32(value * inverse_rms * self.raw(gamma_name))
+
+    def norm_rows(self, rows, gamma_name):
+        """``norm`` of every row of ``rows`` [n, H]."""
+        value = round_f32(rows)
+        mean = np.mean(value * value, axis=-1, dtype=np.float32, keepdims=True)
+        inverse_rms = 1.0 / np.sqrt(mean + self.epsilon)
         return round_f32(value * inverse_rms * self.raw(gamma_name))
 
     def rope_tables(self, position):
@@ -160,6 +181,66 @@ class CPUDecoderStage:
         probabilities /= np.sum(probabilities, axis=-1, keepdims=True)
         out = np.einsum("kqs,ksd->kqd", probabilities, values, optimize=True)
         return round_f32(out.reshape(-1))
+
+    def attention_rows(self, qkv_rows, layer, start, block=256):
+        """``attention`` for rows at positions start..start+n-1 at once: every
+        row's RoPE and KV append first, then each row attends to slots
+        0..its position (causal), as n calls of ``attention`` in order would.
+        Rows are scored in blocks of ``block`` to bound the score matrix."""
+        d = self.head_dim
+        nq = self.q_heads * d
+        nkv = self.kv_heads * d
+        qkv_rows = np.asarray(qkv_rows, dtype=np.float32)
+        n = qkv_rows.shape[0]
+        positions = np.arange(start, start + n)
+        half = d // 2
+        angle = positions.astype(np.float32)[:, None] * self._rope_inv_frequency[None, :]
+        cosine, sine = np.cos(angle)[:, None, :], np.sin(angle)[:, None, :]
+
+        def rotate_rows(heads):
+            first, second = heads[..., :half], heads[..., half:]
+            return round_f32(np.concatenate(
+                [first * cosine - second * sine, second * cosine + first * sine], axis=-1))
+
+        query = rotate_rows(qkv_rows[:, :nq].reshape(n, self.q_heads, d))
+        key = rotate_rows(qkv_rows[:, nq:nq + nkv].reshape(n, self.kv_heads, d))
+        value = qkv_rows[:, nq + nkv:].reshape(n, self.kv_heads, d)
+        self.key_cache[layer][:, start:start + n] = to_bits(key).transpose(1, 0, 2)
+        self.value_cache[layer][:, start:start + n] = to_bits(value).transpose(1, 0, 2)
+        end = start + n
+        keys = from_bits(self.key_cache[layer][:, :end])      # [kvh, end, d]
+        values = from_bits(self.value_cache[layer][:, :end])
+        out = np.empty((n, self.q_heads, d), dtype=np.float32)
+        grouped = query.reshape(n, self.kv_heads, self.q_per_kv, d)
+        slots = np.arange(end)
+        for r0 in range(0, n, block):
+            r1 = min(n, r0 + block)
+            q = grouped[r0:r1].transpose(1, 0, 2, 3)          # [kvh, rows, qpk, d]
+            scores = np.einsum("krqd,ksd->krqs", q, keys, optimize=True) * d**-0.5
+            future = slots[None, :] > positions[r0:r1, None]  # [rows, end]
+            scores[:, future[:, None, :].repeat(self.q_per_kv, axis=1)] = -np.inf
+            scores -= np.max(scores, axis=-1, keepdims=True)
+            probabilities = np.exp(scores)
+            probabilities /= np.sum(probabilities, axis=-1, keepdims=True)
+            o = np.einsum("krqs,ksd->krqd", probabilities, values, optimize=True)
+            out[r0:r1] = o.transpose(1, 0, 2, 3).reshape(r1 - r0, self.q_heads, d)
+        return round_f32(out.reshape(n, -1))
+
+    def layer_rows(self, hidden_rows, layer, start):
+        """``layer`` for rows at positions start..start+n-1 at once."""
+        p = f"layer{layer:02d}"
+        hidden_rows = np.asarray(hidden_rows, dtype=np.float32)
+        normalized = self.norm_rows(hidden_rows, f"{p}.input_norm")
+        bias_name = f"{p}.qkv_bias"
+        bias = self.raw(bias_name) if bias_name in self.model.tensors else 0.0
+        qkv = round_f32(self.project_rows(f"{p}.qkv", normalized) + bias)
+        attended = self.attention_rows(qkv, layer, start)
+        after_attention = round_f32(self.project_rows(f"{p}.o_proj", attended) + hidden_rows)
+        post = self.norm_rows(after_attention, f"{p}.post_attn_norm")
+        gate_up = self.project_rows(f"{p}.gate_up", post)
+        gate, up = np.split(gate_up, 2, axis=-1)
+        activation = round_f32((gate / (1.0 + np.exp(-np.clip(gate, -80.0, 80.0)))) * up)
+        return round_f32(self.project_rows(f"{p}.down_proj", activation) + after_attention)
 
     def layer(self, hidden, layer, position):
         p = f"layer{layer:02d}"
@@ -237,6 +318,25 @@ class OracleDecoder:
         if not compute_logits:
             return None, None
         logits = self.stage.logits(hidden)
+        return decode_result(logits), logits
+
+    def prefill(self, prompt_ids, start=0, compute_logits=True):
+        """Every prompt token at slots start..start+n-1 with logits at the last
+        one, like ``decode_token`` position by position (generate.py:1110-1125)
+        but with each layer applied to all rows at once (matrix products and
+        causal attention); only float32 summation orders differ.  Returns
+        ``(next_token, logits)`` or ``(None, None)``."""
+        ids = [int(t) for t in prompt_ids]
+        if not ids:
+            raise ValueError("prefill needs at least one token")
+        if start < 0 or start + len(ids) > self.context_length:
+            raise ValueError("position outside the context")
+        hidden = round_f32(self._embedding[np.asarray(ids)])
+        for layer in range(self.layers):
+            hidden = self.stage.layer_rows(hidden, layer, start)
+        if not compute_logits:
+            return None, None
+        logits = self.stage.logits(hidden[-1])
         return decode_result(logits), logits
 
     def generate_greedy(self, prompt_ids, new_tokens, *, keep_logits=True, timings=None):

@@ -9,7 +9,8 @@ Both are faithful evaluations of the reference's arithmetic; their logits
 differ only because bf16 rounding points flip where the two sums straddle a
 rounding boundary, and the flips compound with depth.  The rel-L2 between them
 is the floor below which no implementation with a different summation order
-(such as the GPU's) can be held.  Output: order_sensitivity.json next to
+(such as the GPU's) can be held.  W8 models (int8 weights, float32 row scale)
+are measured the same way, with the exact sum taken before the scale.  Output: order_sensitivity.json next to
 this script.  Run time: a few minutes on 8 cores.
 """
 
@@ -33,15 +34,19 @@ class ExactSumStage(CPUDecoderStage):
 
     def project(self, name, activation):
         x = round_f32(activation).astype(np.float64)
+        if self.w8 and name != "lm_head":  # W8: exact sum of q * x, then the row scale
+            q = self.quantized(name)
+            acc = (np.asarray(q.weight, np.float64) @ x).astype(np.float32)
+            return round_f32(acc * np.asarray(q.scale, np.float32))
         return round_f32((from_bits(self.weight(name)).astype(np.float64) @ x).astype(np.float32))
 
 
-def floor_for(shape, layers, prompt_len, seed, label):
+def floor_for(shape, layers, prompt_len, seed, label, w8=False):
     model = SyntheticModel(shape, seed=0, layers=layers)
     rng = np.random.default_rng(seed)
     prompt = [int(t) for t in rng.integers(0, shape["vocab_size"], prompt_len)]
-    a = OracleDecoder(model, prompt_len + 1)
-    b = OracleDecoder(model, prompt_len + 1)
+    a = OracleDecoder(model, prompt_len + 1, w8=w8)
+    b = OracleDecoder(model, prompt_len + 1, w8=w8)
     b.stage.__class__ = ExactSumStage
     for pos, tok in enumerate(prompt):
         last = pos == prompt_len - 1
@@ -50,7 +55,7 @@ def floor_for(shape, layers, prompt_len, seed, label):
     err = float(np.linalg.norm(la - lb) / np.linalg.norm(lb))
     print(f"{label}: rel-L2 {err:.4e}, argmax {int(np.argmax(la))} vs {int(np.argmax(lb))}", flush=True)
     return {"label": label, "layers": model.metadata["layers"], "prompt_tokens": prompt_len,
-            "prompt_seed": seed, "rel_l2": err}
+            "prompt_seed": seed, "w8": w8, "rel_l2": err}
 
 
 def main():
@@ -59,6 +64,8 @@ def main():
         floor_for(QWEN25_05B, None, 40, 12, "qwen2.5-0.5b full depth, last prompt position"),
         floor_for(QWEN25_05B, 4, 40, 12, "qwen2.5-0.5b 4 layers, last prompt position"),
         floor_for(SMOLLM2_135M, 4, 35, 11, "smollm2-135m 4 layers, last prompt position"),
+        floor_for(QWEN25_05B, None, 40, 13, "qwen2.5-0.5b W8 full depth, last prompt position", w8=True),
+        floor_for(QWEN25_05B, 4, 40, 13, "qwen2.5-0.5b W8 4 layers, last prompt position", w8=True),
     ]
     (HERE / "order_sensitivity.json").write_text(json.dumps(rows, indent=2) + "\n")
 

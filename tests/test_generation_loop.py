@@ -262,3 +262,24 @@ def test_generate_text_and_generate():
     assert out[-1][1]["prompt_truncation"] == {"truncated_prompt": False}
     assert "".join(p for p, st in out) == "<6><7>"
     assert list(fake_decoder([5], ramp).generate("hello", 2))[-1][1]["generated_token_ids"] == [6, 7]
+
+
+@pytest.mark.parametrize("family,system", [
+    ("qwen2", "You are Qwen, created by Alibaba Cloud. You are a helpful assistant."),
+    ("llama", "You are a helpful AI assistant named SmolLM."),
+])
+def test_chat_template_system_turn_follows_model_family(tmp_path, monkeypatch, family, system):
+    """NPUDecoder gives its tokenizer the reference's default system turn for
+    the package's model family (npu_llm/runtime/generate.py:47-53): Qwen's for
+    qwen2 packages, SmolLM's otherwise.  The GPU engine is replaced by a stub."""
+    import runtime.generate as gen
+
+    write_chatml_tokenizer(tmp_path, 4096)
+    meta = {"model_family": family, "hidden_size": 64, "intermediate_size": 128, "attention_heads": 4,
+            "kv_heads": 2, "head_dim": 16, "layers": 1, "vocab_size": 4096}
+    monkeypatch.setattr(gen, "_load_model", lambda _: types.SimpleNamespace(metadata=meta))
+    monkeypatch.setattr(gen, "QwenDecoderEngine", lambda *a, **k: types.SimpleNamespace(close=lambda: None))
+    d = NPUDecoder(tmp_path)
+    ids = d.tokenizer.encode_chat([{"role": "user", "content": "hi"}])
+    text = d.tokenizer.decode(ids)
+    assert text.startswith(f"{IM_START}system\n{system}{IM_END}\n"), text[:120]

@@ -88,27 +88,39 @@ def test_gemv_bf16_matches_oracle(hk_lib, m, k, bias):
     _check_bf16(y, bf16.to_bits(ref), _bound(w64, x64, exact))
 
 
-@pytest.mark.parametrize("m,k", [(896, 896), (896, 4864), (9728, 896), (1152, 896), (576, 1536)])
-def test_gemv_w8_matches_oracle(hk_lib, m, k):
+# every Qwen2.5-0.5B projection shape with W8 weights (the QKV with its bias),
+# the LM head shape included, and one SmolLM2-135M shape
+W8_SHAPES = [(m, k, bias) for m, k, bias in QWEN_SHAPES] + [(576, 1536, False)]
+
+
+@pytest.mark.parametrize("m,k,bias", W8_SHAPES)
+def test_gemv_w8_matches_oracle(hk_lib, m, k, bias):
     from runtime import hip
 
-    announce(f"gemv_w8 M={m} K={k}")
+    announce(f"gemv_w8 M={m} K={k} bias={bias}")
     rng = np.random.default_rng(3 * m + k)
     w = bf16.round_f32(rng.normal(0, 0.02, (m, k)).astype(np.float32))
     q, s = quantize_per_output_channel(w)
     x_bits = bf16.to_bits(rng.normal(0, 1, k).astype(np.float32))
+    b = rng.normal(0, 0.02, m).astype(np.float32) if bias else None
     Q, S, X = _dev(q), _dev(s), _dev(x_bits)
+    B = _dev(b) if bias else None
     Yf = hip.DeviceBuffer(4 * m)
     Y = hip.DeviceBuffer(2 * m)
     hip.check(hk_lib.hk_gemv_w8(Q.ptr, S.ptr, X.ptr, None, None, None, Yf.ptr, m, k, None), "w8 f32")
-    hip.check(hk_lib.hk_gemv_w8(Q.ptr, S.ptr, X.ptr, None, None, Y.ptr, None, m, k, None), "w8 bf16")
+    hip.check(hk_lib.hk_gemv_w8(Q.ptr, S.ptr, X.ptr, B.ptr if B else None, None, Y.ptr, None, m, k, None),
+              "w8 bf16")
     hip.check(hk_lib.hk_stream_sync(None), "sync")
     x = bf16.from_bits(x_bits)
     q64 = q.astype(np.float64)
     exact = (q64 @ x.astype(np.float64)) * s
     bound = _bound(q64, x.astype(np.float64), exact) * s + 2e-7 * np.abs(exact)
     assert np.all(np.abs(_read(Yf, np.float32, m) - exact) <= bound)
-    _check_bf16(_read(Y, np.uint16, m), bf16.to_bits(project_w8(q, s, x)), bound)
+    ref = project_w8(q, s, x)
+    if bias:
+        ref = bf16.round_f32(ref + b)
+        bound = bound + _ulp(exact)  # the bias add rounds once more
+    _check_bf16(_read(Y, np.uint16, m), bf16.to_bits(ref), bound)
 
 
 def test_gemv_residual_epilogue(hk_lib):

@@ -313,3 +313,123 @@ def test_whole_step_check_catches_planted_mistakes(monkeypatch):
     for cls in (NoResidual, SwappedGateUp):
         lg = run(cls)
         assert np.linalg.norm(lg - ref) / np.linalg.norm(ref) > 0.1, cls.__name__
+
+
+# -- batched prefill (rows at once) -------------------------------------------
+
+def _per_position(model, tokens, context, *, w8=False):
+    dec = OracleDecoder(model, context, w8=w8)
+    lg = None
+    for pos, tok in enumerate(tokens):
+        _, lg = dec.decode_token(tok, pos, compute_logits=pos == len(tokens) - 1)
+    return dec, lg
+
+
+@pytest.mark.parametrize("w8", [False, True], ids=["bf16", "w8"])
+def test_prefill_rows_matches_per_position_decode(w8):
+    """The batched prefill equals the reference's position-by-position prefill
+    up to float32 summation order: KV caches agree to one bf16 step (nearly
+    all bit for bit), the last logits to rel-L2 1e-3, and both track the
+    float64 model."""
+    model = SyntheticModel(TINY, seed=3, std=0.15)
+    rng = np.random.default_rng(21)
+    tokens = [int(t) for t in rng.integers(0, TINY["vocab_size"], 13)]
+    ref, ref_logits = _per_position(model, tokens, 16, w8=w8)
+    dec = OracleDecoder(model, 16, w8=w8)
+    tok, logits = dec.prefill(tokens)
+    assert tok == int(np.argmax(logits))
+    assert np.linalg.norm(logits - ref_logits) / np.linalg.norm(ref_logits) < 1e-3
+    for layer in range(TINY["layers"]):
+        for got, want in ((dec.stage.key_cache[layer], ref.stage.key_cache[layer]),
+                          (dec.stage.value_cache[layer], ref.stage.value_cache[layer])):
+            from _util import bf16_ulp_diff
+            diff = bf16_ulp_diff(got, want)
+            assert diff.max() <= 1 and (diff == 0).mean() >= 0.97
+            assert np.all(got[:, len(tokens):] == 0)
+    if not w8:
+        f64 = _f64_model_logits(model, tokens, {len(tokens) - 1})[len(tokens) - 1]
+        assert np.linalg.norm(logits - f64) / np.linalg.norm(f64) < 2e-2
+
+
+def test_prefill_rows_blocks_and_offset_start():
+    """Rows scored in several blocks, a prompt starting at a nonzero slot, and
+    a continuation after an earlier prefill give the per-position result."""
+    model = SyntheticModel(TINY, seed=5, std=0.15)
+    rng = np.random.default_rng(22)
+    tokens = [int(t) for t in rng.integers(0, TINY["vocab_size"], 11)]
+    ref, ref_logits = _per_position(model, tokens, 12)
+    dec = OracleDecoder(model, 12)
+    block_rows = CPUDecoderStage.attention_rows.__defaults__
+    CPUDecoderStage.attention_rows.__defaults__ = (3,)
+    try:
+        dec.prefill(tokens[:4], 0, compute_logits=False)
+        _, logits = dec.prefill(tokens[4:], 4)
+    finally:
+        CPUDecoderStage.attention_rows.__defaults__ = block_rows
+    assert np.linalg.norm(logits - ref_logits) / np.linalg.norm(ref_logits) < 1e-3
+    from _util import bf16_ulp_diff
+    for layer in range(TINY["layers"]):
+        assert bf16_ulp_diff(dec.stage.key_cache[layer], ref.stage.key_cache[layer]).max() <= 1
+
+
+def test_prefill_rows_check_catches_a_non_causal_mask():
+    """A planted mistake in a copy of the oracle -- every row also attends to
+    the later prompt slots -- moves the last logits far from the float64
+    model, which the correct batched prefill tracks."""
+    model = SyntheticModel(TINY, seed=3, std=0.15)
+    tokens = [5, 17, 42, 8, 90, 1, 33, 60]
+    ref = _f64_model_logits(model, tokens, {7})[7]
+
+    class SeesTheFuture(CPUDecoderStage):
+        def attention_rows(self, qkv_rows, layer, start, block=256):
+            n = np.asarray(qkv_rows).shape[0]
+            saved = self._rope_inv_frequency
+            out = super().attention_rows(qkv_rows, layer, start, block)
+            # recompute each row over all n slots, keeping its own rotation
+            keys = bf16.from_bits(self.key_cache[layer][:, :start + n])
+            values = bf16.from_bits(self.value_cache[layer][:, :start + n])
+            d = self.head_dim
+            for i in range(n):
+                angle = np.float32(start + i) * saved
+                c, s_ = np.cos(angle), np.sin(angle)
+                q = np.asarray(qkv_rows[i, :self.q_heads * d], np.float32).reshape(self.q_heads, d)
+                q = bf16.round_f32(np.concatenate([q[:, :d // 2] * c - q[:, d // 2:] * s_,
+                                                   q[:, d // 2:] * c + q[:, :d // 2] * s_], axis=-1))
+                g = q.reshape(self.kv_heads, self.q_per_kv, d)
+                sc = np.einsum("kqd,ksd->kqs", g, keys) * d**-0.5
+                pr = np.exp(sc - sc.max(axis=-1, keepdims=True))
+                pr /= pr.sum(axis=-1, keepdims=True)
+                out[i] = bf16.round_f32(np.einsum("kqs,ksd->kqd", pr, values).reshape(-1))
+            return out
+
+    good = OracleDecoder(model, 8)
+    _, lg_good = good.prefill(tokens)
+    bad = OracleDecoder(model, 8)
+    bad.stage.__class__ = SeesTheFuture
+    _, lg_bad = bad.prefill(tokens)
+    assert np.linalg.norm(lg_good - ref) / np.linalg.norm(ref) < 2e-2
+    assert np.linalg.norm(lg_bad - ref) / np.linalg.norm(ref) > 5e-2
+
+
+def test_w8_stage_branch_is_project_w8():
+    """The W8 stage multiplies through oracle.quant.project_w8 (pinned against
+    float64 in test_oracle_quant.py), and the rows form agrees with it."""
+    from oracle.quant import project_w8
+
+    model = SyntheticModel(TINY, seed=6, std=0.15)
+    stage = CPUDecoderStage(model, 0, 8, w8=True)
+    rng = np.random.default_rng(23)
+    for name in ("layer00.qkv", "layer01.down_proj"):
+        q = model.quantized(name)
+        k = q.weight.shape[1]
+        x = bf16.round_f32(rng.normal(size=(3, k)).astype(np.float32))
+        for i in range(3):
+            np.testing.assert_array_equal(stage.project(name, x[i]), project_w8(q.weight, q.scale, x[i]))
+        from _util import bf16_ulp_diff
+        rows = stage.project_rows(name, x)
+        want = np.stack([project_w8(q.weight, q.scale, x[i]) for i in range(3)])
+        assert bf16_ulp_diff(bf16.to_bits(rows), bf16.to_bits(want)).max() <= 1
+    # the LM head stays bf16 in W8 mode
+    x = bf16.round_f32(rng.normal(size=TINY["hidden_size"]).astype(np.float32))
+    np.testing.assert_array_equal(stage.project("lm_head", x),
+                                  CPUDecoderStage(model, 0, 8).project("lm_head", x))
