@@ -1,75 +1,101 @@
-"""Token selection on the host: penalties, logit bias, temperature, top-k,
-top-p and a seeded multinomial draw.
+"""Token selection on the host: request parameters and the sampling pipeline.
 
-Mirrors the reference's ``npu_llm/runtime/sampling.py`` interface
-(``SamplingParams``, ``Sampler``, ``GREEDY``, ``SamplingError`` and the
-``apply_*`` / ``filter_*`` helpers): the same parameter names, ranges,
-validation errors and order of operations (sampling.py:1-19), so a request
-behaves the same on either decoder and a seeded request draws the same
-tokens for the same logits.  Pure NumPy; it never touches the GPU.
+Contract of ``npu_llm/runtime/sampling.py`` (callers: ``generate.py:1050-1200``,
+``api_server.py`` request parsing): ``SamplingParams`` (fields, defaults,
+``build`` / ``from_dict`` / ``from_request`` / ``to_dict``, ``greedy``,
+``greedy_for``, ``deterministic``), ``SamplingError`` with the same messages,
+``GREEDY``, the transforms ``apply_penalties``, ``apply_logit_bias``,
+``filter_top_k``, ``filter_top_p`` and ``Sampler`` (``select``, ``stats``,
+``seed``).  The selection order is the llama.cpp / vLLM one: penalties, logit
+bias, temperature, top-k, top-p, then a draw from the renormalised
+distribution with ``numpy.random.default_rng(seed).choice`` (so a seeded
+request repeats its tokens).  Temperature 0 (the default) is the argmax.
 
-Order for a non-greedy step: penalties over the prompt + generated history,
-then ``logit_bias``, then temperature, then top-k, then top-p, then one draw
-from ``numpy.random.default_rng(seed).choice`` over the renormalised
-distribution.  ``temperature == 0`` (the default) is greedy argmax.
+Design: every scalar parameter is described once in ``_FIELDS`` (default and
+validator) and ``SamplingParams`` normalises itself by walking that table; a
+``Sampler`` turns its parameters into the list of stages that actually change
+the scores, once, and ``select`` runs that list.
 """
 
-import dataclasses
 import math
 import secrets
+from dataclasses import asdict, dataclass, field
 
 import numpy as np
 
-__all__ = [
-    "SamplingError", "SamplingParams", "GREEDY", "Sampler", "apply_penalties", "apply_logit_bias",
-    "filter_top_k", "filter_top_p", "TEMPERATURE_RANGE", "TOP_P_RANGE", "REPETITION_PENALTY_RANGE",
-    "PENALTY_RANGE", "LOGIT_BIAS_RANGE", "SEED_RANGE", "MAX_LOGIT_BIAS_ENTRIES",
-]
+__all__ = ["TEMPERATURE_RANGE", "TOP_P_RANGE", "REPETITION_PENALTY_RANGE", "PENALTY_RANGE",
+           "LOGIT_BIAS_RANGE", "SEED_RANGE", "MAX_LOGIT_BIAS_ENTRIES", "SamplingError",
+           "SamplingParams", "GREEDY", "apply_penalties", "apply_logit_bias", "filter_top_k",
+           "filter_top_p", "Sampler"]
 
-# Accepted ranges (sampling.py:26-38).
 TEMPERATURE_RANGE = (0.0, 2.0)
-TOP_P_RANGE = (0.0, 1.0)            # low end exclusive
+TOP_P_RANGE = (0.0, 1.0)            # the low end is excluded
 REPETITION_PENALTY_RANGE = (0.1, 2.0)
 PENALTY_RANGE = (-2.0, 2.0)
 LOGIT_BIAS_RANGE = (-100.0, 100.0)
 SEED_RANGE = (0, 2**63 - 1)
-MAX_LOGIT_BIAS_ENTRIES = 1024
+MAX_LOGIT_BIAS_ENTRIES = 1024       # bounds the per-step bias work
 
 
 class SamplingError(ValueError):
-    """An invalid sampling parameter."""
+    """A sampling parameter outside its documented domain."""
 
 
-def _as_float(value, name):
-    # bool is an int subclass; a JSON true must not read as 1.0
-    if isinstance(value, bool) or not isinstance(value, (int, float)):
-        raise SamplingError(f"{name} must be a number")
-    try:
-        value = float(value)
-    except OverflowError:
-        raise SamplingError(f"{name} must be finite") from None
-    if not math.isfinite(value):
-        raise SamplingError(f"{name} must be finite")
-    return value
+# ---- validators: (name, raw value) -> normalised value ----
 
-
-def _in_range(value, name, bounds, low_open=False):
-    value = _as_float(value, name)
+def _real(bounds, open_low=False):
     low, high = bounds
-    if value > high or value < low or (low_open and value == low):
-        kind = "exclusive" if low_open else "inclusive"
-        raise SamplingError(f"{name} must be between {low} ({kind}) and {high} (inclusive)")
+    edge = "exclusive" if open_low else "inclusive"
+
+    def check(name, value):
+        if type(value) is bool or not isinstance(value, (int, float)):
+            raise SamplingError(f"{name} must be a number")
+        try:
+            x = float(value)
+        except OverflowError:
+            raise SamplingError(f"{name} must be finite") from None
+        if not math.isfinite(x):
+            raise SamplingError(f"{name} must be finite")
+        above_low = x > low if open_low else x >= low
+        if not above_low or x > high:
+            raise SamplingError(f"{name} must be between {low} ({edge}) and {high} (inclusive)")
+        return x
+
+    return check
+
+
+def _count(name, value):
+    if type(value) is bool or not isinstance(value, int):
+        raise SamplingError(f"{name} must be an integer")
+    if value < 0:
+        raise SamplingError(f"{name} cannot be negative")
     return value
 
 
-class _ReadOnlyBias(dict):
+def _seed(name, value):
+    if type(value) is bool or not isinstance(value, int):
+        raise SamplingError(f"{name} must be an integer")
+    if value not in range(SEED_RANGE[0], SEED_RANGE[1] + 1):
+        raise SamplingError(f"{name} must be between {SEED_RANGE[0]} and {SEED_RANGE[1]}")
+    return value
+
+
+# scalar fields in validation order: default (also what None means) and validator
+_FIELDS = (
+    ("temperature", 0.0, _real(TEMPERATURE_RANGE)),
+    ("top_p", 1.0, _real(TOP_P_RANGE, open_low=True)),
+    ("top_k", 0, _count),
+    ("repetition_penalty", 1.0, _real(REPETITION_PENALTY_RANGE)),
+    ("presence_penalty", 0.0, _real(PENALTY_RANGE)),
+    ("frequency_penalty", 0.0, _real(PENALTY_RANGE)),
+    ("seed", None, _seed),
+)
+_bias_value = _real(LOGIT_BIAS_RANGE)
+
+
+class _BiasMap(dict):
     """A validated ``{token_id: bias}`` map that cannot be changed afterwards
-    (still a dict, so ``asdict`` and ``json`` handle it)."""
-
-    def _refuse(self, *args, **kwargs):
-        raise TypeError("logit_bias is immutable")
-
-    __setitem__ = __delitem__ = clear = pop = popitem = setdefault = update = __ior__ = _refuse
+    (a plain ``dict`` underneath, so ``asdict`` and ``json`` handle it)."""
 
     def __copy__(self):
         return self
@@ -78,46 +104,51 @@ class _ReadOnlyBias(dict):
         return self
 
 
-def _token_key(key):
-    if isinstance(key, bool):
-        raise SamplingError("logit_bias keys must be token ids")
-    if isinstance(key, int):
-        token = key
-    elif isinstance(key, str):
+def _immutable(*args, **kwargs):
+    raise TypeError("logit_bias is immutable")
+
+
+for _mutator in ("__setitem__", "__delitem__", "__ior__", "clear", "pop", "popitem", "setdefault", "update"):
+    setattr(_BiasMap, _mutator, _immutable)
+
+
+def _bias_token(key):
+    """Token id of a ``logit_bias`` key: an int, or a decimal string as JSON
+    object keys always are."""
+    if isinstance(key, str):
         if not (key.isascii() and key.isdigit()):
             raise SamplingError(f"logit_bias key {key!r} is not a token id")
-        token = int(key, 10)
-    else:
+        key = int(key, 10)
+    elif type(key) is bool or not isinstance(key, int):
         raise SamplingError("logit_bias keys must be token ids")
-    if token < 0:
+    if key < 0:
         raise SamplingError("logit_bias token ids cannot be negative")
-    return token
+    return key
 
 
-def _validated_bias(value):
-    """OpenAI ``logit_bias``: string or integer keys; zero entries are dropped
-    (a later zero for the same id removes an earlier entry)."""
+def _bias_map(value):
+    """Normalised ``logit_bias``: int keys, zero biases left out (a later zero
+    for a token removes an earlier entry for it)."""
     if value is None:
-        return _ReadOnlyBias()
+        return _BiasMap()
     if not isinstance(value, dict):
         raise SamplingError("logit_bias must be an object")
     if len(value) > MAX_LOGIT_BIAS_ENTRIES:
         raise SamplingError(f"logit_bias accepts at most {MAX_LOGIT_BIAS_ENTRIES} entries")
-    out = {}
+    entries = {}
     for key, raw in value.items():
-        token = _token_key(key)
-        bias = _in_range(raw, f"logit_bias[{token}]", LOGIT_BIAS_RANGE)
-        if bias == 0.0:
-            out.pop(token, None)
-        else:
-            out[token] = bias
-    return _ReadOnlyBias(out)
+        token = _bias_token(key)
+        bias = _bias_value(f"logit_bias[{token}]", raw)
+        entries.pop(token, None)
+        if bias != 0.0:
+            entries[token] = bias
+    return _BiasMap(entries)
 
 
-@dataclasses.dataclass(frozen=True)
+@dataclass(frozen=True)
 class SamplingParams:
-    """One request's validated sampling settings (``None`` fields take the
-    defaults)."""
+    """One request's sampling parameters, validated on construction (also by
+    ``dataclasses.replace``)."""
 
     temperature: float = 0.0
     top_p: float = 1.0
@@ -125,190 +156,181 @@ class SamplingParams:
     repetition_penalty: float = 1.0
     presence_penalty: float = 0.0
     frequency_penalty: float = 0.0
-    logit_bias: dict = dataclasses.field(default_factory=_ReadOnlyBias)
+    logit_bias: dict = field(default_factory=_BiasMap)
     seed: int = None
 
     def __post_init__(self):
-        def put(name, value):
-            object.__setattr__(self, name, value)
+        for name, default, check in _FIELDS:
+            raw = getattr(self, name)
+            object.__setattr__(self, name, default if raw is None else check(name, raw))
+        object.__setattr__(self, "logit_bias", _bias_map(self.logit_bias))
 
-        put("temperature", 0.0 if self.temperature is None
-            else _in_range(self.temperature, "temperature", TEMPERATURE_RANGE))
-        put("top_p", 1.0 if self.top_p is None else _in_range(self.top_p, "top_p", TOP_P_RANGE, low_open=True))
-        top_k = 0 if self.top_k is None else self.top_k
-        if isinstance(top_k, bool) or not isinstance(top_k, int):
-            raise SamplingError("top_k must be an integer")
-        if top_k < 0:
-            raise SamplingError("top_k cannot be negative")
-        put("top_k", top_k)
-        put("repetition_penalty", 1.0 if self.repetition_penalty is None
-            else _in_range(self.repetition_penalty, "repetition_penalty", REPETITION_PENALTY_RANGE))
-        put("presence_penalty", 0.0 if self.presence_penalty is None
-            else _in_range(self.presence_penalty, "presence_penalty", PENALTY_RANGE))
-        put("frequency_penalty", 0.0 if self.frequency_penalty is None
-            else _in_range(self.frequency_penalty, "frequency_penalty", PENALTY_RANGE))
-        if self.seed is not None:
-            if isinstance(self.seed, bool) or not isinstance(self.seed, int):
-                raise SamplingError("seed must be an integer")
-            if not SEED_RANGE[0] <= self.seed <= SEED_RANGE[1]:
-                raise SamplingError(f"seed must be between {SEED_RANGE[0]} and {SEED_RANGE[1]}")
-        put("logit_bias", _validated_bias(self.logit_bias))
-
-    def _order_preserving(self):
-        # nothing ahead of top-k / top-p can reorder the logits
-        no_penalty = (self.repetition_penalty == 1.0 and self.presence_penalty == 0.0
-                      and self.frequency_penalty == 0.0)
-        return no_penalty and (self.temperature == 0.0 or self.top_k == 1)
+    @property
+    def _keeps_order(self):
+        """No penalty can move a score, and either no draw happens or top-1
+        leaves one candidate."""
+        penalties = (self.repetition_penalty, self.presence_penalty, self.frequency_penalty) != (1.0, 0.0, 0.0)
+        return not penalties and (self.temperature == 0.0 or self.top_k == 1)
 
     @property
     def greedy(self):
-        """The selection is the argmax whatever the logits."""
-        return self._order_preserving() and not self.logit_bias
+        """Selection is the argmax whatever the logits."""
+        return self._keeps_order and not self.logit_bias
 
     def greedy_for(self, vocab_size):
-        """``greedy``, ignoring bias entries for ids outside the vocabulary
-        (they are never applied)."""
-        return self._order_preserving() and not any(0 <= t < vocab_size for t in self.logit_bias)
+        """``greedy`` for a vocabulary of ``vocab_size``: bias entries outside
+        it are ignored by ``apply_logit_bias`` and so cannot matter."""
+        return self._keeps_order and all(not 0 <= token < vocab_size for token in self.logit_bias)
 
     @property
     def deterministic(self):
+        """Repeating the request repeats its tokens."""
         return self.greedy or self.temperature == 0.0 or self.seed is not None
 
     def to_dict(self):
-        return dataclasses.asdict(self)
+        return asdict(self)
 
     @classmethod
     def build(cls, temperature=None, top_p=None, top_k=None, repetition_penalty=None,
               presence_penalty=None, frequency_penalty=None, logit_bias=None, seed=None):
-        return cls(temperature=temperature, top_p=top_p, top_k=top_k,
-                   repetition_penalty=repetition_penalty, presence_penalty=presence_penalty,
-                   frequency_penalty=frequency_penalty, logit_bias=logit_bias, seed=seed)
+        """From raw request values; None means the default."""
+        return cls(temperature, top_p, top_k, repetition_penalty, presence_penalty, frequency_penalty,
+                   logit_bias, seed)
 
     @classmethod
     def from_dict(cls, values):
-        """Rebuild (and re-validate) from a transport dict."""
+        """From a transport dict (re-validated: it crossed a process boundary)."""
         if values is None:
             return cls()
         if not isinstance(values, dict):
             raise SamplingError("sampling parameters must be an object")
-        unknown = sorted(set(values) - {f.name for f in dataclasses.fields(cls)})
-        if unknown:
-            raise SamplingError("unsupported sampling parameters: " + ", ".join(unknown))
+        extra = sorted(set(values).difference(cls.__dataclass_fields__))
+        if extra:
+            raise SamplingError("unsupported sampling parameters: " + ", ".join(extra))
         return cls.build(**values)
 
     @classmethod
     def from_request(cls, request):
-        """From an OpenAI-style request body."""
-        names = ("temperature", "top_p", "top_k", "repetition_penalty", "presence_penalty",
-                 "frequency_penalty", "logit_bias", "seed")
-        return cls.build(**{n: request.get(n) for n in names})
+        """From an OpenAI chat-completion request body."""
+        return cls.build(**{name: request.get(name) for name in cls.__dataclass_fields__})
 
 
 GREEDY = SamplingParams()
 
 
+# ---- transforms (each changes `logits` in place and returns it) ----
+
 def apply_penalties(logits, history, params):
-    """Repetition (CTRL: positive scores divided, negative multiplied),
-    frequency (count-scaled) and presence penalties over the tokens seen so
-    far; ids outside the vocabulary are ignored.  Returns ``logits``."""
-    if len(history) == 0 or (params.repetition_penalty == 1.0 and params.presence_penalty == 0.0
-                             and params.frequency_penalty == 0.0):
+    """CTRL repetition penalty (positive scores divided by it, negative ones
+    multiplied), then the OpenAI frequency (per occurrence) and presence
+    (once) penalties, on tokens of ``history`` inside the vocabulary."""
+    rp, fp, pp = params.repetition_penalty, params.frequency_penalty, params.presence_penalty
+    if len(history) == 0 or (rp, fp, pp) == (1.0, 0.0, 0.0):
         return logits
-    ids, counts = np.unique(np.asarray(history, dtype=np.int64), return_counts=True)
-    keep = (ids >= 0) & (ids < logits.shape[0])
-    ids, counts = ids[keep], counts[keep].astype(np.float32)
+    ids = np.asarray(history, dtype=np.int64)
+    ids = ids[(ids >= 0) & (ids < logits.shape[0])]  # out-of-range ids must not wrap
     if ids.size == 0:
         return logits
-    seen = logits[ids]
-    if params.repetition_penalty != 1.0:
-        seen = np.where(seen > 0, seen / params.repetition_penalty, seen * params.repetition_penalty)
-    seen = seen - params.frequency_penalty * counts
-    seen = seen - params.presence_penalty
-    logits[ids] = seen
+    occurrences = np.bincount(ids, minlength=logits.shape[0])
+    seen = np.flatnonzero(occurrences)
+    score = logits[seen]
+    if rp != 1.0:
+        score = np.where(score > 0, score / rp, score * rp)
+    score = score - fp * occurrences[seen].astype(np.float32)
+    logits[seen] = score - pp
     return logits
 
 
 def apply_logit_bias(logits, logit_bias):
-    """Add each bias to its token's logit; ids outside the vocabulary are
-    skipped.  Returns ``logits``."""
-    vocab = logits.shape[0]
-    for token, bias in (logit_bias or {}).items():
-        token = int(token)
-        if 0 <= token < vocab:
-            logits[token] += bias
+    """Add each bias to its token's score (OpenAI semantics: -100 bans, +100
+    forces); ids outside the vocabulary are skipped."""
+    if logit_bias:
+        ids = np.fromiter(logit_bias.keys(), dtype=np.int64, count=len(logit_bias))
+        bias = np.fromiter(logit_bias.values(), dtype=np.float64, count=len(logit_bias))
+        inside = (ids >= 0) & (ids < logits.shape[0])
+        logits[ids[inside]] += bias[inside].astype(logits.dtype)
     return logits
 
 
 def filter_top_k(logits, top_k):
-    """Set every score below the k-th highest to -inf (ties at the threshold
-    stay).  ``top_k`` 0 or >= the vocabulary is a no-op."""
-    if 0 < top_k < logits.shape[0]:
-        kth = np.partition(logits, logits.shape[0] - top_k)[logits.shape[0] - top_k]
-        logits[logits < kth] = -np.inf
+    """Only scores at or above the k-th largest survive (ties at the
+    threshold all survive); others become -inf."""
+    n = logits.shape[0]
+    if 0 < top_k < n:
+        kth_largest = np.partition(logits, n - top_k)[n - top_k]
+        logits[logits < kth_largest] = -np.inf
     return logits
 
 
 def filter_top_p(logits, top_p):
-    """Keep the smallest set of highest-probability tokens whose mass reaches
-    ``top_p`` (the token that crosses it included; the best token always
-    stays)."""
-    if top_p >= 1.0:
-        return logits
-    order = np.argsort(logits)[::-1]
-    mass = _softmax(logits[order])
-    before = np.cumsum(mass) - mass  # probability mass strictly ahead of each token
-    drop = before >= top_p
-    drop[0] = False
-    logits[order[drop]] = -np.inf
+    """Nucleus: in descending order of probability a token survives while the
+    mass of the tokens before it is below ``top_p``, so the token that crosses
+    the threshold stays, and so does the best one always."""
+    if top_p < 1.0:
+        order = np.argsort(-logits, kind="stable")
+        p = _softmax(logits[order])
+        mass_before = np.concatenate(([0.0], np.cumsum(p)[:-1]))
+        dropped = order[1:][mass_before[1:] >= top_p]
+        logits[dropped] = -np.inf
     return logits
 
 
 def _softmax(scores):
-    """Softmax over the finite scores (-inf entries get zero); if everything
-    underflows, all the mass goes to the best score."""
+    """Probabilities of the finite scores (zero elsewhere); one-hot on the
+    best score when everything underflows."""
     finite = np.isfinite(scores)
-    peak = scores[finite].max() if finite.any() else 0.0
-    weights = np.zeros_like(scores)
-    np.exp(scores - peak, where=finite, out=weights)
-    total = weights.sum()
-    if not (math.isfinite(float(total)) and total > 0):
-        weights = np.zeros_like(scores)
-        weights[int(np.argmax(scores))] = 1.0
-        return weights
-    return weights / total
+    top = scores[finite].max() if finite.any() else 0.0
+    e = np.exp(scores - top, where=finite, out=np.zeros_like(scores))
+    total = e.sum()
+    if total > 0 and np.isfinite(total):
+        return e / total
+    onehot = np.zeros_like(scores)
+    onehot[int(np.argmax(scores))] = 1.0
+    return onehot
 
 
 class Sampler:
-    """Selects the tokens of one completion; owns the request's random stream
-    (an unseeded sampled request draws a seed and reports it)."""
+    """Token selection for one completion; owns its random stream.  An
+    unseeded, non-greedy request draws a seed and reports it in ``stats``."""
 
     def __init__(self, params=GREEDY, vocab_size=None):
         self.params = params
         self.vocab_size = vocab_size
         self.seed = params.seed
-        if self.seed is None and not self.greedy:
+        if self.greedy:
+            self._rng = None
+            self._stages = ()
+            return
+        if self.seed is None:
             self.seed = secrets.randbelow(SEED_RANGE[1] + 1)
-        self._rng = None if self.greedy else np.random.default_rng(self.seed)
+        self._rng = np.random.default_rng(self.seed)
+        stages = []
+        if (params.repetition_penalty, params.presence_penalty, params.frequency_penalty) != (1.0, 0.0, 0.0):
+            stages.append(lambda s, history: apply_penalties(s, history, params))
+        if params.logit_bias:
+            stages.append(lambda s, history: apply_logit_bias(s, params.logit_bias))
+        self._stages = tuple(stages)
 
     @property
     def greedy(self):
-        if self.vocab_size is None:
-            return self.params.greedy
-        return self.params.greedy_for(self.vocab_size)
+        return self.params.greedy if self.vocab_size is None else self.params.greedy_for(self.vocab_size)
 
     def select(self, logits, history=()):
-        """The next token id for ``logits`` after ``history``."""
+        """The next token id for ``logits`` after the tokens in ``history``."""
         scores = np.asarray(logits, dtype=np.float32)
-        if self.greedy:
+        if self._rng is None:
             return int(np.argmax(scores))
+        scores = scores.copy()
+        for stage in self._stages:
+            scores = stage(scores, history)
         p = self.params
-        scores = apply_logit_bias(apply_penalties(scores.copy(), history, p), p.logit_bias)
         if p.temperature == 0.0:
             return int(np.argmax(scores))
         scores = filter_top_p(filter_top_k(scores / p.temperature, p.top_k), p.top_p)
         probs = _softmax(scores).astype(np.float64)
-        probs /= probs.sum()  # choice() wants the float64 sum within its tolerance
+        probs /= probs.sum()  # Generator.choice wants a sum of 1 within its tolerance
         return int(self._rng.choice(probs.shape[0], p=probs))
 
     def stats(self):
+        """Parameters, mode and seed, for the generation statistics."""
         return {**self.params.to_dict(), "mode": "greedy" if self.greedy else "sampled", "seed": self.seed}

@@ -1,14 +1,29 @@
-"""ChatML tokenizer wrapper, UTF-8-safe streaming, and a synthetic ChatML
-tokenizer for random-init packages.
+"""ChatML tokenizer, UTF-8-safe streaming, and a synthetic ChatML tokenizer
+for random-init packages.
 
-Mirrors the reference's ``npu_llm/runtime/tokenizer.py`` interface
-(``SmolLMTokenizer``, ``StreamDetokenizer``, ``DEFAULT_SYSTEM``, ``IM_START``,
-``IM_END``): the chat template, the control tokens inserted by id (message
-text is encoded with special-token parsing off, so a literal "<|im_end|>" in a
-message cannot close a turn), the context-window truncation order of
-``encode_chat_window`` (tokenizer.py:118-209) and the byte-exact
-``token_bytes`` of byte-level BPE pieces.  Built on the ``tokenizers``
-library, like the reference.
+Contract of ``npu_llm/runtime/tokenizer.py`` as its callers use it
+(``generate.py``, ``api_server.py``, ``chat.py``): ``SmolLMTokenizer(model_dir,
+default_system=...)`` with ``eos_token`` / ``eos_id``, ``format_chat``,
+``encode_chat``, ``encode_prompt_window``, ``encode_chat_window`` (the
+truncation order and report keys of tokenizer.py:119-196), ``decode`` and the
+byte-exact ``token_bytes``; ``StreamDetokenizer`` (``push``, ``flush``,
+``text``); ``DEFAULT_SYSTEM``, ``IM_START``, ``IM_END``.  Message text is
+encoded with special-token parsing off and the control tokens are inserted by
+id, so a literal "<|im_end|>" inside a message cannot close its turn.
+
+Design:
+- a turn is ``<|im_start|>`` + ids of "role\ncontent" + ``<|im_end|>`` + ids
+  of "\n"; the control tokens split the text, so turns encode independently
+  and a prompt is the concatenation of its turns' ids plus the generation
+  prompt;
+- ``encode_chat_window`` walks an ordered list of candidate prompts, from the
+  whole conversation to the last-resort token cut, and returns the first that
+  fits the budget (candidates are built lazily, so only the ones tried cost
+  an encode);
+- the streaming detokenizer feeds each token's bytes into an incremental
+  UTF-8 decoder, which holds an incomplete character until its last byte
+  arrives, so each token costs O(1) instead of a decode of the whole
+  sequence.
 
 ``write_chatml_tokenizer`` writes a byte-level BPE ``tokenizer.json`` (plus
 ``tokenizer_config.json``) of any vocabulary size, with <|endoftext|>,
@@ -18,6 +33,7 @@ generation stack and the OpenAI-style callers run on synthetic packages
 ids decode to fixed 2-3 byte strings.
 """
 
+import codecs
 import json
 from pathlib import Path
 
@@ -30,7 +46,7 @@ DEFAULT_SYSTEM = "You are a helpful AI assistant named SmolLM, trained by Huggin
 IM_START = "<|im_start|>"
 IM_END = "<|im_end|>"
 END_OF_TEXT = "<|endoftext|>"
-REPLACEMENT_CHARACTER = "�"
+REPLACEMENT_CHARACTER = "\ufffd"
 
 
 def _byte_alphabet():
@@ -52,157 +68,159 @@ _BYTE_TO_CHAR = _byte_alphabet()
 _CHAR_TO_BYTE = {c: b for b, c in _BYTE_TO_CHAR.items()}
 
 
+def _largest_fitting(limit, fits):
+    """Largest n in 0..limit with fits(n) for a predicate that holds up to
+    some n and not beyond (token counts grow with kept text); None when not
+    even fits(0).  Bisection over [known fit, known miss)."""
+    if not fits(0):
+        return None
+    if fits(limit):
+        return limit
+    good, bad = 0, limit
+    while bad - good > 1:
+        mid = (good + bad) // 2
+        if fits(mid):
+            good = mid
+        else:
+            bad = mid
+    return good
+
+
+def _word_prefix(text, n):
+    """The first n characters of text, ended at a word boundary when the cut
+    falls inside the text and one exists, without trailing spaces."""
+    kept = text[:n]
+    if 0 < n < len(text):
+        space = kept.rstrip().rfind(" ")
+        if space > 0:
+            kept = kept[:space]
+    return kept.rstrip()
+
+
 class SmolLMTokenizer:
     """ChatML tokenizer over a package's ``tokenizer.json`` and
     ``tokenizer_config.json``."""
 
     def __init__(self, model_dir, default_system=DEFAULT_SYSTEM):
-        path = str(Path(model_dir) / "tokenizer.json")
-        self._tokenizer = Tokenizer.from_file(path)
-        self._content_tokenizer = Tokenizer.from_file(path)
-        self._content_tokenizer.encode_special_tokens = True
-        config = json.loads((Path(model_dir) / "tokenizer_config.json").read_text())
+        folder = Path(model_dir)
+        self._tokenizer = Tokenizer.from_file(str(folder / "tokenizer.json"))
+        # message text is untrusted: a second instance encodes it with
+        # special-token parsing off
+        self._plain = Tokenizer.from_file(str(folder / "tokenizer.json"))
+        self._plain.encode_special_tokens = True
+        config = json.loads((folder / "tokenizer_config.json").read_text())
         self.eos_token = config.get("eos_token", IM_END)
         self.eos_id = self._tokenizer.token_to_id(self.eos_token)
         self.default_system = default_system
         self._im_start_id = self._tokenizer.token_to_id(IM_START)
         self._im_end_id = self._tokenizer.token_to_id(IM_END)
-        if self._im_start_id is None or self._im_end_id is None:
+        if None in (self._im_start_id, self._im_end_id):
             raise ValueError(f"tokenizer does not define the ChatML control tokens {IM_START} and {IM_END}")
-        self._newline_ids = self._text_ids("\n")
+        self._turn_end = [self._im_end_id, *self._text_ids("\n")]
+        self._reply_start = [self._im_start_id, *self._text_ids("assistant\n")]
 
     # -- encoding ------------------------------------------------------------
     def _text_ids(self, text):
-        return self._content_tokenizer.encode(text, add_special_tokens=False).ids
+        return self._plain.encode(text, add_special_tokens=False).ids
 
-    def _with_system(self, messages):
-        if messages and messages[0]["role"] == "system":
-            return list(messages)
-        return [{"role": "system", "content": self.default_system}, *messages]
+    def _conversation(self, messages):
+        """The messages with the default system turn in front when they bring none."""
+        messages = list(messages)
+        if not messages or messages[0]["role"] != "system":
+            messages.insert(0, {"role": "system", "content": self.default_system})
+        return messages
 
     def format_chat(self, messages, add_generation_prompt=True):
-        text = "".join(f"{IM_START}{m['role']}\n{m['content']}{IM_END}\n" for m in self._with_system(messages))
-        return text + (f"{IM_START}assistant\n" if add_generation_prompt else "")
+        turns = (f"{IM_START}{m['role']}\n{m['content']}{IM_END}\n" for m in self._conversation(messages))
+        return "".join(turns) + (f"{IM_START}assistant\n" if add_generation_prompt else "")
 
-    def _turn_ids(self, role, content):
-        # one turn encoded alone gives the same ids as the rendered template:
-        # the control tokens split the text and nothing merges across them
-        return [self._im_start_id, *self._text_ids(f"{role}\n{content}"), self._im_end_id, *self._newline_ids]
+    def _turn(self, message):
+        return [self._im_start_id, *self._text_ids(f"{message['role']}\n{message['content']}"), *self._turn_end]
 
-    def _prompt_tail(self):
-        return [self._im_start_id, *self._text_ids("assistant\n")]
+    def _prompt(self, turn_ids):
+        """Concatenated turns plus the generation prompt."""
+        out = [t for ids in turn_ids for t in ids]
+        out += self._reply_start
+        return out
 
     def _turns_ids(self, messages):
-        out = []
-        for m in messages:
-            out += self._turn_ids(m["role"], m["content"])
-        return out + self._prompt_tail()
+        return self._prompt([self._turn(m) for m in messages])
 
     def encode_chat(self, messages):
-        return self._turns_ids(self._with_system(messages))
+        return self._turns_ids(self._conversation(messages))
 
     def encode_prompt_window(self, prompt, budget):
-        """A raw prompt in at most ``budget`` tokens (the newest ones).
-        Returns ``(ids, truncated)``."""
+        """A raw prompt (no chat turns) in at most ``budget`` tokens, its
+        newest ones when it is longer.  Returns ``(ids, truncated)``."""
         if budget <= 0:
             raise ValueError("prompt budget must be positive")
         ids = self._text_ids(prompt)
-        return (ids, False) if len(ids) <= budget else (ids[len(ids) - budget:], True)
+        truncated = len(ids) > budget
+        return (ids[-budget:] if truncated else ids), truncated
 
     def encode_chat_window(self, messages, budget):
-        """A conversation in at most ``budget`` prompt tokens, shortened at turn
-        boundaries so the newest message stays whole as long as possible:
-        (1) drop the oldest turns after the system prompt; (2) cut the system
-        prompt back to a whole-word prefix, or drop it; (3) keep only the
-        newest characters of the newest message; (4) as a last resort keep the
-        newest ``budget`` tokens.  Returns ``(ids, truncation)``."""
+        """A conversation in at most ``budget`` prompt tokens.  The newest
+        message stays whole as long as possible; the prompt is shortened at
+        turn boundaries, in this order: drop the oldest turns after the
+        system prompt; cut the system prompt back to a whole-word prefix, or
+        drop it; keep only the newest characters of the newest message; as a
+        last resort keep the newest ``budget`` tokens.  Returns ``(ids,
+        truncation)`` with the reference's report keys."""
         if budget <= 0:
             raise ValueError("prompt budget must be positive")
-        messages = self._with_system(messages)
         report = {"dropped_messages": 0, "truncated_system": False, "dropped_system": False,
                   "truncated_content": False, "token_fallback": False}
-        per_turn = [self._turn_ids(m["role"], m["content"]) for m in messages]
-        tail = self._prompt_tail()
-        everything = [t for ids in per_turn for t in ids] + tail
-        if len(everything) <= budget:
-            return everything, report
+        for ids, changes in self._window_plans(self._conversation(messages), budget):
+            if ids is not None and len(ids) <= budget:
+                for key, value in changes.items():
+                    report[key] = value
+                return ids, report
+        raise AssertionError("the token cut always fits")  # unreachable
 
-        system, turns = messages[0], messages[1:]
-        system_ids, turn_ids = per_turn[0], per_turn[1:]
-        if not turns:  # the system message is the only, hence newest, message
-            system, turns, system_ids, turn_ids = None, [system], [], [system_ids]
-        # (1) oldest turns first, the newest always kept
-        total = len(everything)
-        first = 0
-        while len(turns) - first > 1:
-            total -= len(turn_ids[first])
-            first += 1
-            report["dropped_messages"] += 1
-            if total <= budget:
-                ids = list(system_ids)
-                for t in turn_ids[first:]:
-                    ids += t
-                return ids + tail, report
-        newest = turns[-1]
-        # (2) a shorter system prompt, else none
+    def _window_plans(self, messages, budget):
+        """Candidate prompts in order of preference, each with the report
+        entries it implies; None for a plan that has no fitting form."""
+        turn_ids = [self._turn(m) for m in messages]
+        everything = self._prompt(turn_ids)
+        yield everything, {}
+        if len(messages) > 1:
+            system, system_ids, rest, rest_ids = messages[0], turn_ids[0], messages[1:], turn_ids[1:]
+        else:  # a lone system message is the newest message
+            system, system_ids, rest, rest_ids = None, [], messages, turn_ids
+        for dropped in range(1, len(rest)):
+            yield self._prompt([system_ids] + rest_ids[dropped:]), {"dropped_messages": dropped}
+        newest = rest[-1]
+        dropped = len(rest) - 1
         if system is not None:
-            ids = self._system_prefix_fit(system, newest, budget)
-            if ids is not None:
-                report["truncated_system"] = True
-                return ids, report
-            report["dropped_system"] = True
-            report["dropped_messages"] += 1
-            ids = self._turns_ids([newest])
-            if len(ids) <= budget:
-                return ids, report
-        # (3) the newest characters of the newest message
-        ids = self._newest_suffix_fit(newest, budget)
-        if ids is not None:
-            report["truncated_content"] = True
-            return ids, report
-        report["token_fallback"] = True
-        return everything[len(everything) - budget:], report
-
-    @staticmethod
-    def _largest(n, ok):
-        """Largest k in 0..n with ok(k), or None if not even ok(0).  Token
-        counts grow only roughly with text length (BPE merges), so the binary
-        search result is checked and walked down if needed."""
-        if not ok(0):
-            return None
-        lo, hi = 0, n
-        while lo < hi:
-            mid = (lo + hi + 1) // 2
-            if ok(mid):
-                lo = mid
-            else:
-                hi = mid - 1
-        while lo > 0 and not ok(lo):
-            lo -= 1
-        return lo
+            yield self._system_prefix_fit(system, newest, budget), {"dropped_messages": dropped,
+                                                                    "truncated_system": True}
+            dropped += 1
+            yield self._turns_ids([newest]), {"dropped_messages": dropped, "dropped_system": True}
+        system_gone = {"dropped_system": True} if system is not None else {}
+        yield self._newest_suffix_fit(newest, budget), {"dropped_messages": dropped, **system_gone,
+                                                        "truncated_content": True}
+        yield everything[-budget:], {"dropped_messages": dropped, **system_gone, "token_fallback": True}
 
     def _system_prefix_fit(self, system, newest, budget):
-        text = system["content"]
+        """The longest whole-word beginning (at least one character kept) of
+        the system prompt that fits together with the newest turn."""
+        text, newest_ids = system["content"], self._turn(newest)
 
-        def ids_for(k):
-            kept = text[:k]
-            if 0 < k < len(text):
-                cut = kept.rstrip().rfind(" ")  # end on a word boundary when there is one
-                if cut > 0:
-                    kept = kept[:cut]
-            return self._turns_ids([{"role": system["role"], "content": kept.rstrip()}, newest])
+        def prompt(n):
+            return self._prompt([self._turn({"role": system["role"], "content": _word_prefix(text, n)}), newest_ids])
 
-        k = self._largest(len(text), lambda k: len(ids_for(k)) <= budget)
-        return ids_for(k) if k else None
+        n = _largest_fitting(len(text), lambda n: len(prompt(n)) <= budget)
+        return prompt(n) if n else None
 
     def _newest_suffix_fit(self, turn, budget):
+        """The newest turn with the longest tail of its text that fits."""
         text = turn["content"]
 
-        def ids_for(k):
-            return self._turns_ids([{"role": turn["role"], "content": text[len(text) - k:] if k else ""}])
+        def prompt(n):
+            return self._turns_ids([{"role": turn["role"], "content": text[len(text) - n:]}])
 
-        k = self._largest(len(text), lambda k: len(ids_for(k)) <= budget)
-        return None if k is None else ids_for(k)
+        n = _largest_fitting(len(text), lambda n: len(prompt(n)) <= budget)
+        return None if n is None else prompt(n)
 
     # -- decoding ------------------------------------------------------------
     def decode(self, token_ids, skip_special_tokens=False):
@@ -213,37 +231,40 @@ class SmolLMTokenizer:
         hold part of a multi-byte UTF-8 character, which ``decode`` alone would
         render as U+FFFD)."""
         piece = self._tokenizer.id_to_token(int(token_id))
-        if piece is not None and all(ch in _CHAR_TO_BYTE for ch in piece):
-            return bytes(_CHAR_TO_BYTE[ch] for ch in piece)
+        if piece is not None:
+            raw = [_CHAR_TO_BYTE.get(ch) for ch in piece]
+            if None not in raw:
+                return bytes(raw)
         return self.decode([int(token_id)]).encode("utf-8")
 
 
 class StreamDetokenizer:
-    """Text of a growing token sequence, released only in whole characters: a
-    trailing partial UTF-8 character (decoded as U+FFFD) is held until a later
-    token completes it or ``flush``."""
+    """Text of a growing token sequence, released in whole characters only:
+    each token's bytes (``tokenizer.token_bytes``) go through an incremental
+    UTF-8 decoder, which keeps an incomplete trailing character until a later
+    token completes it or ``flush`` renders it as U+FFFD."""
 
     def __init__(self, tokenizer):
         self._tokenizer = tokenizer
-        self._ids = []
-        self._text = ""
-        self._sent = 0
+        self._utf8 = codecs.getincrementaldecoder("utf-8")(errors="replace")
+        self._released = []
 
     @property
     def text(self):
-        return self._text
+        """Everything decoded so far, a held partial character as U+FFFD."""
+        pending, _ = self._utf8.getstate()
+        return "".join(self._released) + pending.decode("utf-8", errors="replace")
 
     def push(self, token_id):
-        self._ids.append(int(token_id))
-        self._text = self._tokenizer.decode(self._ids)
-        return "" if self._text.endswith(REPLACEMENT_CHARACTER) else self._release()
+        """Add a token; return the text it completes (possibly empty)."""
+        out = self._utf8.decode(self._tokenizer.token_bytes(int(token_id)))
+        self._released.append(out)
+        return out
 
     def flush(self):
-        return self._release()
-
-    def _release(self):
-        out = self._text[self._sent:]
-        self._sent = len(self._text)
+        """Release whatever is held, an incomplete character as U+FFFD."""
+        out = self._utf8.decode(b"", final=True)
+        self._released.append(out)
         return out
 
 

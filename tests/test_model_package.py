@@ -76,3 +76,81 @@ def test_truncated_file_is_rejected(package):
     f.write_bytes(f.read_bytes()[:-2])
     with pytest.raises(RuntimeError, match="missing or truncated"):
         XDNA1Model(path)
+
+
+def _bare_package(root, metadata):
+    """A package directory with `metadata` and its digest (the style of the
+    reference's tests/test_model_integrity.py)."""
+    from runtime.model import _canonical_digest
+
+    body = dict(metadata)
+    body["metadata_sha256"] = _canonical_digest(body)
+    (root / "metadata.json").write_text(json.dumps(body))
+    return body
+
+
+def test_integrity_manifest_rules(tmp_path):
+    import hashlib
+
+    from runtime.model import XDNA1Model
+
+    data = b"verified model bytes"
+    (tmp_path / "weights.bin").write_bytes(data)
+    good = {"size": len(data), "sha256": hashlib.sha256(data).hexdigest()}
+    _bare_package(tmp_path, {"tensors": {}, "files": {"weights.bin": good}})
+    XDNA1Model(tmp_path)  # a package without tensors but with a verified file loads
+    cases = [
+        ({"tensors": {}}, "no integrity manifest"),
+        ({"tensors": {}, "files": {}}, "no integrity manifest"),
+        ({"tensors": {}, "files": {"weights.bin": {"size": True, "sha256": good["sha256"]}}},
+         "invalid integrity entry"),
+        ({"tensors": {}, "files": {"weights.bin": {"size": len(data), "sha256": "ab"}}},
+         "invalid integrity entry"),
+        ({"tensors": {}, "files": {"weights.bin": {**good, "size": len(data) + 1}}}, "missing or truncated"),
+        ({"tensors": {}, "files": {str(tmp_path / "weights.bin"): good}}, "absolute model path"),
+        ({"tensors": {"w": {"file": "other.bin", "shape": [2], "dtype": "float32"}},
+          "files": {"weights.bin": good}}, "missing from integrity manifest: other.bin"),
+        ({"tensors": {"w": [1]}, "files": {"weights.bin": good}}, "invalid tensor specification: w"),
+        ({"files": {"weights.bin": good}}, "no tensor manifest"),
+    ]
+    for metadata, message in cases:
+        _bare_package(tmp_path, metadata)
+        with pytest.raises(RuntimeError, match=message):
+            XDNA1Model(tmp_path)
+    (tmp_path / "metadata.json").write_text("[1, 2]")
+    with pytest.raises(RuntimeError, match="must be a JSON object"):
+        XDNA1Model(tmp_path)
+    (tmp_path / "metadata.json").write_text("{not json")
+    with pytest.raises(RuntimeError, match="invalid metadata.json"):
+        XDNA1Model(tmp_path)
+    body = _bare_package(tmp_path, {"tensors": {}, "files": {"weights.bin": good}})
+    body.pop("metadata_sha256")
+    (tmp_path / "metadata.json").write_text(json.dumps(body))
+    with pytest.raises(RuntimeError, match="no metadata_sha256"):
+        XDNA1Model(tmp_path)
+
+
+def test_tensor_shape_and_size_checks(tmp_path):
+    import hashlib
+
+    from runtime.model import XDNA1Model
+
+    data = np.arange(6, dtype=np.float32).tobytes()
+    (tmp_path / "t.bin").write_bytes(data)
+    entry = {"t.bin": {"size": len(data), "sha256": hashlib.sha256(data).hexdigest()}}
+    for shape, message in (([2, 3], None), ([3, 3], "size mismatch"), ([0, 6], "non-positive"),
+                           ([2.0, 3], "non-integer"), ([], "invalid shape"), ([1 << 16, 1 << 16], "too large")):
+        _bare_package(tmp_path, {"tensors": {"t": {"file": "t.bin", "shape": shape, "dtype": "float32"}},
+                                 "files": entry})
+        model = XDNA1Model(tmp_path)
+        if message is None:
+            np.testing.assert_array_equal(model.raw("t"), np.arange(6, dtype=np.float32).reshape(2, 3))
+        else:
+            with pytest.raises(RuntimeError, match=message):
+                model.raw("t")
+    _bare_package(tmp_path, {"tensors": {"t": {"file": "t.bin", "shape": [6], "dtype": "nonsense"}},
+                             "files": entry})
+    with pytest.raises(RuntimeError, match="invalid dtype"):
+        XDNA1Model(tmp_path).raw("t")
+    with pytest.raises(RuntimeError, match="no BF16 weights"):
+        XDNA1Model(tmp_path).bf16_projection("t")

@@ -166,3 +166,29 @@ def test_log_softmax_closed_form():
     assert np.isneginf(lp[2])
     with pytest.raises(ValueError):
         log_softmax([-np.inf, -np.inf])
+
+
+def test_stop_matcher_properties_on_random_streams():
+    """Over random texts split into random pieces: the emitted text never
+    contains a stop; with a match, the matched stop starts exactly where the
+    emitted text ends; without one, everything is emitted.  Same-start ties
+    go to the earlier-listed stop."""
+    rng = np.random.default_rng(77)
+    alphabet = "abc"
+    for _ in range(2000):
+        stops = tuple(dict.fromkeys("".join(rng.choice(list(alphabet), rng.integers(1, 4)))
+                                    for _ in range(rng.integers(1, 4))))
+        text = "".join(rng.choice(list(alphabet), rng.integers(0, 14)))
+        cuts = sorted(rng.choice(len(text) + 1, rng.integers(0, 4)).tolist()) if text else []
+        pieces = [text[a:b] for a, b in zip([0] + cuts, cuts + [len(text)])]
+        m = StopMatcher(stops)
+        out = "".join(m.feed(p) for p in pieces) + m.flush()
+        assert not any(s in out for s in stops), (stops, pieces, out)
+        if m.matched is None:
+            assert out == text and not any(s in text for s in stops)
+        else:
+            assert text.startswith(out + m.matched), (stops, pieces, out, m.matched)
+    m = StopMatcher(("ab", "a"))
+    assert m.feed("xab") == "x" and m.matched == "ab"
+    m = StopMatcher(("a", "ab"))
+    assert m.feed("xab") == "x" and m.matched == "a"
