@@ -598,6 +598,64 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
   return 0;
 }
 
+// ---- static scratch of hk_attention_decode_noalloc ----
+// Layout: [0, 256) the position word; [256, 256 + 4 kScratchTickets) the
+// per-head split-KV tickets; then the split-KV partials, [q_heads][splits][66]
+// floats.  Every GPU holds its own copy until the process ends; calls on one
+// GPU share it.
+constexpr size_t kScratchTicketsOffset = 256;
+constexpr int kScratchTickets = 1024;
+constexpr size_t kScratchPartialOffset = kScratchTicketsOffset + 4 * kScratchTickets;
+constexpr size_t kScratchPartialBytes = size_t(1) << 20;
+constexpr size_t kScratchBytes = kScratchPartialOffset + kScratchPartialBytes;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch_address;  // device address of `scratch` per device
+
+// Device address of `scratch` on the current device, looked up once per
+// device (the array's name in host code is not a device address).
+int scratch_address(void** out) {
+  int dev = 0;
+  HK_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if ((int)g_scratch_address.size() <= dev) g_scratch_address.resize(dev + 1, nullptr);
+  if (g_scratch_address[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail("hipGetSymbolAddress(scratch) returned null");
+    g_scratch_address[dev] = ptr;
+  }
+  *out = g_scratch_address[dev];
+  return 0;
+}
+
+// Position word and cleared tickets for one attention call.
+__global__ void attention_scratch_kernel(int32_t* position_word, int32_t position, unsigned int* tickets, int n) {
+  if (threadIdx.x == 0) *position_word = position;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) tickets[i] = 0u;
+}
+
+// Argument checks shared by both attention entry points.
+int check_attention_args(const uint16_t* qkv, const float* rope_cos, const float* rope_sin,
+                         const uint16_t* kcache, const uint16_t* vcache, int32_t position,
+                         int32_t max_context, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                         const uint16_t* out) {
+  if (!qkv || !rope_cos || !rope_sin || !kcache || !vcache || !out)
+    return fail("hk_attention_decode: null pointer");
+  if (head_dim != kHeadDim) {
+    set_error("hk_attention_decode: only head_dim 64 is supported");
+    return HK_ERR_UNSUPPORTED;
+  }
+  if (max_context <= 0 || position < 0 || position >= max_context)
+    return fail("hk_attention_decode: position outside the context");
+  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0)
+    return fail("hk_attention_decode: q_heads must be a multiple of kv_heads");
+  if (max_context > kMaxContext) return fail("hk_attention_decode: context above 65536 slots");
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -619,7 +677,8 @@ int hk_init(int32_t device_ordinal) {
               prop.gcnArchName);
     return HK_ERR_UNSUPPORTED;
   }
-  return 0;
+  void* unused = nullptr;
+  return scratch_address(&unused);  // resolved once per device, here or at first use
 }
 
 int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
@@ -1053,19 +1112,10 @@ int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float*
                         uint16_t* kcache, uint16_t* vcache, int32_t position,
                         int32_t max_context, int32_t q_heads, int32_t kv_heads,
                         int32_t head_dim, uint16_t* out, void* stream) {
-  if (!qkv || !rope_cos || !rope_sin || !kcache || !vcache || !out)
-    return fail("hk_attention_decode: null pointer");
-  if (head_dim != kHeadDim) {
-    set_error("hk_attention_decode: only head_dim 64 is supported");
-    return HK_ERR_UNSUPPORTED;
-  }
-  if (max_context <= 0 || position < 0 || position >= max_context)
-    return fail("hk_attention_decode: position outside the context");
-  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0)
-    return fail("hk_attention_decode: q_heads must be a multiple of kv_heads");
+  HK_TRY(check_attention_args(qkv, rope_cos, rope_sin, kcache, vcache, position, max_context, q_heads,
+                              kv_heads, head_dim, out));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   std::lock_guard<std::mutex> lock(g_op_mutex);
-  if (max_context > kMaxContext) return fail("hk_attention_decode: context above 65536 slots");
   const int splits = attention_splits(max_context);
   OpScratch* s = nullptr;
   HK_TRY(op_scratch(&s, (size_t)q_heads * splits * (kHeadDim + 2), q_heads));
@@ -1081,6 +1131,43 @@ int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float*
   a.out = out;
   a.partial = s->partial;
   a.counters = s->counters;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.max_ctx = max_context;
+  a.max_splits = splits;
+  return launch_attention_decode(a, st);
+}
+
+int hk_attention_decode_noalloc(const uint16_t* qkv, const float* rope_cos, const float* rope_sin,
+                                uint16_t* kcache, uint16_t* vcache, int32_t position,
+                                int32_t max_context, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, uint16_t* out, void* stream) {
+  HK_TRY(check_attention_args(qkv, rope_cos, rope_sin, kcache, vcache, position, max_context, q_heads,
+                              kv_heads, head_dim, out));
+  const int splits = attention_splits(max_context);
+  const size_t partial_bytes = (size_t)q_heads * splits * (kHeadDim + 2) * sizeof(float);
+  if (q_heads > kScratchTickets || partial_bytes > kScratchPartialBytes)
+    return fail("hk_attention_decode_noalloc: q_heads x ceil(max_context / 256) x 264 bytes of split-KV "
+                "partials exceed its 1 MiB static scratch (" + std::to_string(partial_bytes) + " bytes asked)");
+  void* base = nullptr;
+  HK_TRY(scratch_address(&base));
+  unsigned char* b = static_cast<unsigned char*>(base);
+  int32_t* position_word = reinterpret_cast<int32_t*>(b);
+  unsigned int* tickets = reinterpret_cast<unsigned int*>(b + kScratchTicketsOffset);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(attention_scratch_kernel, dim3(1), dim3(256), 0, st, position_word, position, tickets,
+                     (int)q_heads);
+  HK_CHECK(hipGetLastError());
+  AttnArgs a = {};
+  a.qkv = qkv;
+  a.cos_tab = rope_cos;
+  a.sin_tab = rope_sin;
+  a.kcache = kcache;
+  a.vcache = vcache;
+  a.position = position_word;
+  a.out = out;
+  a.partial = reinterpret_cast<float*>(b + kScratchPartialOffset);
+  a.counters = tickets;
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;
   a.max_ctx = max_context;

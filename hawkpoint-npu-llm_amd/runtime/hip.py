@@ -112,6 +112,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
     ),
+    "hk_attention_decode_noalloc": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp],
+    ),
     "hk_stream_sync": (ctypes.c_int, [_vp]),
     "hk_moe_create": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp)]),
     "hk_moe_forward": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp]),

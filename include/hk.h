@@ -243,6 +243,21 @@ int hk_attention_decode(const uint16_t* qkv, const float* rope_cos, const float*
                         int32_t max_context, int32_t q_heads, int32_t kv_heads,
                         int32_t head_dim, uint16_t* out, void* stream);
 
+/* hk_attention_decode without any allocation, for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it).  No counterpart in the reference.  Same arguments, results
+ * and errors as hk_attention_decode; its scratch (the position word, one
+ * split-KV ticket per query head and the split-KV partials) is a static
+ * device array of 1 MiB + 4352 bytes per GPU, held until the process ends.
+ * HK_ERR_INVALID when q_heads > 1024 or q_heads * ceil(max_context / 256) *
+ * 264 bytes of partials exceed 1 MiB (Qwen2.5-0.5B's 14 heads: any context up
+ * to 65536).  Calls on one GPU share the scratch: calls that overlap in time
+ * on one GPU (several streams, or several host threads) race. */
+int hk_attention_decode_noalloc(const uint16_t* qkv, const float* rope_cos, const float* rope_sin,
+                                uint16_t* kcache, uint16_t* vcache, int32_t position,
+                                int32_t max_context, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, uint16_t* out, void* stream);
+
 /* Wait for all work on `stream`. */
 int hk_stream_sync(void* stream);
 
