@@ -10,7 +10,8 @@ per run with the prefill's token, the reference's "40-token prompt, 32
 tokens" protocol.  One step = one decode token: every layer, the final norm,
 the LM head and the argmax, with weights and KV resident in HBM.
 
-value = timed steps / wall seconds between two stream synchronisations.
+value = timed steps / wall seconds between two stream synchronisations, the
+median of --runs (default 5) timed runs of --steps steps each.
 roofline: the decode-step kernel -- one persistent launch runs the whole step
 (all 24 layers, the LM head and the argmax) -- timed with HIP events on the
 engine's stream over a graph of back-to-back step launches; achieved = the
@@ -18,7 +19,15 @@ step's algorithmic bytes (988 MB of weights plus KV) / its duration, against
 the MI355X's 8 TB/s HBM peak.  The per-kernel path (one GEMV or attention
 kernel per part, used for int8 weights and other shapes) is timed too.
 cpu_baseline: the oracle (NumPy BF16 CPU restatement of the reference's CPU
-runtime) on a bounded sample of the same workload.
+runtime) on a bounded sample of the same workload, with every host core and
+with one BLAS thread.
+smollm2_135m: the SmolLM2-135M-shaped decoder's decode tok/s and step-kernel
+roofline (35-token prompt, 16 greedy tokens, 64-slot context).
+
+Other workloads (each prints its own JSON line): --workload experts (the
+GGML / Colibri expert shims), gemv (the isolated batch-1 GEMVs at the
+Qwen2.5-0.5B projection shapes, bf16 and W8, for kernel traces), prefill
+(batched prefill of 40- and 4064-token prompts, for kernel traces).
 """
 
 import argparse
@@ -45,14 +54,14 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def step_bytes(meta, position):
+def step_bytes(meta, position, bias=True):
     """Algorithmic HBM bytes of one decode step at `position`: every weight
-    once (bf16), qkv bias, norm gains, the embedding row, KV read for slots
-    0..position and the new slot written."""
+    once (bf16), the qkv bias (when the model has one), norm gains, the
+    embedding row, KV read for slots 0..position and the new slot written."""
     h, i = meta["hidden_size"], meta["intermediate_size"]
     nq, nkv, d = meta["attention_heads"], meta["kv_heads"], meta["head_dim"]
     qkv = (nq + 2 * nkv) * d
-    per_layer = 2 * (qkv * h + h * nq * d + 2 * i * h + h * i) + 4 * qkv + 2 * 2 * h
+    per_layer = 2 * (qkv * h + h * nq * d + 2 * i * h + h * i) + (4 * qkv if bias else 0) + 2 * 2 * h
     head = 2 * meta["vocab_size"] * h + 2 * h
     kv_slot = meta["layers"] * 2 * nkv * d * 2
     return meta["layers"] * per_layer + head + 2 * h + kv_slot * (position + 1) + kv_slot
@@ -92,25 +101,58 @@ def part_bytes(meta, part):
     }.get(part)
 
 
-def cpu_baseline(model, prompt, decode_steps):
-    """Oracle decode tok/s on the host cores: a short prefill, then
-    `decode_steps` timed greedy steps (reference protocol: decode steps over
-    the seconds after TTFT)."""
+def _blas_info():
+    from threadpoolctl import threadpool_info
+
+    blas = [t for t in threadpool_info() if t.get("user_api") == "blas"]
+    return {"library": blas[0].get("internal_api") if blas else None,
+            "version": blas[0].get("version") if blas else None,
+            "threads": blas[0].get("num_threads") if blas else None}
+
+
+def cpu_baseline(model, prompt, steps_all, steps_one):
+    """Oracle decode tok/s on the host cores: the prompt through the oracle's
+    batched prefill (untimed), one untimed decode step (it widens the LM head
+    to float32 once, as the reference caches it), then timed greedy steps,
+    first with every BLAS thread, then with one.  Decode tok/s = steps /
+    their seconds (the reference's definition, generate.py:1167-1188)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
     from oracle.cpu_backend import OracleDecoder
 
-    threads = os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS")
-    cores = int(threads) if threads else len(os.sched_getaffinity(0))
-    oracle = OracleDecoder(model, len(prompt) + decode_steps + 1)
-    timings = []
-    oracle.generate_greedy(prompt, decode_steps + 1, keep_logits=False, timings=timings)
-    decode = timings[len(prompt):]
+    n = len(prompt)
+    oracle = OracleDecoder(model, n + max(steps_all, steps_one) + 2)
+    first, _ = oracle.prefill(prompt)
+    tok, _ = oracle.decode_token(first, n)
+
+    def timed_steps(count):
+        t, total = tok, 0.0
+        for k in range(count):
+            t0 = time.perf_counter()
+            t, _ = oracle.decode_token(t, n + 1 + k)
+            total += time.perf_counter() - t0
+        return count / total
+
+    blas = _blas_info()
+    all_cores = timed_steps(steps_all)
+    with threadpool_limits(limits=1):
+        one = timed_steps(steps_one)
+    host = {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "blas": blas["library"], "blas_version": blas["version"],
+            "OPENBLAS_NUM_THREADS": os.environ.get("OPENBLAS_NUM_THREADS"),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"), "numpy": np.__version__}
     return {
-        "value": round(len(decode) / sum(decode), 3),
+        "value": round(all_cores, 3),
         "unit": "tok/s",
-        "cores": cores,
+        "cores": blas["threads"],
         "kind": "port",
-        "sample": f"{len(prompt)}-token prefill then {len(decode)} greedy decode steps of the same "
-        f"model; NumPy {__import__('numpy').__version__} float32 BLAS, {cores} threads",
+        "sample": f"{n}-token prompt (oracle batched prefill, untimed) and one untimed step, then "
+        f"{steps_all} timed greedy decode steps of the same model; NumPy float32 BLAS with "
+        f"{blas['threads']} threads",
+        "one_thread": {"value": round(one, 3), "unit": "tok/s", "cores": 1,
+                       "sample": f"the same after the prompt, {steps_one} timed steps, one BLAS thread"},
+        "host": host,
     }
 
 
@@ -202,15 +244,18 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3100)
     ap.add_argument("--warmup", type=int, default=310)
+    ap.add_argument("--runs", type=int, default=5, help="timed runs of --steps steps; value is the median")
     ap.add_argument("--kernel-launches", type=int, default=240)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
     ap.add_argument("--no-parts", action="store_true",
-                    help="skip the graph-replayed step and per-part timing (for profiler runs)")
+                    help="skip the per-kernel path timing, which replays hipGraphs (for profiler runs)")
     ap.add_argument("--cpu-steps", type=int, default=16)
-    ap.add_argument("--workload", choices=("decode", "experts"), default="decode",
-                    help="experts: the GGML MUL_MAT_ID / Colibri expert-group shims instead of "
-                    "the decode step (prints its own JSON line)")
+    ap.add_argument("--cpu-steps-one-thread", type=int, default=4)
+    ap.add_argument("--no-smollm", action="store_true", help="skip the SmolLM2-135M decode line")
+    ap.add_argument("--workload", choices=("decode", "experts", "gemv", "prefill"), default="decode",
+                    help="experts: the GGML MUL_MAT_ID / Colibri expert-group shims; gemv: the isolated "
+                    "GEMVs; prefill: batched prefills of 40 and 4064 tokens (each prints its own JSON line)")
     ap.add_argument("--probe", action="store_true",
                     help="only the counter-calibration workload: decode-step launches, then "
                     "4 device copies of 256 MiB")
@@ -221,6 +266,12 @@ def main():
         sys.exit(2)
     if args.workload == "experts":
         experts_main(args)
+        return
+    if args.workload == "gemv":
+        gemv_main(args)
+        return
+    if args.workload == "prefill":
+        prefill_main(args)
         return
 
     import numpy as np
@@ -272,31 +323,33 @@ def main():
         return tokens
 
     decode(args.warmup)
-    hip.check(lib.hk_stream_sync(engine.stream), "sync")
-    t0 = time.perf_counter()
-    decode(args.steps)
-    hip.check(lib.hk_stream_sync(engine.stream), "sync")
-    elapsed = time.perf_counter() - t0
-    tok_s = args.steps / elapsed
-    ms_step = elapsed / args.steps * 1e3
-    mean_pos = PROMPT + (RUN - 1) / 2.0
+    run_tok_s = []
+    for _ in range(max(1, args.runs)):
+        hip.check(lib.hk_stream_sync(engine.stream), "sync")
+        t0 = time.perf_counter()
+        decode(args.steps)
+        hip.check(lib.hk_stream_sync(engine.stream), "sync")
+        run_tok_s.append(args.steps / (time.perf_counter() - t0))
+    tok_s = sorted(run_tok_s)[len(run_tok_s) // 2]
+    ms_step = 1e3 / tok_s
+    last_pos = PROMPT + min(args.steps, RUN) - 1  # the positions a run covers: PROMPT .. last_pos
+    mean_pos = (PROMPT + last_pos) / 2.0
     step_gbs = step_bytes(meta, mean_pos) / (ms_step * 1e-3) / 1e9
-    log(f"decode: {tok_s:.1f} tok/s, {ms_step * 1e3:.1f} us/step, {step_gbs:.0f} GB/s whole step")
+    log(f"decode: {tok_s:.1f} tok/s (median of {len(run_tok_s)} runs: "
+        f"{', '.join(f'{v:.0f}' for v in run_tok_s)}), {ms_step * 1e3:.1f} us/step, {step_gbs:.0f} GB/s whole step")
 
     stream = engine.stream
     end_pos = PROMPT + RUN  # ctrl position after the last timed run
     # the decode-step kernel: a graph of back-to-back step launches at the
     # last position (no token feedback), timed with HIP events on its stream
     n = args.kernel_launches
-    if args.no_parts:  # profiler runs: no graph replays; the step's wall time stands in
-        step_kernel_us = ms_step * 1e3
-    else:
-        ev0, ev1 = hip.Event(), hip.Event()
-        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
-        ev0.record(stream)
-        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
-        ev1.record(stream)
-        step_kernel_us = ev0.elapsed_ms(ev1) * 1e3 / n
+    # (a persistent step is repeated as direct launches, no graph)
+    ev0, ev1 = hip.Event(), hip.Event()
+    hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
+    ev0.record(stream)
+    hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
+    ev1.record(stream)
+    step_kernel_us = ev0.elapsed_ms(ev1) * 1e3 / n
     dom_bytes = step_bytes(meta, end_pos)
     achieved = dom_bytes / (step_kernel_us * 1e-6) / 1e9
     log(f"decode-step kernel: {step_kernel_us:.1f} us/launch, {achieved:.0f} GB/s")
@@ -347,7 +400,7 @@ def main():
     w8_tok_s = sorted(w8_runs)[len(w8_runs) // 2]
     w8_kind = w8.step_kind(PROMPT)
     w8_kernel_us = None
-    if not args.no_parts:  # the W8 step kernel alone, as for the bf16 one above
+    if True:  # the W8 step kernel alone, as for the bf16 one above
         ev0, ev1 = hip.Event(), hip.Event()
         hip.check(lib.hk_engine_launch_part_repeat(w8._engine, hip.PART_STEP, n), "W8 step repeat")
         ev0.record(w8.stream)
@@ -376,6 +429,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "runs": [round(v, 2) for v in run_tok_s],
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -385,10 +439,11 @@ def main():
         "config": {
             "workload": "Qwen2.5-0.5B-shape decoder (24L, H896, 14q/2kv heads, I4864, V151936, "
             "tied head, qkv bias), seeded N(0,0.02) bf16 weights, batch 1, 40-token random prompt "
-            "prefilled per position, greedy decode at positions 40..70 in 31-step runs",
+            f"prefilled per position, greedy decode from position 40 in runs of up to {RUN} steps; value = "
+            f"median of {len(run_tok_s)} timed runs",
             "batch": 1,
             "prompt_tokens": PROMPT,
-            "decode_positions": [PROMPT, PROMPT + RUN - 1],
+            "decode_positions": [PROMPT, last_pos],
             "kv_slots_allocated": 4096,
         },
         "ttft_ms": round(ttft * 1e3, 3),
@@ -441,10 +496,105 @@ def main():
         log("GEMV microbench (512 MiB rotation)")
         result["gemv_microbench"] = gemv_microbench()
         log(" ".join(f"{k}:{v['gbs']:.0f}GB/s" for k, v in result["gemv_microbench"].items()))
+    if not args.no_smollm:
+        log("SmolLM2-135M shape")
+        result["smollm2_135m"] = smollm_decode(args)
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
-        result["cpu_baseline"] = cpu_baseline(model, prompt[:8], args.cpu_steps)
+        result["cpu_baseline"] = cpu_baseline(model, prompt, args.cpu_steps, args.cpu_steps_one_thread)
     print(json.dumps(result), flush=True)
+
+
+def smollm_decode(args, runs=5):
+    """SmolLM2-135M-shaped decoder (30 layers, H576, 9/3 heads, I1536,
+    V49152, tied head, no qkv bias), seeded N(0,0.02) bf16 weights: a
+    35-token prompt in one batched prefill, then 15 greedy steps (16 tokens)
+    at positions 35..49 in a 64-slot context, median of `runs` runs; and the
+    step kernel alone (direct launches at position 50, HIP events)."""
+    import numpy as np
+
+    from runtime import hip
+    from runtime.qwen_engine import QwenDecoderEngine
+    from runtime.synthetic import SMOLLM2_135M, SyntheticModel
+
+    lib = hip.lib()
+    model = SyntheticModel(SMOLLM2_135M, seed=0)
+    meta = model.metadata
+    prompt = [int(t) for t in np.random.default_rng(11).integers(0, meta["vocab_size"], 35)]
+    engine = QwenDecoderEngine(model, context_length=64)
+    try:
+        first, _ = engine.prefill(prompt, want_logits_array=False)
+        engine.generate(first, 35, 15)
+        rates = []
+        for _ in range(runs):
+            hip.check(lib.hk_stream_sync(engine.stream), "sync")
+            t0 = time.perf_counter()
+            engine.generate(first, 35, 15)
+            rates.append(15 / (time.perf_counter() - t0))
+        n = args.kernel_launches
+        ev0, ev1 = hip.Event(), hip.Event()
+        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
+        ev0.record(engine.stream)
+        hip.check(lib.hk_engine_launch_part_repeat(engine._engine, hip.PART_STEP, n), "step repeat")
+        ev1.record(engine.stream)
+        us = ev0.elapsed_ms(ev1) * 1e3 / n
+        kind = engine.step_kind(50)
+    finally:
+        engine.close()
+    nbytes = step_bytes(meta, 50, bias=False)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    tok_s = sorted(rates)[len(rates) // 2]
+    log(f"SmolLM2-135M: {tok_s:.1f} tok/s ({kind} step), step kernel {us:.1f} us, {gbs:.0f} GB/s")
+    return {"workload": "SmolLM2-135M-shape decoder, seeded N(0,0.02) bf16 weights, 35-token prompt "
+            "(batched prefill), 16 greedy tokens (15 decode steps at positions 35..49), 64-slot context",
+            "tok_s": round(tok_s, 1), "runs": [round(v, 1) for v in rates], "step": kind,
+            "step_kernel_us": round(us, 2), "step_bytes": int(nbytes),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "note": "269 MB per step: the weights fit the 256 MB Infinity Cache almost whole"}}
+
+
+def gemv_main(args):
+    """Only the isolated GEMV microbench (for kernel traces of its launches)."""
+    from runtime import hip
+
+    hip.init(0)
+    out = gemv_microbench()
+    print(json.dumps({"workload": "gemv", "gemv_microbench": out}), flush=True)
+
+
+def prefill_main(args):
+    """Batched prefills of the Qwen2.5-0.5B-shape decoder for kernel traces:
+    the 40-token prompt five times and a 4064-token prompt three times
+    (wall-clock times printed; the kernel durations come from the trace)."""
+    import numpy as np
+
+    from runtime.qwen_engine import QwenDecoderEngine
+    from runtime.synthetic import QWEN25_05B, SyntheticModel
+
+    model = SyntheticModel(QWEN25_05B, seed=0)
+    meta = model.metadata
+    rng = np.random.default_rng(12)
+    short = [int(t) for t in rng.integers(0, meta["vocab_size"], PROMPT)]
+    long_prompt = [int(t) for t in rng.integers(0, meta["vocab_size"], 4064)]
+    engine = QwenDecoderEngine(model, context_length=4096)
+    out = {"workload": "prefill", "prompt_40_ms": [], "prompt_4064_ms": []}
+    try:
+        engine.prefill(short)
+        for _ in range(5):
+            t0 = time.perf_counter()
+            engine.prefill(short, want_logits_array=False)
+            out["prompt_40_ms"].append(round((time.perf_counter() - t0) * 1e3, 3))
+        for _ in range(3):
+            t0 = time.perf_counter()
+            engine.prefill(long_prompt, want_logits_array=False)
+            out["prompt_4064_ms"].append(round((time.perf_counter() - t0) * 1e3, 3))
+    finally:
+        engine.close()
+    attn = 4.0 * meta["attention_heads"] * meta["head_dim"] * meta["layers"] * 4064 * 4065 / 2
+    out["flops_4064"] = 2.0 * 4064 * layer_params(meta) + attn
+    out["flops_40"] = 2.0 * PROMPT * layer_params(meta)
+    print(json.dumps(out), flush=True)
 
 
 EXPERTS, EXPERT_ROWS, EXPERT_COLS = 8, 2048, 2048  # the reference's 8 expert slots of 2048 x 2048

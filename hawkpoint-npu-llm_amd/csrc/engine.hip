@@ -513,11 +513,16 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
   const hipStream_t s = e->stream;
   const int H = d.hidden, I = d.intermediate, QD = d.q_heads * kHeadDim;
   HK_TRY(launch_embed_rows(tokens_dev, n, d.vocab, e->w.token_embedding, H, e->pf_x, s));
+  // chunks of up to 64 tokens run the slab GEMMs, which apply the RMSNorms
+  // to their A operand as they load it (hidden sizes up to 1024)
+  const bool fused_norm = n <= kSlabMaxTokens && H <= kSlabNormMaxK;
   for (int l = 0; l < d.layers; ++l) {
     const hk_layer_weights& lw = e->layers[l];
-    HK_TRY(launch_rmsnorm_rows(e->pf_x, H, lw.input_norm, d.rms_eps, e->pf_xn, H, n, H, s));
+    if (!fused_norm) HK_TRY(launch_rmsnorm_rows(e->pf_x, H, lw.input_norm, d.rms_eps, e->pf_xn, H, n, H, s));
     PrefillGemmArgs q = {};
-    q.A = e->pf_xn;
+    q.A = fused_norm ? e->pf_x : e->pf_xn;
+    q.gamma = fused_norm ? lw.input_norm : nullptr;
+    q.eps = d.rms_eps;
     q.lda = H;
     q.W = static_cast<const uint16_t*>(lw.qkv);
     q.scale = e->w8 ? lw.qkv_scale : nullptr;
@@ -563,9 +568,11 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     o.split_ws = e->pf_split;
     o.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(o, s));
-    HK_TRY(launch_rmsnorm_rows(e->pf_h1, H, lw.post_attn_norm, d.rms_eps, e->pf_xn, H, n, H, s));
+    if (!fused_norm) HK_TRY(launch_rmsnorm_rows(e->pf_h1, H, lw.post_attn_norm, d.rms_eps, e->pf_xn, H, n, H, s));
     PrefillGemmArgs g = {};
-    g.A = e->pf_xn;
+    g.A = fused_norm ? e->pf_h1 : e->pf_xn;
+    g.gamma = fused_norm ? lw.post_attn_norm : nullptr;
+    g.eps = d.rms_eps;
     g.lda = H;
     g.W = static_cast<const uint16_t*>(lw.gate_up);
     g.scale = e->w8 ? lw.gate_up_scale : nullptr;
@@ -944,6 +951,13 @@ int hk_engine_launch_part_repeat(hk_engine* e, int32_t part, int32_t count) {
   if (count <= 0 || count > 100000) return fail("hk_engine_launch_part_repeat: count out of range");
   HK_CHECK(hipSetDevice(e->device));
   if (part >= HK_PART_HEAD) HK_TRY(set_ctrl_keep(e));
+  if (part == HK_PART_STEP && e->pshape >= 0) {
+    // one persistent launch per step: launched back to back, the GPU never
+    // waits for the host, so no graph is needed (and profilers that trace
+    // kernels see ordinary launches)
+    for (int i = 0; i < count; ++i) HK_TRY(launch_persistent(e, true));
+    return 0;
+  }
   const long long key = (long long)part << 32 | (unsigned)count |
                         (part == HK_PART_STEP && e->pshape >= 0 ? (long long)step_form(e) << 60 : 0);
   auto it = e->repeat_graphs.find(key);

@@ -1,7 +1,7 @@
 // Device-side helpers shared by every hk kernel (gfx950, wave64).
 //
 // BF16 values travel as uint16 bit patterns.  The float32 -> bfloat16 cast is
-// round-to-nearest-even with a quiet-NaN branch, the same rounding the
+// round-to-nearest-even (NaN stays a quiet NaN), the same rounding the
 // reference's CPU runtime gets from ml_dtypes (npu_llm/runtime/cpu_backend.py:7-8)
 // and writes out as integer code in npu_llm/kernels/qwen_engine_common.h:35-46.
 //
@@ -22,13 +22,19 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
+// One v_cvt_pk_bf16_f32 (gfx950), round to nearest even.  Run on the device
+// over all 2^32 float32 bit patterns it gives exactly
+//   (u + 0x7fff + ((u >> 16) & 1)) >> 16   (u the float's bits)
+// for every non-NaN input; a NaN stays a quiet NaN of the same sign.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  // both results are formed and one selected: a branch here would diverge
-  // per element and cost more than the arithmetic
-  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t nan = ((u >> 16) & 0x8000u) | 0x7fc0u;
-  return (u & 0x7fffffffu) > 0x7f800000u ? nan : rounded;
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// Two floats as one packed bf16 pair (lo in bits 0..15), one instruction.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
 __device__ __forceinline__ float round_bf16(float f) {
@@ -38,6 +44,13 @@ __device__ __forceinline__ float round_bf16(float f) {
 // Low / high bf16 of a packed 32-bit word (element 2i is the low half).
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Buffer resource over [base, base + bytes): loads through it take a 32-bit
+// byte offset, and offsets past `bytes` read zero instead of faulting, so a
+// load that may fall outside needs no branch around it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
 
 // Global-memory accesses go through address-space-1 pointers.  Through a
 // generic pointer the compiler emits flat instructions, which count in both

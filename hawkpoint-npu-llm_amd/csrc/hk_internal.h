@@ -221,7 +221,16 @@ struct PrefillGemmArgs {
   // unsplit.
   float* split_ws;
   size_t split_ws_floats;
+  // Prompts of at most kSlabMaxTokens tokens run on the slab GEMM (one
+  // workgroup per 16 outputs over all of K; no workspace).  With `gamma` (K at
+  // most kSlabNormMaxK) the A rows are RMSNorm inputs, normalised as they are
+  // loaded: A = bf16((x * inv_rms) * gamma) with inv_rms = 1 / sqrt(mean(x^2) + eps).
+  const uint16_t* gamma;
+  float eps;
 };
+
+constexpr int kSlabMaxTokens = 64;
+constexpr int kSlabNormMaxK = 1024;
 
 constexpr int kSplitTarget = 256;  // workgroups the split aims for
 // float32 workspace the split-K path needs for an M x N GEMM (2N outputs

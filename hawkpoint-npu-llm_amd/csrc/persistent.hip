@@ -103,11 +103,6 @@ __device__ __forceinline__ unsigned long long ld_c64(const unsigned long long* p
   return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
 }
-// Buffer resource over [base, base + bytes): loads through it take a 32-bit
-// byte offset, and offsets past `bytes` read zero instead of faulting.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
 
 
 __device__ __forceinline__ bool reached(unsigned v, unsigned target) {
@@ -262,6 +257,7 @@ struct Shape {
   static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
                              xnq + HQ <= kXcdWg && xhn <= (kXcdWg - xnq) * kSW &&
                              2 * xg.nj + 4 * xkd <= kPf && xno <= xnq && xsl <= 64 && H <= kHMax &&
+                             (!W8 || (2 * (xq.nj + xo.nj) <= kPf && 4 * xg.nj + 8 * xkd <= kPf)) &&
                              I % 4 == 0 && xnq <= kXcdWg && xng <= kPersistentGrid - kXcdWg;
 };
 
@@ -293,6 +289,8 @@ struct Ctx {
   int gw;  // compute-wave index wg * kCW + wave (wave < kCW)
 };
 
+constexpr unsigned kOutsideWord = 0x7ffffff0u;  // byte offset beyond every resource (reads zero)
+
 // Record an abandoned launch (first failing wait) for the host.
 __device__ __forceinline__ bool give_up(const PersistentArgs& a) {
   st_c32(a.error, 1u);
@@ -315,6 +313,29 @@ __device__ bool poll_word(const PersistentArgs& a, const uint32_t* p, unsigned t
       out = w;
       return true;
     }
+    if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Poll the N tagged words at byte offsets off[i] of the buffer r together
+// (one round trip per poll round) until each carries `tag`; an offset of
+// kOutside marks a word this thread does not wait for (it reads zero).  False
+// when the launch is abandoned.
+template <int N, int POL>
+__device__ bool poll_words(const PersistentArgs& a, __amdgpu_buffer_rsrc_t r, const unsigned (&off)[N],
+                           unsigned tag, uint32_t (&w)[N]) {
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) any = any || off[i] != kOutsideWord;
+  if (!any) return true;
+  for (unsigned spins = 1;; ++spins) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_raw_buffer_load_b32(r, off[i], 0, POL);
+    bool have = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) have = have && (off[i] == kOutsideWord || (w[i] >> 16) == tag);
+    if (have) return true;
     if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
     __builtin_amdgcn_s_sleep(1);
   }
@@ -489,8 +510,13 @@ __device__ __forceinline__ void normalise_staged(Ctx& c, uint16_t* xs, float eps
 // every phase and the compiler can wait for exactly the loads it needs.
 constexpr unsigned kOutside = 0x7ffffff0u;  // byte offset beyond every resource
 constexpr int kNT = 2;                      // buffer-load cache policy: non-temporal
+// The LM head's weights load with the default policy, the layers' with nt:
+// measured, that keeps part of the 272 MB head in the Infinity Cache from
+// one step to the next (304.0 against 307.4 us per Qwen2.5-0.5B step; layer
+// weights with the default policy too: 323.8 us)
+constexpr int kHeadPol = 0;
 
-template <int LPR, int NJ, bool PAIR, int OFF, int EB = 2>
+template <int LPR, int NJ, bool PAIR, int OFF, int EB = 2, int POL = kNT, int UOFF = OFF + NJ>
 __device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const void* W, int M, int K,
                                          int group, bool live_wg) {
   constexpr int RPW = 64 / LPR;
@@ -505,9 +531,9 @@ __device__ __forceinline__ void prefetch(u32x4 (&pf)[kPf], const void* W, int M,
   const unsigned voff = live ? (unsigned)row * (unsigned)K * (unsigned)EB + (unsigned)l * 16u : kOutside;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    pf[OFF + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, j * LPR * 16, kNT);
+    pf[OFF + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, j * LPR * 16, POL);
     if constexpr (PAIR)
-      pf[OFF + NJ + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, M * K * EB + j * LPR * 16, kNT);
+      pf[UOFF + j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, M * K * EB + j * LPR * 16, POL);
   }
 }
 
@@ -558,7 +584,24 @@ __device__ __forceinline__ void fma16_i8(const u32x4 w, const u32x4 x0, const u3
   a1 = dot2(i8pair_bf16(w.w, 2), x1.w, a1);
 }
 
-template <int LPR, int NJ, bool PAIR, int OFF, int EB = 2>
+// W8 rows widened ahead of their dot products: the N raw 16-byte int8 chunks
+// in slots OFF + N .. OFF + 2N - 1 become 2N chunks of bf16 pairs in slots
+// OFF .. OFF + 2N - 1 (raw chunk i: its weights 0..7 in slot OFF + 2i, 8..15
+// in OFF + 2i + 1).  A wave does this while it waits for the phase's input,
+// so the dot products then cost what bf16 rows cost.
+template <int OFF, int N>
+__device__ __forceinline__ void widen_w8(u32x4 (&pf)[kPf]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const u32x4 w = pf[OFF + N + i];
+    pf[OFF + 2 * i] = u32x4{i8pair_bf16(w.x, 0), i8pair_bf16(w.x, 2), i8pair_bf16(w.y, 0), i8pair_bf16(w.y, 2)};
+    pf[OFF + 2 * i + 1] = u32x4{i8pair_bf16(w.z, 0), i8pair_bf16(w.z, 2), i8pair_bf16(w.w, 0), i8pair_bf16(w.w, 2)};
+  }
+}
+
+// EB 1 with WIDE: the rows' int8 chunks were widened by widen_w8 (chunk j in
+// slots OFF + 2j, OFF + 2j + 1; with PAIR the up rows' from OFF + 2 NJ).
+template <int LPR, int NJ, bool PAIR, int OFF, int EB = 2, bool WIDE = false>
 __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t* xs, int K,
                                           float& acc, float& accu) {
   if constexpr (EB == 1) {
@@ -581,8 +624,17 @@ __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t
     float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      fma16_i8(pf[OFF + j], xv[j][0], xv[j][1], a0, a1);
-      if constexpr (PAIR) fma16_i8(pf[OFF + NJ + j], xv[j][0], xv[j][1], b0, b1);
+      if constexpr (WIDE) {
+        fma8(pf[OFF + 2 * j], xv[j][0], a0, a1);
+        fma8(pf[OFF + 2 * j + 1], xv[j][1], a0, a1);
+        if constexpr (PAIR) {
+          fma8(pf[OFF + 2 * NJ + 2 * j], xv[j][0], b0, b1);
+          fma8(pf[OFF + 2 * NJ + 2 * j + 1], xv[j][1], b0, b1);
+        }
+      } else {
+        fma16_i8(pf[OFF + j], xv[j][0], xv[j][1], a0, a1);
+        if constexpr (PAIR) fma16_i8(pf[OFF + NJ + j], xv[j][0], xv[j][1], b0, b1);
+      }
     }
     if constexpr (LPR >= 16) {
       acc = wave_sum<LPR>(a0 + a1);
@@ -668,48 +720,54 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     vw[k] = __builtin_amdgcn_raw_buffer_load_b32(vc, voff, k * kHeadDim * 2, 0);
 
   const int qr = h * kHeadDim, kr = (S::HQ + g) * kHeadDim, vr = (S::HQ + S::HKV + g) * kHeadDim;
-  const uint32_t* tq = a.tqkv;
   const __amdgpu_buffer_rsrc_t tqr = rsrc(a.tqkv, S::QKV * 4);
-  bool ok = true;
-  // the slot-p value word of the P @ V loop, for the group holding slot p
-  if (p - t0 - gi * kSlotsPV >= 0 && p - t0 - gi * kSlotsPV < kSlotsPV) {
-    const int kp = p - t0 - gi * kSlotsPV;
-    uint32_t lo = 0, hi = 0;
-    ok = poll_word<POL>(a, tq + vr + 2 * dp, tag_q, lo, tqr, (vr + 2 * dp) * 4) &&
-         poll_word<POL>(a, tq + vr + 2 * dp + 1, tag_q, hi, tqr, (vr + 2 * dp + 1) * 4);
-    const uint32_t word = (lo & 0xffffu) | (hi << 16);
+  // The words this thread waits for, polled together: [0, 1] its halves of
+  // q or of the new key (threads 0..63, for RoPE), [2, 3] the new value (the
+  // key threads of the group's first query head append k and v at slot p),
+  // [4, 5] the slot-p value word of its P @ V group
+  const int j = tid & (kHalf - 1);
+  const bool rope = tid < 2 * kHalf;
+  const bool is_k = tid >= kHalf;
+  const bool appends = rope && is_k && holds_new && h % S::QPK == 0;
+  const int kp = p - t0 - gi * kSlotsPV;  // slot p's index within this thread's P @ V group
+  const bool pv_new = kp >= 0 && kp < kSlotsPV;
+  const int src_row = is_k ? kr : qr;
+  unsigned off[6];
+  off[0] = rope ? (unsigned)(src_row + j) * 4u : kOutsideWord;
+  off[1] = rope ? (unsigned)(src_row + j + kHalf) * 4u : kOutsideWord;
+  off[2] = appends ? (unsigned)(vr + j) * 4u : kOutsideWord;
+  off[3] = appends ? (unsigned)(vr + j + kHalf) * 4u : kOutsideWord;
+  off[4] = pv_new ? (unsigned)(vr + 2 * dp) * 4u : kOutsideWord;
+  off[5] = pv_new ? (unsigned)(vr + 2 * dp + 1) * 4u : kOutsideWord;
+  float cs = 0.0f, sn = 0.0f;  // RoPE of position p (constant tables: fetched ahead of the poll)
+  if (rope) {
+    cs = ldg(a.cos_tab + (size_t)p * kHalf + j);
+    sn = ldg(a.sin_tab + (size_t)p * kHalf + j);
+  }
+  uint32_t w[6];
+  bool ok = poll_words<6, POL>(a, tqr, off, tag_q, w);
+  if (pv_new) {
+    const uint32_t word = (w[4] & 0xffffu) | (w[5] << 16);
 #pragma unroll
     for (int k = 0; k < kSlotsPV; ++k)
       if (k == kp) vw[k] = word;
   }
   // rotated q head and new key (bf16-rounded); the group's first query head
   // appends k and v at slot p
-  if (tid < 2 * kHalf && ok) {
-    const int j = tid & (kHalf - 1);
-    const bool is_k = tid >= kHalf;
-    const int src_row = is_k ? kr : qr;
-    const uint32_t* src = tq + src_row;
-    const float cs = ldg(a.cos_tab + (size_t)p * kHalf + j);
-    const float sn = ldg(a.sin_tab + (size_t)p * kHalf + j);
-    uint32_t w1 = 0, w2 = 0;
-    ok = poll_word<POL>(a, src + j, tag_q, w1, tqr, (src_row + j) * 4) &&
-         poll_word<POL>(a, src + j + kHalf, tag_q, w2, tqr, (src_row + j + kHalf) * 4);
-    const float x1 = bf_lo(w1), x2 = bf_lo(w2);
+  if (rope && ok) {
+    const float x1 = bf_lo(w[0]), x2 = bf_lo(w[1]);
     const uint32_t r1 = f32_to_bf16(x1 * cs - x2 * sn);
     const uint32_t r2 = f32_to_bf16(x2 * cs + x1 * sn);
     uint16_t* dst = is_k ? knew : qs;
     dst[j] = (uint16_t)r1;
     dst[j + kHalf] = (uint16_t)r2;
-    if (is_k && holds_new && h % S::QPK == 0 && ok) {
-      uint32_t v1 = 0, v2 = 0;
-      ok = poll_word<POL>(a, tq + vr + j, tag_q, v1, tqr, (vr + j) * 4) &&
-           poll_word<POL>(a, tq + vr + j + kHalf, tag_q, v2, tqr, (vr + j + kHalf) * 4);
+    if (appends) {
       uint16_t* kd = a.kcache + (head_base + p) * kHeadDim;
       uint16_t* vd = a.vcache + (head_base + p) * kHeadDim;
       stg(kd + j, (uint16_t)r1);
       stg(kd + j + kHalf, (uint16_t)r2);
-      stg(vd + j, (uint16_t)v1);
-      stg(vd + j + kHalf, (uint16_t)v2);
+      stg(vd + j, (uint16_t)w[2]);
+      stg(vd + j + kHalf, (uint16_t)w[3]);
     }
   }
   if (__syncthreads_or(!ok)) return false;
@@ -952,14 +1010,14 @@ __device__ __forceinline__ void lm_head_phase(Ctx& c, u32x4 (&pf)[kPf], int buf,
   float* const lpad = a.logits + a.vocab + c.wg * kPW + c.wave;
   u32x4 wb[kPf];
   int grp = c.wg * kPW + c.wave;
-  if (!stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
+  if (!stager) prefetch<HL, HNJ, false, 0, 2, kHeadPol>(pf, a.lm_head, a.vocab, S::H, grp, true);
   {
     bool ok = true;
     if (stager) ok = stage_wave<S::H, true, false>(c, a.th, tag_of(ep_layers), a.final_norm, sm.xs[buf], nullptr);
     if (!handoff(ok)) return;
     normalise_staged<S::H>(c, sm.xs[buf], a.eps);
   }
-  if (stager) prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp, true);
+  if (stager) prefetch<HL, HNJ, false, 0, 2, kHeadPol>(pf, a.lm_head, a.vocab, S::H, grp, true);
   const uint16_t* xh = sm.xs[buf];
   unsigned long long best = 0ull;
   const int sub = c.lane / HL;
@@ -970,11 +1028,11 @@ __device__ __forceinline__ void lm_head_phase(Ctx& c, u32x4 (&pf)[kPf], int buf,
     best = umax64(best, valid ? argmax_key(acc, (uint32_t)row) : 0ull);
   };
   for (int it = 0; it < iters; it += 2) {
-    prefetch<HL, HNJ, false, 0>(wb, a.lm_head, a.vocab, S::H, grp + stride, true);
+    prefetch<HL, HNJ, false, 0, 2, kHeadPol>(wb, a.lm_head, a.vocab, S::H, grp + stride, true);
     dot_group<HL, HNJ, false, 0>(pf, xh, S::H, acc, accu);
     finish(grp);
     grp += stride;
-    prefetch<HL, HNJ, false, 0>(pf, a.lm_head, a.vocab, S::H, grp + stride, true);
+    prefetch<HL, HNJ, false, 0, 2, kHeadPol>(pf, a.lm_head, a.vocab, S::H, grp + stride, true);
     dot_group<HL, HNJ, false, 0>(wb, xh, S::H, acc, accu);
     finish(grp);
     grp += stride;
@@ -1245,13 +1303,34 @@ __device__ __forceinline__ void prefetch_down_x(u32x4 (&pf)[kPf], const uint16_t
 // For W8 (unscaled int8 down rows; the row scale is applied to the finished
 // sum in reduce_h) a chunk holds 16 outputs: slot q outputs 4q .. 4q + 3,
 // each as the four rows' int8 weights.
-template <class S, int OFF>
+template <class S, int OFF, bool WIDE = false>
 __device__ __forceinline__ void down_partial(const u32x4 (&pf)[kPf], uint32_t act, float* ws) {
   constexpr int CC = S::xdc;
   const int lane = threadIdx.x & 63;
   const uint32_t a0 = __shfl(act, 0, 64), a1 = __shfl(act, 16, 64);
   const uint32_t a2 = __shfl(act, 32, 64), a3 = __shfl(act, 48, 64);
   const uint32_t A01 = (a0 & 0xffffu) | (a1 << 16), A23 = (a2 & 0xffffu) | (a3 << 16);
+  if constexpr (S::W8 && WIDE) {
+    // widened chunks (widen_w8): slot q of chunk k holds outputs 2q, 2q + 1
+    // of its 16, the four rows' bf16 weights each, as for bf16 rows
+#pragma unroll
+    for (int k = 0; k < S::xkd; ++k) {
+      const int cc = lane + 64 * k;
+      float o[16];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const u32x4 w = pf[OFF + 8 * k + q];
+        o[2 * q] = dot2(w.x, A01, dot2(w.y, A23, 0.0f));
+        o[2 * q + 1] = dot2(w.z, A01, dot2(w.w, A23, 0.0f));
+      }
+      if (cc < CC) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          reinterpret_cast<float4*>(ws + 16 * cc)[q] = make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+      }
+    }
+    return;
+  }
   if constexpr (S::W8) {
 #pragma unroll
     for (int k = 0; k < S::xkd; ++k) {
@@ -1461,7 +1540,11 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
 
   if (attn) {
     constexpr PhaseCfg Q = S::xq, O = S::xo;
-    constexpr int RQ = 64 / Q.lpr, RO = 64 / O.lpr, OFF_O = Q.nj;
+    // register slots: Q rows from 0, O rows after them; W8 rows are loaded
+    // into the upper half of twice their slots and widened there (widen_w8)
+    constexpr int WQ = S::W8 ? 2 : 1;
+    constexpr int RQ = 64 / Q.lpr, RO = 64 / O.lpr, OFF_O = WQ * Q.nj;
+    constexpr int LQ = S::W8 ? Q.nj : 0, LO = OFF_O + (S::W8 ? O.nj : 0);  // where the loads land
     const bool is_q = rank < S::xnq, is_o = rank < S::xno;
     const int row_q = c.gw * RQ + c.lane / Q.lpr, row_o = c.gw * RO + c.lane / O.lpr;
     const int fo = rank * kPW * RO;
@@ -1477,8 +1560,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       sq = row_scale<Q.lpr>(sm.layers[0].qkv_scale, S::QKV, c.gw, pq);
       so = row_scale<O.lpr>(sm.layers[0].o_scale, S::H, c.gw, po);
     }
-    prefetch<Q.lpr, Q.nj, false, 0, S::EB>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
-    prefetch<O.lpr, O.nj, false, OFF_O, S::EB>(pf, sm.layers[0].o, S::H, S::AO, c.gw, po);
+    prefetch<Q.lpr, Q.nj, false, LQ, S::EB>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
+    prefetch<O.lpr, O.nj, false, LO, S::EB>(pf, sm.layers[0].o, S::H, S::AO, c.gw, po);
     float bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                  bias_rsrc<S>(sm.layers[0].qkv_bias), bias_off, 0, 0));
     for (int l = 0; l < L; ++l) {
@@ -1489,6 +1572,10 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       // ---- Q: h from the MLP side (across XCDs) ----
       if (is_q) {
         bool ok = true;
+        if constexpr (S::W8) {  // before the wait: the loads have had the MLP phase to land
+          widen_w8<0, Q.nj>(pf);
+          if (is_o) widen_w8<OFF_O, O.nj>(pf);
+        }
         if (stager) {
           if (l == 0)
             stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
@@ -1501,7 +1588,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       {  // all eight waves; the rows go straight to XCD 0's L2 (only the
          // attention tasks there poll them): each row's first lane stores it,
          // the other lanes the wave's pad word, one store per wave
-        dot_group<Q.lpr, Q.nj, false, 0, S::EB>(pf, sm.xs[buf], S::H, acc, accu);
+        dot_group<Q.lpr, Q.nj, false, 0, S::EB, S::W8>(pf, sm.xs[buf], S::H, acc, accu);
         if constexpr (S::W8) acc *= sq;
         const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
         if constexpr (LONG) {  // to the MLP workgroups: gathered, one writer per workgroup
@@ -1529,7 +1616,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
       }
       {  // all eight waves
-        dot_group<O.lpr, O.nj, false, OFF_O, S::EB>(pf, sm.xs[buf], S::AO, acc, accu);
+        dot_group<O.lpr, O.nj, false, OFF_O, S::EB, S::W8>(pf, sm.xs[buf], S::AO, acc, accu);
         if constexpr (S::W8) acc *= so;
         publish_rows<RO, kSc1, kPW>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
                                     lo, tbuf, o_h1 + fo, S::H - fo, pad, true);
@@ -1543,10 +1630,10 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         sq = row_scale<Q.lpr>(nx.qkv_scale, S::QKV, c.gw, pq && more);
         so = row_scale<O.lpr>(nx.o_scale, S::H, c.gw, po && more);
       }
-      prefetch<Q.lpr, Q.nj, false, 0, S::EB>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      prefetch<Q.lpr, Q.nj, false, LQ, S::EB>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
       bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
-      prefetch<O.lpr, O.nj, false, OFF_O, S::EB>(pf, nx.o, S::H, S::AO, c.gw, po && more);
+      prefetch<O.lpr, O.nj, false, LO, S::EB>(pf, nx.o, S::H, S::AO, c.gw, po && more);
       // ---- h = h1 + down(act) from the MLP XCDs' partials, on the stager
       // waves of the workgroups without rows (an abandoned wait ends every
       // later wait of the launch through the error word) ----
@@ -1557,7 +1644,11 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     }
   } else {
     constexpr PhaseCfg G = S::xg;
-    constexpr int OFF_D = 2 * G.nj;
+    // slots: gate rows from 0, up rows, then the down chunks; W8 rows and
+    // chunks are loaded into the upper half of twice their slots and widened
+    constexpr int WG = S::W8 ? 2 : 1;
+    constexpr int OFF_U = WG * G.nj, OFF_D = 2 * WG * G.nj;
+    constexpr int LG = S::W8 ? G.nj : 0, LU = OFF_U + LG, LD = OFF_D + (S::W8 ? 4 * S::xkd : 0);
     const int xcd = c.wg % kXcds, jx = c.wg / kXcds;  // this XCD, and the index within it
     const bool is_g = rank < S::xng;
     const bool pg = is_g && !stager;
@@ -1573,8 +1664,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       }
     };
     scales_g(sm.layers[0], pg);
-    prefetch<G.lpr, G.nj, true, 0, S::EB>(pf, sm.layers[0].gate_up, S::I, S::H, c.gw, pg);
-    prefetch_down_x<S, OFF_D>(pf, sm.layers[0].down_x, c.gw, pg);
+    prefetch<G.lpr, G.nj, true, LG, S::EB, kNT, LU>(pf, sm.layers[0].gate_up, S::I, S::H, c.gw, pg);
+    prefetch_down_x<S, LD>(pf, sm.layers[0].down_x, c.gw, pg);
     for (int l = 0; l < L; ++l) {
       const PersistentLayer& lw = sm.layers[l];
       const unsigned ep = base + 5u * (unsigned)l;
@@ -1593,23 +1684,30 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         }
         if (l > 0) {
           scales_g(lw, pg);
-          prefetch<G.lpr, G.nj, true, 0, S::EB>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
-          prefetch_down_x<S, OFF_D>(pf, lw.down_x, c.gw, pg);
+          prefetch<G.lpr, G.nj, true, LG, S::EB, kNT, LU>(pf, lw.gate_up, S::I, S::H, c.gw, pg);
+          prefetch_down_x<S, LD>(pf, lw.down_x, c.gw, pg);
         }
       }
       // ---- gate/up + SwiGLU on h1 from XCD 0, then this wave's rows of down ----
       if (is_g) {
         bool ok = true;
+        if constexpr (S::W8) {  // before the wait, as on XCD 0
+          if (pg) {
+            widen_w8<0, G.nj>(pf);
+            widen_w8<OFF_U, G.nj>(pf);
+            widen_w8<OFF_D, 4 * S::xkd>(pf);
+          }
+        }
         if (stager) ok = stage_wave<S::H, true, false>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], nullptr);
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
         if (!stager) {
-          dot_group<G.lpr, G.nj, true, 0, S::EB>(pf, sm.xs[buf], S::H, acc, accu);
+          dot_group<G.lpr, G.nj, true, 0, S::EB, S::W8>(pf, sm.xs[buf], S::H, acc, accu);
           if constexpr (S::W8) {
             acc *= sg;
             accu *= su;
           }
-          down_partial<S, OFF_D>(pf, f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), sm.wsum[c.wave]);
+          down_partial<S, OFF_D, S::W8>(pf, f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), sm.wsum[c.wave]);
         }
         __syncthreads();
         // the workgroup's partial: thread t adds outputs 2t, 2t + 1 over the
@@ -1637,8 +1735,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       }
       if constexpr (!LONG) {
         scales_g(nx, pg && more);
-        prefetch<G.lpr, G.nj, true, 0, S::EB>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
-        prefetch_down_x<S, OFF_D>(pf, nx.down_x, c.gw, pg && more);
+        prefetch<G.lpr, G.nj, true, LG, S::EB, kNT, LU>(pf, nx.gate_up, S::I, S::H, c.gw, pg && more);
+        prefetch_down_x<S, LD>(pf, nx.down_x, c.gw, pg && more);
       }
     }
   }

@@ -407,6 +407,308 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
       }
 }
 
+// ---- slab GEMM: prompts of at most 64 tokens ----
+// One workgroup of 16 waves per slab of 16 outputs (and, for SwiGLU, the
+// matching up rows), over all of K: wave w takes K steps w, w + 16, ... (32
+// deep each) and the waves' sums are added in LDS in wave order, so there is
+// no workspace and no second pass, and every run gives the same result.  A
+// wave issues the weight and token loads of two steps before it waits for
+// any, and loads the next two while it multiplies (the weights are read once
+// from HBM, the token rows come from L2).  Every load goes through a buffer
+// resource, and a load that falls outside (a step the wave does not own, a
+// token or output row past the end) takes an offset past the resource and
+// reads zero: no branch around a load, so the compiler's wait counts stay
+// exact and the next batch stays in flight.  With RMSNorm gains the token
+// rows are normalised as they arrive: every lane adds the squares of its
+// fragments, the waves add theirs in LDS (every step belongs to exactly one
+// wave, so the sums cover each row once) and the fragments are scaled in
+// registers before their products; K is then at most 32 steps, one batch.
+// MFMA 16x16x32: A = 16 tokens x 32 k, B = 32 k x 16 outputs; lane L holds
+// token / output L % 16 and k 8 (L / 16) .. + 7 of each operand and, after
+// the product, tokens 4 (L / 16) .. + 3 of output L % 16.
+constexpr int kSlabBlocks = kSlabMaxTokens / 16;  // 16-token blocks at most
+constexpr int kSlabBatch = 2;                     // K steps per wave in flight together
+constexpr int kSlabLongWaves = 8;                 // waves of a long-K workgroup
+constexpr int kSlabWPre = 20;                     // its weight steps per wave requested at once
+constexpr unsigned kSlabOutside = 0x7ffffff0u;    // a byte offset past every resource
+
+// RMSNorm of eight bf16 inputs (one 16-byte fragment) with the token's
+// inverse rms and eight gains: bf16((x * inv) * gamma), the reference's order.
+__device__ __forceinline__ u32x4 norm8(u32x4 x, float inv, u32x4 g) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, gs[4] = {g.x, g.y, g.z, g.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = f32x2_to_bf16x2((bf_lo(xs[i]) * inv) * bf_lo(gs[i]), (bf_hi(xs[i]) * inv) * bf_hi(gs[i]));
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ float sq8(u32x4 x) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += bf_lo(xs[i]) * bf_lo(xs[i]);
+    s += bf_hi(xs[i]) * bf_hi(xs[i]);
+  }
+  return s;
+}
+
+// One batch of a wave's K steps: weight fragments (raw int8 for W8, widened
+// just before the product) and the token fragments of every block.
+template <bool PAIR, bool W8, int B>
+struct SlabBatch {
+  using WRaw = typename std::conditional<W8, u32x2_t, u32x4>::type;
+  WRaw w[B], u[PAIR ? B : 1];
+  u32x4 x[B][kSlabBlocks];
+};
+
+// WAVES 16 for K up to 16 batches of steps; WAVES kSlabLongWaves for longer
+// K (non-normalised A): each wave then requests the weights of up to
+// kSlabWPre of its steps at once (one HBM latency for all of them) and
+// streams the token fragments two steps at a time, double buffered.
+template <bool PAIR, bool NORM, bool W8, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a) {
+  constexpr int kSlabWaves = WAVES;
+  constexpr int P = PAIR ? 2 : 1;
+  constexpr int EB = W8 ? 1 : 2;  // bytes per weight
+  // SwiGLU pairs without the norm keep one step per batch (two batches of
+  // two would not fit the registers of 16 waves)
+  constexpr int B = PAIR && !NORM ? 1 : kSlabBatch;
+  using Batch = SlabBatch<PAIR, W8, B>;
+  __shared__ f32x4 red[kSlabWaves][P * kSlabBlocks][64];
+  __shared__ float ssq[NORM ? kSlabWaves : 1][kSlabMaxTokens];
+  __shared__ float inv_s[kSlabMaxTokens];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n0 = blockIdx.x * 16;
+  const int M = a.M, N = a.N, K = a.K;
+  const int mb = (M + 15) / 16;
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  const int steps = K / 32;
+  const int mine = steps > wave ? (steps - wave + kSlabWaves - 1) / kSlabWaves : 0;  // this wave's steps
+  // byte offsets of this lane's weight row (and up row) and token rows at k
+  // = fk; kSlabOutside for a row past the end
+  const int wrow = n0 + fr;
+  const unsigned wofs = wrow < N ? (unsigned)(wrow * K + fk) * EB : kSlabOutside;
+  const unsigned uofs = wrow < N ? (unsigned)((wrow + N) * K + fk) * EB : kSlabOutside;
+  unsigned aofs[kSlabBlocks];
+#pragma unroll
+  for (int b = 0; b < kSlabBlocks; ++b) {
+    const int t = 16 * b + fr;
+    aofs[b] = t < M ? (unsigned)(t * a.lda + fk) * 2u : kSlabOutside;
+  }
+  const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, P * N * K * EB);
+  const __amdgpu_buffer_rsrc_t ar = rsrc(a.A, ((M - 1) * a.lda + K) * 2);
+
+  // loads of the batch starting at this wave's step index j0 (nontemporal
+  // weights: each is read once)
+  auto load = [&](Batch& bt, int j0) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int j = j0 + i;
+      const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
+      const bool live = j < mine;
+      const unsigned wo = live ? wofs + k0 * EB : kSlabOutside;
+      if constexpr (W8) {
+        bt.w[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
+        if constexpr (PAIR)
+          bt.u[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                    wr, live ? uofs + k0 : kSlabOutside, 0, 2));
+      } else {
+        bt.w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2);
+        if constexpr (PAIR)
+          bt.u[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, live ? uofs + 2 * k0 : kSlabOutside, 0, 2);
+      }
+#pragma unroll
+      for (int b = 0; b < kSlabBlocks; ++b)
+        bt.x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, live ? aofs[b] + 2 * k0 : kSlabOutside, 0, 0);
+    }
+  };
+  auto widen = [&](const typename Batch::WRaw& r) -> bf16x8 {
+    if constexpr (W8)
+      return __builtin_bit_cast(bf16x8, (u32x4{i8pair_bf16(r.x, 0), i8pair_bf16(r.x, 2), i8pair_bf16(r.y, 0),
+                                              i8pair_bf16(r.y, 2)}));
+    else
+      return __builtin_bit_cast(bf16x8, r);
+  };
+
+  f32x4 acc[kSlabBlocks], accu[PAIR ? kSlabBlocks : 1];
+#pragma unroll
+  for (int b = 0; b < kSlabBlocks; ++b) {
+    acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (PAIR) accu[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto multiply = [&](const Batch& bt) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const bf16x8 w = widen(bt.w[i]);
+      const bf16x8 wu = PAIR ? widen(bt.u[i]) : w;
+#pragma unroll
+      for (int b = 0; b < kSlabBlocks; ++b) {  // blocks past the last token hold zeros
+        const bf16x8 xa = __builtin_bit_cast(bf16x8, bt.x[i][b]);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, w, acc[b], 0, 0, 0);
+        if constexpr (PAIR) accu[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wu, accu[b], 0, 0, 0);
+      }
+    }
+  };
+
+  if constexpr (NORM) {
+    // one batch holds every step of the wave (the host keeps K <= 32 steps)
+    Batch bt;
+    load(bt, 0);
+    u32x4 g[B];
+    const __amdgpu_buffer_rsrc_t gr = rsrc(a.gamma, K * 2);
+#pragma unroll
+    for (int i = 0; i < B; ++i)
+      g[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          gr, i < mine ? (unsigned)(32 * (wave + kSlabWaves * i) + fk) * 2u : kSlabOutside, 0, 0);
+    // squares of this lane's fragments, per token row; the four lanes of a
+    // row hold its four 8-wide k groups
+#pragma unroll
+    for (int b = 0; b < kSlabBlocks; ++b) {
+      float sq = 0.0f;
+#pragma unroll
+      for (int i = 0; i < B; ++i) sq += sq8(bt.x[i][b]);
+      sq += __shfl_xor(sq, 16, 64);
+      sq += __shfl_xor(sq, 32, 64);
+      if (lane < 16) ssq[wave][16 * b + fr] = sq;
+    }
+    __syncthreads();
+    if (tid < kSlabMaxTokens) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kSlabWaves; ++w) ss += ssq[w][tid];
+      inv_s[tid] = tid < M ? 1.0f / sqrtf(ss / (float)K + a.eps) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < kSlabBlocks; ++b) {
+      const float inv = inv_s[16 * b + fr];
+#pragma unroll
+      for (int i = 0; i < B; ++i) bt.x[i][b] = norm8(bt.x[i][b], inv, g[i]);
+    }
+    multiply(bt);
+  } else if (steps <= kSlabWaves * B) {
+    // every step of the wave in one batch
+    Batch bt;
+    load(bt, 0);
+    multiply(bt);
+  } else if constexpr (!PAIR && WAVES != kSlabLongWaves) {
+    // (long K runs on kSlabLongWaves waves; this form stays correct for any K)
+    for (int j = 0; j < mine; j += B) {
+      Batch bt;
+      load(bt, j);
+      multiply(bt);
+    }
+  } else if constexpr (PAIR) {
+    // two batches in flight: the next one loads while this one multiplies
+    // (unconditionally: steps past the wave's last read zero and add zero;
+    // sched_barrier keeps the next batch's loads ahead of the products)
+    Batch b0, b1;
+    load(b0, 0);
+    for (int j = 0; j < mine; j += 2 * B) {
+      load(b1, j + B);
+      __builtin_amdgcn_sched_barrier(0);
+      multiply(b0);
+      load(b0, j + 2 * B);
+      __builtin_amdgcn_sched_barrier(0);
+      multiply(b1);
+    }
+  } else {
+    // long K: the weights of kSlabWPre steps at once, token fragments two
+    // steps at a time in two buffers (sched_barrier keeps the next buffer's
+    // loads ahead of this one's products; steps past the wave's last read
+    // zero and add zero)
+    using WRaw = typename Batch::WRaw;
+    for (int g0 = 0; g0 < mine; g0 += kSlabWPre) {
+      WRaw wv[kSlabWPre];
+#pragma unroll
+      for (int i = 0; i < kSlabWPre; ++i) {
+        const int j = g0 + i;
+        const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
+        const unsigned wo = j < mine ? wofs + k0 * EB : kSlabOutside;
+        if constexpr (W8)
+          wv[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
+        else
+          wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2);
+      }
+      u32x4 x0[2][kSlabBlocks], x1[2][kSlabBlocks];
+      auto load_x = [&](u32x4 (&x)[2][kSlabBlocks], int j0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int j = j0 + i;
+          const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
+#pragma unroll
+          for (int b = 0; b < kSlabBlocks; ++b)
+            x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, j < mine ? aofs[b] + 2 * k0 : kSlabOutside, 0, 0);
+        }
+      };
+      auto mul_x = [&](const u32x4 (&x)[2][kSlabBlocks], int i0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const bf16x8 w = widen(wv[i0 + i]);
+#pragma unroll
+          for (int b = 0; b < kSlabBlocks; ++b)
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x[i][b]), w, acc[b], 0, 0, 0);
+        }
+      };
+      load_x(x0, g0);
+#pragma unroll
+      for (int i = 0; i < kSlabWPre; i += 4) {
+        load_x(x1, g0 + i + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        mul_x(x0, i);
+        if (i + 4 < kSlabWPre) load_x(x0, g0 + i + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        mul_x(x1, i + 2);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int b = 0; b < kSlabBlocks; ++b) {
+    red[wave][b][lane] = acc[b];
+    if constexpr (PAIR) red[wave][kSlabBlocks + b][lane] = accu[b];
+  }
+  __syncthreads();
+
+  // values f = t, t + 64 WAVES, ... of [mb][64 lanes][4 rows] on thread t,
+  // each summed over the waves in wave order, then the epilogue (the
+  // rounding points of the other GEMM kernels)
+  for (int f = tid; f < mb * 256; f += kSlabWaves * 64) {
+    const int b = f >> 8, l = (f >> 2) & 63, r = f & 3;
+    const int m = 16 * b + 4 * (l >> 4) + r, n = n0 + (l & 15);
+    if (m >= M || n >= N) continue;
+    float x = 0.0f, u = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSlabWaves; ++w) {
+      x += red[w][b][l][r];
+      if constexpr (PAIR) u += red[w][kSlabBlocks + b][l][r];
+    }
+    if constexpr (W8) {
+      x *= a.scale[n];
+      if constexpr (PAIR) u *= a.scale[N + n];
+    }
+    uint16_t* y = a.Y + (size_t)m * a.ldy + n;
+    switch (a.epi) {
+      case EPI_BF16:
+        *y = (uint16_t)f32_to_bf16(x);
+        break;
+      case EPI_BIAS:
+        *y = (uint16_t)f32_to_bf16(round_bf16(x) + a.bias[n]);
+        break;
+      case EPI_RESID:
+        *y = (uint16_t)f32_to_bf16(round_bf16(x) + bf16_to_f32(a.resid[(size_t)m * a.ldr + n]));
+        break;
+      case EPI_SWIGLU:
+        if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(x), round_bf16(u)));
+        break;
+      default:
+        break;
+    }
+  }
+}
+
 // Sum of the split-K partial sums of output (m, n) in slice order, then the
 // epilogue of the GEMM (the same rounding points as gemm_big_kernel's).
 __global__ __launch_bounds__(kThreads) void split_reduce_kernel(PrefillGemmArgs a, int parts) {
@@ -641,8 +943,33 @@ size_t split_ws_need(int M, int N, int K, bool pair) {
 }
 
 namespace {
+template <bool PAIR, bool W8>
+int launch_slab(const PrefillGemmArgs& a, hipStream_t stream) {
+  const dim3 grid((a.N + 15) / 16);
+  const bool long_k = a.K / 32 > 16 * kSlabBatch;
+  if (a.gamma)
+    hipLaunchKernelGGL((gemm_slab_kernel<PAIR, true, W8, 16>), grid, dim3(16 * 64), 0, stream, a);
+  else if constexpr (!PAIR) {
+    if (long_k)
+      hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, kSlabLongWaves>), grid, dim3(kSlabLongWaves * 64), 0,
+                         stream, a);
+    else
+      hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, 16>), grid, dim3(16 * 64), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((gemm_slab_kernel<true, false, W8, 16>), grid, dim3(16 * 64), 0, stream, a);
+  }
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "slab gemm launch");
+}
+
 template <bool W8>
 int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
+  const bool pair = a.epi == EPI_SWIGLU;
+  if (a.grp_count == nullptr && a.M <= kSlabMaxTokens) {
+    if (a.gamma && a.K > kSlabNormMaxK) return fail("slab gemm: a normalised A operand needs K <= 1024");
+    return pair ? launch_slab<true, W8>(a, stream) : launch_slab<false, W8>(a, stream);
+  }
+  if (a.gamma) return fail("prefill gemm: a normalised A operand needs the slab path (M <= 64)");
   dim3 grid((a.N + kTN - 1) / kTN, (a.M + kTM - 1) / kTM);
   if (a.grp_count != nullptr) {
     if (a.max_groups <= 0 || a.max_rows <= 0 || a.n_groups == nullptr || a.grp_expert == nullptr ||
@@ -651,7 +978,6 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     grid.y = (a.max_rows + kTM - 1) / kTM;
     grid.z = a.max_groups;
   }
-  const bool pair = a.epi == EPI_SWIGLU;
   if (a.grp_count == nullptr && a.split_ws != nullptr && a.K % kBK == 0 && split_parts(a.M, a.N, a.K) > 1 &&
       split_ws_need(a.M, a.N, a.K, pair) <= a.split_ws_floats) {
     // too few tiles to fill the GPU: K split over ~kSplitTarget workgroups

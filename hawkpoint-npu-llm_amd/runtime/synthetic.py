@@ -16,7 +16,12 @@ writes (``npu_llm/tools/convert_smollm2.py:220-311``):
 - ``lm_head``                     tied: the embedding
 
 Weights are N(0, 0.02) float32 samples rounded to bf16; RMSNorm gains are
-1.0; the qkv bias is N(0, 0.02) float32 when the shape has one.  W8 tensors
+1.0, or with ``norm_gains=g`` bf16 samples of U(0.5, 1.5) for the layer norms
+and of g * U(0.5, 1.5) for the final norm, drawn from a generator of their
+own (seed + 7919) so the weights stay those of the same seed; a final gain
+of about 8 spreads the logits of these random weights like a trained
+model's (standard deviation of a few units instead of about 0.5); the qkv
+bias is N(0, 0.02) float32 when the shape has one.  W8 tensors
 are the per-output-row int8 quantisation of the bf16 weights
 (``convert_smollm2.py:81-86``), computed lazily.
 
@@ -82,7 +87,7 @@ class QuantizedWeights:
 class SyntheticModel:
     """Random-init model of a given shape; see the module docstring."""
 
-    def __init__(self, shape, seed=0, *, layers=None, std=0.02):
+    def __init__(self, shape, seed=0, *, layers=None, std=0.02, norm_gains=None):
         shape = dict(shape)
         if layers is not None:
             shape["layers"] = int(layers)
@@ -135,6 +140,13 @@ class SyntheticModel:
                 self.tensors[f"{p}.{g}"] = {"shape": [h], "dtype": "bfloat16"}
         self._bits["final_norm"] = ones
         self.tensors["final_norm"] = {"shape": [h], "dtype": "bfloat16"}
+        if norm_gains is not None:
+            gain_rng = np.random.default_rng(self.seed + 7919)
+            for layer in range(shape["layers"]):
+                for g in ("input_norm", "post_attn_norm"):
+                    self._bits[f"layer{layer:02d}.{g}"] = to_bits(gain_rng.uniform(0.5, 1.5, h).astype(np.float32))
+            final = np.float32(norm_gains) * gain_rng.uniform(0.5, 1.5, h).astype(np.float32)
+            self._bits["final_norm"] = to_bits(final)
         self._bits["lm_head"] = self._bits["token_embedding"]
         self.tensors["lm_head"] = {"shape": [vocab, h], "bf16_file": "tied"}
 

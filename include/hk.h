@@ -154,7 +154,9 @@ int hk_engine_launch_part(hk_engine* engine, int32_t part, int32_t layer);
 /* Enqueue `count` launches of one part, layer i % layers for launch i, as one
  * hipGraph (captured on first use per (part, count)), so host launch cost does
  * not pace the GPU when the launches are timed with events.  HK_PART_STEP
- * repeats the whole step at the last token/position, without token feedback. */
+ * repeats the whole step at the last token/position, without token feedback;
+ * a persistent step (one launch per step) is enqueued directly, without a
+ * graph. */
 int hk_engine_launch_part_repeat(hk_engine* engine, int32_t part, int32_t count);
 
 /* Enqueue `count` GEMVs y = W_i @ x, W_i = weights[i % n_weights] (bf16, or

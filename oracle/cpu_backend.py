@@ -21,6 +21,7 @@ generate.py:709-730 argmax       ``decode_result``
 generate.py:830-846 CPU step     ``OracleDecoder.decode_token``
 generate.py:1110-1158 loop       ``OracleDecoder.generate_greedy``
 generate.py:1110-1125 prefill    ``OracleDecoder.prefill`` (rows at once)
+validate_engine_npu.py:58-64     ``OracleDecoder.teacher_forced`` (rows at once)
 ===============================  =========================================
 
 BF16 tensors are carried as uint16 bit patterns because ``ml_dtypes`` is not
@@ -265,6 +266,14 @@ class CPUDecoderStage:
             self._lm_head_f32 = from_bits(self.weight("lm_head"))
         return self._lm_head_f32 @ round_f32(normalized)
 
+    def logits_rows(self, hidden_rows):
+        """``logits`` of every row of ``hidden_rows`` [n, H] as one product;
+        returns [n, vocab]."""
+        normalized = self.norm_rows(hidden_rows, "final_norm")
+        if self._lm_head_f32 is None:
+            self._lm_head_f32 = from_bits(self.weight("lm_head"))
+        return (self._lm_head_f32 @ normalized.T).T
+
     def reset(self):
         for cache in self.key_cache.values():
             cache.fill(0)
@@ -338,6 +347,22 @@ class OracleDecoder:
             return None, None
         logits = self.stage.logits(hidden[-1])
         return decode_result(logits), logits
+
+    def teacher_forced(self, token_ids, start=0):
+        """Logits at every position of ``token_ids`` fed from slot ``start``,
+        as the reference's gate collects them by decoding the tokens one by
+        one (npu_llm/tests/validate_engine_npu.py:58-64); here every row of
+        ``prefill`` goes through the final norm and the LM head.  Returns an
+        ``(n, vocab)`` float32 array."""
+        ids = [int(t) for t in token_ids]
+        if not ids:
+            raise ValueError("teacher forcing needs at least one token")
+        if start < 0 or start + len(ids) > self.context_length:
+            raise ValueError("position outside the context")
+        hidden = round_f32(self._embedding[np.asarray(ids)])
+        for layer in range(self.layers):
+            hidden = self.stage.layer_rows(hidden, layer, start)
+        return np.ascontiguousarray(self.stage.logits_rows(hidden), dtype=np.float32)
 
     def generate_greedy(self, prompt_ids, new_tokens, *, keep_logits=True, timings=None):
         """Per-position prefill (logits at the last prompt position only),

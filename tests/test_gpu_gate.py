@@ -1,0 +1,112 @@
+"""The reference's multi-prompt agreement gate on the GPU engine
+(npu_llm/tests/validate_engine_npu.py:23-131).
+
+The reference's gate: six chat prompts (its PROMPTS, kept here), each
+encoded with the ChatML template and cut to its last 64 - 31 tokens, are
+continued greedily by the CPU reference to 63 tokens; the engine is then
+teacher-forced on each sequence and its argmax compared with the reference's
+at every position.  A position where they differ is a hard miss unless the
+reference's top-2 logit gap is below 0.5.  The engine must reach the
+chunked (per-layer) path's top-1 count within 6 and have at most one hard
+miss more than it.
+
+Here the CPU reference is the oracle, the chunked path is the per-kernel
+step (HK_PERSISTENT=0: one kernel per part, as the reference's chunked
+layer graphs run one part at a time) and the engine is the persistent step
+the engine picks by default.  The prompts are encoded with the synthetic
+byte-level ChatML tokenizer (no trained tokenizer is available), and the
+weights are random, so the final RMSNorm gain is set to about 8: the logits
+then spread like a trained model's (standard deviation near 4) and a 0.5 gap
+is as strict as it is on the reference's model; with unit gains nearly every
+position would be a near-tie.  On top of the reference's relative bar, both
+paths must have no hard miss at all.
+"""
+
+import numpy as np
+import pytest
+
+from _util import announce
+from oracle.cpu_backend import OracleDecoder, decode_result
+from runtime.synthetic import QWEN25_05B, SMOLLM2_135M, SyntheticModel
+
+pytestmark = pytest.mark.gpu
+
+PROMPTS = [
+    "Explain in simple terms why the sky looks blue during the day. Give a detailed answer.",
+    "Write a haiku about the ocean.",
+    "What is 12 times 7?",
+    "Merhaba! Bugün nasılsın?",
+    "List three uses of copper.",
+    "Translate 'good morning' into French and Spanish.",
+]
+NEAR_TIE = 0.5
+TOKENS = 31
+TOLERANCE = 6
+CONTEXT = 64
+
+
+def _sequences(model, oracle, tmp_path):
+    """The oracle's greedy continuations of the six prompts, cut to 63
+    tokens, and its teacher-forced logits on each."""
+    from runtime.generate import default_system_prompt
+    from runtime.tokenizer import SmolLMTokenizer, write_chatml_tokenizer
+
+    folder = write_chatml_tokenizer(tmp_path / "tokenizer", model.metadata["vocab_size"])
+    tokenizer = SmolLMTokenizer(folder, default_system=default_system_prompt(model.metadata["model_family"]))
+    sequences, references = [], []
+    for prompt in PROMPTS:
+        ids = tokenizer.encode_chat([{"role": "user", "content": prompt}])[-(CONTEXT - TOKENS):]
+        first, _ = oracle.prefill(ids)
+        sequence = list(ids) + [first]
+        while len(sequence) < len(ids) + TOKENS:
+            token, _ = oracle.decode_token(sequence[-1], len(sequence) - 1)
+            sequence.append(token)
+        sequence = sequence[:CONTEXT - 1]
+        sequences.append(sequence)
+        references.append([decode_result(row, diagnostics=True)[1] for row in oracle.teacher_forced(sequence)])
+    return sequences, references
+
+
+def _agreement(model, w8, sequences, references):
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    engine = QwenDecoderEngine(model, context_length=CONTEXT, w8=w8)
+    exact = total = 0
+    hard = []
+    try:
+        kind = engine.step_kind(CONTEXT - 2)
+        for index, sequence in enumerate(sequences):
+            engine.reset()
+            for position, token in enumerate(sequence):
+                _, logits = engine.step_token(token, position, logits=True)
+                want = references[index][position]
+                total += 1
+                if int(np.argmax(logits)) == want["top_token_ids"][0]:
+                    exact += 1
+                elif want["top_logit_margin"] >= NEAR_TIE:
+                    hard.append((index, position, round(want["top_logit_margin"], 3)))
+    finally:
+        engine.close()
+    return kind, exact, total, hard
+
+
+@pytest.mark.parametrize("family,w8", [("smollm", True), ("smollm", False), ("qwen", False), ("qwen", True)],
+                         ids=["smollm2-135m-w8", "smollm2-135m-bf16", "qwen2.5-0.5b-bf16", "qwen2.5-0.5b-w8"])
+def test_six_prompt_agreement_gate(family, w8, monkeypatch, tmp_path):
+    shape = SMOLLM2_135M if family == "smollm" else QWEN25_05B
+    model = SyntheticModel(shape, seed=0, norm_gains=8.0)
+    announce(f"six-prompt gate {family} w8={w8}: oracle sequences")
+    sequences, references = _sequences(model, OracleDecoder(model, CONTEXT, w8=w8), tmp_path)
+    margins = np.array([r["top_logit_margin"] for ref in references for r in ref])
+    announce(f"  {len(margins)} positions, oracle top-2 gap median {np.median(margins):.3f}, "
+             f"{(margins < NEAR_TIE).mean():.0%} below {NEAR_TIE}")
+    monkeypatch.setenv("HK_PERSISTENT", "0")
+    chunked = _agreement(model, w8, sequences, references)
+    monkeypatch.delenv("HK_PERSISTENT")
+    engine = _agreement(model, w8, sequences, references)
+    for name, (kind, exact, total, hard) in (("per-kernel", chunked), ("engine", engine)):
+        announce(f"  {name} ({kind}): top-1 {exact}/{total}, hard misses {hard}")
+    assert chunked[0] != engine[0], "the two runs took the same step form"
+    assert engine[1] + TOLERANCE >= chunked[1]
+    assert len(engine[3]) <= len(chunked[3]) + 1
+    assert not engine[3] and not chunked[3]

@@ -168,10 +168,42 @@ def test_prefill_continues_from_cached_prefix():
         engine.close()
 
 
+@pytest.mark.parametrize("n,w8", [(1, False), (16, False), (17, False), (63, False), (64, False), (65, False),
+                                  (130, False), (1, True), (64, True)])
+def test_prefill_lengths_around_the_slab_gemm(n, w8):
+    """Chunks of up to 64 tokens run the slab GEMMs (one workgroup per 16
+    outputs over all of K, RMSNorm applied while loading A); 65 and more take
+    the tiled GEMMs.  Last-token logits and KV slots of a 2-layer
+    Qwen2.5-0.5B-shape model with random RMSNorm gains against the oracle's
+    prefill at each length."""
+    from runtime.qwen_engine import QwenDecoderEngine
+    from test_gpu_engine import _check_kv_slot
+
+    announce(f"prefill length {n} w8={w8}")
+    model = SyntheticModel(QWEN25_05B, seed=40 + n, layers=2, norm_gains=1.0)
+    prompt = _prompt(151936, n, 60 + n)
+    oracle = OracleDecoder(model, 256, w8=w8)
+    ref_tok, ref = oracle.prefill(prompt)
+    engine = QwenDecoderEngine(model, context_length=256, w8=w8)
+    try:
+        tok, logits = engine.prefill(prompt, 0)
+        err = rel_l2(logits, ref)
+        announce(f"  rel-L2 {err:.3e}, token {tok} oracle {ref_tok}")
+        assert err <= 1e-2
+        assert tok == ref_tok or near_tie(ref)
+        for layer in (0, 1):
+            for slot in sorted({0, n // 2, n - 1}):
+                _check_kv_slot(engine, oracle.stage, layer, slot, 2e-2)
+            k, v = engine.read_kv(layer, n)
+            assert np.all(k == 0) and np.all(v == 0)
+    finally:
+        engine.close()
+
+
 def test_prefill_w8_qwen_4_layer():
     """W8 prefill on the MFMA GEMMs: int8 weight tiles converted exactly to
     bf16 on load, the row scale applied to the finished sums (40 tokens: the
-    split-K GEMM and its reduce)."""
+    slab GEMM)."""
     model = SyntheticModel(QWEN25_05B, seed=3, layers=4)
     _prefill_case(model, _prompt(151936, 40, 16), 8, 72, 1e-2, "qwen-4L-w8", w8=True)
 

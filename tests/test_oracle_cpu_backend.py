@@ -433,3 +433,38 @@ def test_w8_stage_branch_is_project_w8():
     x = bf16.round_f32(rng.normal(size=TINY["hidden_size"]).astype(np.float32))
     np.testing.assert_array_equal(stage.project("lm_head", x),
                                   CPUDecoderStage(model, 0, 8).project("lm_head", x))
+
+
+def test_teacher_forced_rows_match_per_position_logits_with_random_gains():
+    """``teacher_forced`` (every row of a batched prefill through the final
+    norm and LM head) gives the per-position decode's logits at every
+    position up to float32 summation order, and tracks the float64 model,
+    on a model whose RMSNorm gains are random (layer gains U(0.5, 1.5), final
+    gains 8 U(0.5, 1.5)) so a gain applied wrongly or not at all shows."""
+    model = SyntheticModel(TINY, seed=6, std=0.15, norm_gains=8.0)
+    assert not np.all(model.raw_f32("layer00.input_norm") == 1.0)
+    rng = np.random.default_rng(23)
+    tokens = [int(t) for t in rng.integers(0, TINY["vocab_size"], 9)]
+    rows = OracleDecoder(model, 12).teacher_forced(tokens)
+    assert rows.shape == (9, TINY["vocab_size"]) and rows.dtype == np.float32
+    dec = OracleDecoder(model, 12)
+    for pos, tok in enumerate(tokens):
+        _, lg = dec.decode_token(tok, pos)
+        assert np.linalg.norm(rows[pos] - lg) / np.linalg.norm(lg) < 1e-3, pos
+    ref = _f64_model_logits(model, tokens, set(range(9)))
+    for pos in ref:
+        assert np.linalg.norm(rows[pos] - ref[pos]) / np.linalg.norm(ref[pos]) < 2e-2, pos
+    # the same weights with unit gains are far away: the gains are in use
+    plain = _f64_model_logits(SyntheticModel(TINY, seed=6, std=0.15), tokens, {8})[8]
+    assert np.linalg.norm(rows[8] - plain) / np.linalg.norm(ref[8]) > 0.2
+
+
+def test_norm_gains_leave_the_weights_of_the_seed():
+    a = SyntheticModel(TINY, seed=2)
+    b = SyntheticModel(TINY, seed=2, norm_gains=8.0)
+    for name in ("token_embedding", "layer01.gate_up", "layer00.qkv"):
+        np.testing.assert_array_equal(a.raw(name), b.raw(name))
+    final = b.raw_f32("final_norm")
+    assert final.min() >= 4.0 and final.max() <= 12.0
+    gains = b.raw_f32("layer01.post_attn_norm")
+    assert gains.min() >= 0.5 and gains.max() <= 1.5 and np.std(gains) > 0.1
