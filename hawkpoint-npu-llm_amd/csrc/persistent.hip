@@ -131,39 +131,53 @@ __device__ __forceinline__ unsigned long long ld_p64(__amdgpu_buffer_rsrc_t r, u
 // for ds_bpermute (what __shfl_xor compiles to).  Steps: swap neighbours
 // (quad_perm 1,0,3,2), swap pairs (2,3,0,1), then pair quads (half-row mirror)
 // and halves (row mirror); each step adds lanes holding equal partial sums,
-// so every lane of the group ends with the same total.  Rows are joined with
-// two shuffles.
+// so every lane of the group ends with the same total.  Across rows,
+// row_bcast15 adds row 0 to row 1 and row 2 to row 3, row_bcast31 then adds
+// rows 0 + 1 to row 3, and v_readlane hands lane 63's total to the whole wave
+// (the same value in every lane).  Checked on the device against shuffle
+// butterflies: equal groups, equal maxima, sums within float rounding.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xf, false));
+}
 template <int CTRL>
 __device__ __forceinline__ float dpp_plus(float v) {
-  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
-  return v + __builtin_bit_cast(float, moved);
+  return v + dpp_mov<CTRL>(v);
+}
+__device__ __forceinline__ float lane63(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// sum over each group of 8 lanes, in all 8
+__device__ __forceinline__ float group_sum8(float v) {
+  v = dpp_plus<0xb1>(v);   // quad_perm 1,0,3,2
+  v = dpp_plus<0x4e>(v);   // quad_perm 2,3,0,1
+  return dpp_plus<0x141>(v);  // row_half_mirror
 }
 
 template <int W>
 __device__ __forceinline__ float wave_sum(float v) {
-  static_assert(W == 16 || W == 32 || W == 64, "row-multiple widths only");
+  static_assert(W == 16 || W == 64, "a row or the whole wave");
   v = dpp_plus<0xb1>(v);   // quad_perm 1,0,3,2
   v = dpp_plus<0x4e>(v);   // quad_perm 2,3,0,1
   v = dpp_plus<0x141>(v);  // row_half_mirror
   v = dpp_plus<0x140>(v);  // row_mirror
-  if (W >= 32) v += __shfl_xor(v, 16, 64);
-  if (W >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (W == 64) {
+    v = v + dpp_mov<0x142, 0xa>(v);  // row_bcast15 into rows 1 and 3
+    v = v + dpp_mov<0x143, 0x8>(v);  // row_bcast31 into row 3
+    v = lane63(v);
+  }
   return v;
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_max(float v) {
-  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
-  return fmaxf(v, __builtin_bit_cast(float, moved));
-}
-
 __device__ __forceinline__ float wave_max64(float v) {
-  v = dpp_max<0xb1>(v);
-  v = dpp_max<0x4e>(v);
-  v = dpp_max<0x141>(v);
-  v = dpp_max<0x140>(v);
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  v = fmaxf(v, dpp_mov<0xb1>(v));
+  v = fmaxf(v, dpp_mov<0x4e>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  v = fmaxf(v, dpp_mov<0x142, 0xa>(v));
+  v = fmaxf(v, dpp_mov<0x143, 0x8>(v));
+  return lane63(v);
 }
 
 // ---- phase shapes ----
@@ -636,9 +650,12 @@ __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t
         if constexpr (PAIR) fma16_i8(pf[OFF + NJ + j], xv[j][0], xv[j][1], b0, b1);
       }
     }
-    if constexpr (LPR >= 16) {
+    if constexpr (LPR == 16 || LPR == 64) {
       acc = wave_sum<LPR>(a0 + a1);
       accu = PAIR ? wave_sum<LPR>(b0 + b1) : 0.0f;
+    } else if constexpr (LPR == 8) {
+      acc = group_sum8(a0 + a1);
+      accu = PAIR ? group_sum8(b0 + b1) : 0.0f;
     } else {
       acc = group_sum<LPR>(a0 + a1);
       accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
@@ -660,9 +677,12 @@ __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t
     fma8(pf[OFF + j], xv[j], a0, a1);
     if constexpr (PAIR) fma8(pf[OFF + NJ + j], xv[j], b0, b1);
   }
-  if constexpr (LPR >= 16) {
+  if constexpr (LPR == 16 || LPR == 64) {
     acc = wave_sum<LPR>(a0 + a1);
     accu = PAIR ? wave_sum<LPR>(b0 + b1) : 0.0f;
+  } else if constexpr (LPR == 8) {
+    acc = group_sum8(a0 + a1);
+    accu = PAIR ? group_sum8(b0 + b1) : 0.0f;
   } else {
     acc = group_sum<LPR>(a0 + a1);
     accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
@@ -796,7 +816,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     }
     dot = d0 + d1;
   }
-  dot += __shfl_xor(dot, 1, 64);  // the two halves of the slot
+  dot = dpp_plus<0xb1>(dot);  // the two halves of the slot (neighbouring lanes)
   const bool live = si < n;
   const float sc = live ? dot * scale : -INFINITY;
   // Softmax and P @ V per wave, flash-style: a wave's 32 slots are exactly
@@ -1307,8 +1327,8 @@ template <class S, int OFF, bool WIDE = false>
 __device__ __forceinline__ void down_partial(const u32x4 (&pf)[kPf], uint32_t act, float* ws) {
   constexpr int CC = S::xdc;
   const int lane = threadIdx.x & 63;
-  const uint32_t a0 = __shfl(act, 0, 64), a1 = __shfl(act, 16, 64);
-  const uint32_t a2 = __shfl(act, 32, 64), a3 = __shfl(act, 48, 64);
+  const uint32_t a0 = __builtin_amdgcn_readlane(act, 0), a1 = __builtin_amdgcn_readlane(act, 16);
+  const uint32_t a2 = __builtin_amdgcn_readlane(act, 32), a3 = __builtin_amdgcn_readlane(act, 48);
   const uint32_t A01 = (a0 & 0xffffu) | (a1 << 16), A23 = (a2 & 0xffffu) | (a3 << 16);
   if constexpr (S::W8 && WIDE) {
     // widened chunks (widen_w8): slot q of chunk k holds outputs 2q, 2q + 1
