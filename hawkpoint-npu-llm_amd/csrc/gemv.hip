@@ -30,6 +30,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
+constexpr unsigned kGemvOutside = 0x7ffffff0u;  // a byte offset past every buffer resource
 
 // Stage x (optionally RMS-normalised) into LDS as float32.
 // RMSNorm follows cpu_backend.py:71-76: v = f32(bf16 x); mean of v*v in f32;
@@ -175,26 +176,54 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   u32x4 wa[NJ], wb[NJ];
   u32x4 ua[PAIR ? NJ : 1], ub[PAIR ? NJ : 1];
 
+  // Branch-free loads through a buffer resource: a chunk past the row or a
+  // group past the matrix takes an offset past the resource and reads zero.
+  // With a branch around each load the compiler waited for all of them
+  // (the next group's too) before the first product.  The host keeps the
+  // matrix below 2 GiB (32-bit offsets).
+  const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, (int)((PAIR ? 2 : 1) * pair_off));
+  // (int8 rows keep the branches: measured, the branch-free form took their
+  // GEMVs 10-25% longer)
   auto load = [&](int g, int base, u32x4 (&w)[NJ], u32x4 (&u)[PAIR ? NJ : 1]) {
     const int row = g * RPW + sub;
     const bool live = g < groups && row < a.M;
-    const char* wrow = static_cast<const char*>(a.W) + (size_t)(live ? row : 0) * row_bytes;
+    if constexpr (W8) {
+      const char* wrow = static_cast<const char*>(a.W) + (size_t)(live ? row : 0) * row_bytes;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int c = base + l + j * LPR;
-      const bool ok = live && c < CH;
-      w[j] = ok ? load_stream16(wrow + (size_t)c * 16) : zero;
-      if constexpr (PAIR) u[j] = ok ? load_stream16(wrow + pair_off + (size_t)c * 16) : zero;
+      for (int j = 0; j < NJ; ++j) {
+        const int c = base + l + j * LPR;
+        const bool ok = live && c < CH;
+        w[j] = ok ? load_stream16(wrow + (size_t)c * 16) : zero;
+        if constexpr (PAIR) u[j] = ok ? load_stream16(wrow + pair_off + (size_t)c * 16) : zero;
+      }
+    } else {
+      const unsigned rofs = (unsigned)((size_t)(live ? row : 0) * row_bytes);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int c = base + l + j * LPR;
+        const unsigned off = live && c < CH ? rofs + (unsigned)c * 16u : kGemvOutside;
+        w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2);
+        if constexpr (PAIR)
+          u[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, off == kGemvOutside ? off : off + (unsigned)pair_off, 0, 2);
+      }
     }
   };
+  // bf16: chunks past the row hold zero weights and their x index is
+  // clamped, so the products read a finite x and need no branch
   auto dot = [&](int base, const u32x4 (&w)[NJ], const u32x4 (&u)[PAIR ? NJ : 1], float& a0,
                  float& a1, float& b0, float& b1) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int c = base + l + j * LPR;
-      if (c < CH) {
-        fma_chunk<W8>(w[j], xs, c, a0, a1);
-        if constexpr (PAIR) fma_chunk<W8>(u[j], xs, c, b0, b1);
+      if constexpr (W8) {
+        if (c < CH) {
+          fma_chunk<W8>(w[j], xs, c, a0, a1);
+          if constexpr (PAIR) fma_chunk<W8>(u[j], xs, c, b0, b1);
+        }
+      } else {
+        const int cx = c < CH ? c : 0;
+        fma_chunk<W8>(w[j], xs, cx, a0, a1);
+        if constexpr (PAIR) fma_chunk<W8>(u[j], xs, cx, b0, b1);
       }
     }
   };
@@ -425,12 +454,35 @@ int blocks_for(int groups) {
   return needed < cap ? needed : cap;
 }
 
+// Workgroups of gemv_kernel<...> that stay resident on one CU with `lds`
+// bytes of LDS each (registers limit most forms to three: a grid of four per
+// CU would leave a quarter of the workgroups to start after the others and
+// run the tail alone).  Cached per form for the last LDS size asked.
+template <int LPR, int NJ, bool W8, bool PAIR>
+int resident_per_cu(size_t lds) {
+  static size_t cached_lds = 0;
+  static int cached = 0;
+  if (cached == 0 || cached_lds != lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel<LPR, NJ, W8, PAIR>, kThreads, lds) !=
+            hipSuccess ||
+        n <= 0)
+      n = 1;
+    cached = n < 4 ? n : 4;
+    cached_lds = lds;
+  }
+  return cached;
+}
+
 template <int LPR, int NJ, bool W8, bool PAIR>
 int launch_cfg(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
   constexpr int RPW = 64 / LPR;
-  const int blocks = blocks_for((a.M + RPW - 1) / RPW);
-  if (blocks_out) *blocks_out = blocks;
   const size_t lds = (size_t)(a.K + 8) * sizeof(float);
+  const int needed = ((a.M + RPW - 1) / RPW + kWaves - 1) / kWaves;
+  int cap = cu_count() * resident_per_cu<LPR, NJ, W8, PAIR>(lds);
+  if (cap > kMaxPartialKeys) cap = kMaxPartialKeys;
+  const int blocks = needed < cap ? needed : cap;
+  if (blocks_out) *blocks_out = blocks;
   hipLaunchKernelGGL((gemv_kernel<LPR, NJ, W8, PAIR>), dim3(blocks), dim3(kThreads), lds, stream,
                      a);
   const hipError_t err = hipGetLastError();
@@ -544,23 +596,14 @@ int launch_xreg(const XregPlan& p, const GemvArgs& a, hipStream_t stream, int* b
 
 }  // namespace
 
-int gemv_blocks(const GemvArgs& a, bool w8) {
-  XregPlan plan;
-  if (xreg_plan(a, w8, &plan)) {
-    const int rpw = 64 / plan.lpr;
-    return blocks_for((a.M + rpw - 1) / rpw);
-  }
-  const int CH = w8 ? a.K / 16 : a.K / 8;
-  const int rpw = 64 / pick_lpr(CH);
-  return blocks_for((a.M + rpw - 1) / rpw);
-}
-
 int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out) {
   if (a.M <= 0 || a.K <= 0) return fail("gemv: M and K must be positive");
   if (a.K % (w8 ? 16 : 8) != 0)
     return fail(w8 ? "gemv: K must be a multiple of 16 for int8 weights"
                    : "gemv: K must be a multiple of 8 for bf16 weights");
   if (a.K > 16384) return fail("gemv: K above 16384 is not supported");
+  if ((a.epi == EPI_SWIGLU ? 2.0 : 1.0) * a.M * a.K * (w8 ? 1 : 2) >= 2147483632.0)
+    return fail("gemv: weight matrices of 2 GiB or more are not supported");
   if (a.pro == PRO_NORM && a.gamma == nullptr) return fail("gemv: RMSNorm needs gamma");
   if (w8 && a.scale == nullptr) return fail("gemv: int8 weights need per-row scales");
   const bool pair = a.epi == EPI_SWIGLU;

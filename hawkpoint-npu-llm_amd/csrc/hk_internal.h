@@ -64,8 +64,6 @@ struct GemvArgs {
 // the number of workgroups, i.e. of partial argmax keys written.
 int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out = nullptr);
 
-// Workgroups the GEMV launches for these arguments (<= kMaxPartialKeys).
-int gemv_blocks(const GemvArgs& a, bool w8);
 
 // Reduce `n` partial keys to the first-maximum index; write it to
 // `token_out` (if set) and, when ctrl->advance, feed it back into `ctrl`
