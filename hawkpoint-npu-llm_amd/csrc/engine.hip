@@ -512,10 +512,13 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
   const hk_model_desc& d = e->d;
   const hipStream_t s = e->stream;
   const int H = d.hidden, I = d.intermediate, QD = d.q_heads * kHeadDim;
-  HK_TRY(launch_embed_rows(tokens_dev, n, d.vocab, e->w.token_embedding, H, e->pf_x, s));
   // chunks of up to 64 tokens run the slab GEMMs, which apply the RMSNorms
-  // to their A operand as they load it (hidden sizes up to 1024)
+  // to their A operand as they load it (hidden sizes up to 1024); their
+  // activations (x, the attention output, h1, act) are then k-blocked, so
+  // the 16 token rows of an MFMA fragment are one 256-byte run
   const bool fused_norm = n <= kSlabMaxTokens && H <= kSlabNormMaxK;
+  const int kb = fused_norm ? 2 : 0;
+  HK_TRY(launch_embed_rows(tokens_dev, n, d.vocab, e->w.token_embedding, H, e->pf_x, s, fused_norm ? n : 0));
   for (int l = 0; l < d.layers; ++l) {
     const hk_layer_weights& lw = e->layers[l];
     if (!fused_norm) HK_TRY(launch_rmsnorm_rows(e->pf_x, H, lw.input_norm, d.rms_eps, e->pf_xn, H, n, H, s));
@@ -533,6 +536,19 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     q.N = e->qkv_rows;
     q.K = H;
     q.epi = lw.qkv_bias ? EPI_BIAS : EPI_BF16;
+    q.kblock = fused_norm ? 1 : 0;
+    if (fused_norm) {  // RoPE and the KV append in the QKV epilogue (no q/k/v rows, no rope_append launch)
+      q.rope.cos_tab = e->w.rope_cos;
+      q.rope.sin_tab = e->w.rope_sin;
+      q.rope.qrot = e->pf_q;
+      q.rope.kcache = e->kcache + (size_t)l * kv_layer_elems(e);
+      q.rope.vcache = e->vcache + (size_t)l * kv_layer_elems(e);
+      q.rope.start = start;
+      q.rope.q_heads = d.q_heads;
+      q.rope.kv_heads = d.kv_heads;
+      q.rope.max_ctx = d.max_context;
+      q.rope.on = 1;
+    }
     q.split_ws = e->pf_split;
     q.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(q, s));
@@ -546,6 +562,8 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     at.vcache = e->vcache + (size_t)l * kv_layer_elems(e);
     at.out = e->pf_att;
     at.ld_out = QD;
+    at.out_kblock = kb;
+    at.rope_done = fused_norm ? 1 : 0;
     at.n = n;
     at.start = start;
     at.q_heads = d.q_heads;
@@ -565,6 +583,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     o.N = H;
     o.K = QD;
     o.epi = EPI_RESID;
+    o.kblock = kb;
     o.split_ws = e->pf_split;
     o.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(o, s));
@@ -582,6 +601,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     g.N = I;
     g.K = H;
     g.epi = EPI_SWIGLU;
+    g.kblock = kb;
     g.split_ws = e->pf_split;
     g.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(g, s));
@@ -598,6 +618,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     dn.N = H;
     dn.K = I;
     dn.epi = EPI_RESID;
+    dn.kblock = kb;
     dn.split_ws = e->pf_split;
     dn.split_ws_floats = e->pf_split_floats;
     HK_TRY(launch_prefill_gemm(dn, s));
@@ -904,8 +925,12 @@ int hk_engine_prefill(hk_engine* e, const int32_t* tokens_host, int32_t n, int32
                               hipMemcpyHostToDevice, e->stream));
       HK_TRY(prefill_chunk(e, e->pf_tokens, m, start + c0));
       if (c0 + m == n && want) {
-        HK_CHECK(hipMemcpyAsync(e->h, e->pf_x + (size_t)(m - 1) * e->d.hidden,
-                                e->d.hidden * sizeof(uint16_t), hipMemcpyDeviceToDevice, e->stream));
+        if (m <= kSlabMaxTokens && e->d.hidden <= kSlabNormMaxK)  // k-blocked x: 16-byte pieces m * 16 bytes apart
+          HK_CHECK(hipMemcpy2DAsync(e->h, 16, e->pf_x + (size_t)(m - 1) * 8, (size_t)m * 16, 16, e->d.hidden / 8,
+                                    hipMemcpyDeviceToDevice, e->stream));
+        else
+          HK_CHECK(hipMemcpyAsync(e->h, e->pf_x + (size_t)(m - 1) * e->d.hidden,
+                                  e->d.hidden * sizeof(uint16_t), hipMemcpyDeviceToDevice, e->stream));
         HK_TRY(set_ctrl(e, -1, start + n - 1, 0));
         HK_TRY(launch_part(e, HK_PART_HEAD, 0));
       }

@@ -225,6 +225,24 @@ struct PrefillGemmArgs {
   // loaded: A = bf16((x * inv_rms) * gamma) with inv_rms = 1 / sqrt(mean(x^2) + eps).
   const uint16_t* gamma;
   float eps;
+  // Slab GEMM only: A, and Y with the residual, k-blocked with M rows --
+  // element (m, k) at ((k / 8) M + m) 8 + k % 8 -- so that the 16 token rows
+  // of an MFMA fragment are one 256-byte run (lda, ldy, ldr unused).  A only
+  // with kblock = 1, all three with kblock = 2.
+  int kblock;
+  // Slab GEMM only, the QKV projection: with rope.on the epilogue applies
+  // RoPE and writes the rotated queries to rope.qrot and the rotated keys and
+  // the values to the caches at slots rope.start.. (rope_append_kernel's job;
+  // Y is not written).  The slabs then take the rows of each RoPE pair
+  // together (rope_row).  N = (q_heads + 2 kv_heads) * 64.
+  struct {
+    const float* cos_tab;  // [max_ctx, 32]
+    const float* sin_tab;
+    uint16_t* qrot;        // [M, q_heads * 64]
+    uint16_t* kcache;      // this layer: [kv_heads, max_ctx, 64]
+    uint16_t* vcache;
+    int start, q_heads, kv_heads, max_ctx, on;
+  } rope;
 };
 
 constexpr int kSlabMaxTokens = 64;
@@ -248,13 +266,15 @@ struct PrefillAttnArgs {
   uint16_t* vcache;
   uint16_t* out;            // [n, ld_out] bf16 attention output
   int ld_out;
+  int out_kblock;           // nonzero: out k-blocked with n rows (see PrefillGemmArgs::kblock)
+  int rope_done;            // nonzero: qrot and the caches are written already (the QKV GEMM's RoPE)
   int n, start, q_heads, kv_heads, max_ctx;
 };
 
-// rope_append then causal attention for tokens start..start+n-1.
+// rope_append (unless rope_done) then causal attention for tokens start..start+n-1.
 int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream);
 int launch_embed_rows(const int32_t* tokens, int n, int vocab, const uint16_t* table, int H,
-                      uint16_t* X, hipStream_t stream);
+                      uint16_t* X, hipStream_t stream, int kb_rows = 0);
 int launch_rmsnorm_rows(const uint16_t* X, int ldx, const uint16_t* gamma, float eps, uint16_t* out,
                         int ldo, int rows, int H, hipStream_t stream);
 

@@ -163,13 +163,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillGemmArgs a) {
 }
 
 // X[i] = E[token_i] (bf16 rows), tokens read from device memory.
+// Row i of X = the embedding of tokens[i]; with kb_rows (the row count) X is
+// k-blocked: element (i, k) at ((k / 8) kb_rows + i) 8 + k % 8.
 __global__ __launch_bounds__(kThreads) void embed_rows_kernel(const int32_t* tokens, int vocab,
                                                               const uint16_t* table, int H,
-                                                              uint16_t* X) {
+                                                              uint16_t* X, int kb_rows) {
   const int i = blockIdx.x;
   int t = tokens[i];
   t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
   const uint32_t* src = reinterpret_cast<const uint32_t*>(table + (size_t)t * H);
+  if (kb_rows) {
+    uint32_t* dst = reinterpret_cast<uint32_t*>(X);
+    for (int j = threadIdx.x; j < H / 2; j += kThreads)
+      dst[((size_t)(j >> 2) * kb_rows + i) * 4 + (j & 3)] = src[j];
+    return;
+  }
   uint32_t* dst = reinterpret_cast<uint32_t*>(X + (size_t)i * H);
   for (int j = threadIdx.x; j < H / 2; j += kThreads) dst[j] = src[j];
 }
@@ -454,6 +462,14 @@ __device__ __forceinline__ float sq8(u32x4 x) {
   return s;
 }
 
+// QKV rows of slab s and lane row r (0..15) when the QKV GEMM applies RoPE
+// itself: slab s covers rows 8 (s % 4) .. + 7 and 32 + 8 (s % 4) .. + 7 of
+// head s / 4, so each RoPE pair (j, j + 32) of a head sits in one workgroup,
+// eight lanes apart.
+__device__ __forceinline__ int rope_row(int s, int r) {
+  return (s >> 2) * kHeadDim + 8 * (s & 3) + (r & 7) + (r >= 8 ? kHeadDim / 2 : 0);
+}
+
 // One batch of a wave's K steps: weight fragments (raw int8 for W8, widened
 // just before the product) and the token fragments of every block.
 template <bool PAIR, bool W8, int B>
@@ -488,17 +504,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   const int mine = steps > wave ? (steps - wave + kSlabWaves - 1) / kSlabWaves : 0;  // this wave's steps
   // byte offsets of this lane's weight row (and up row) and token rows at k
   // = fk; kSlabOutside for a row past the end
-  const int wrow = n0 + fr;
+  const int wrow = a.rope.on ? rope_row(blockIdx.x, fr) : n0 + fr;
   const unsigned wofs = wrow < N ? (unsigned)(wrow * K + fk) * EB : kSlabOutside;
   const unsigned uofs = wrow < N ? (unsigned)((wrow + N) * K + fk) * EB : kSlabOutside;
   unsigned aofs[kSlabBlocks];
 #pragma unroll
   for (int b = 0; b < kSlabBlocks; ++b) {
     const int t = 16 * b + fr;
-    aofs[b] = t < M ? (unsigned)(t * a.lda + fk) * 2u : kSlabOutside;
+    aofs[b] = t >= M ? kSlabOutside
+              : a.kblock ? (unsigned)(((fk >> 3) * M + t) * 16) : (unsigned)(t * a.lda + fk) * 2u;
   }
+  // bytes from column k to column k + 1 of a token row (k a multiple of 8)
+  const unsigned akm = a.kblock ? 2u * (unsigned)M : 2u;
   const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, P * N * K * EB);
-  const __amdgpu_buffer_rsrc_t ar = rsrc(a.A, ((M - 1) * a.lda + K) * 2);
+  const __amdgpu_buffer_rsrc_t ar = rsrc(a.A, a.kblock ? M * K * 2 : ((M - 1) * a.lda + K) * 2);
 
   // loads of the batch starting at this wave's step index j0 (nontemporal
   // weights: each is read once)
@@ -521,7 +540,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
       }
 #pragma unroll
       for (int b = 0; b < kSlabBlocks; ++b)
-        bt.x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, live ? aofs[b] + 2 * k0 : kSlabOutside, 0, 0);
+        bt.x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, live ? aofs[b] + akm * k0 : kSlabOutside, 0, 0);
     }
   };
   auto widen = [&](const typename Batch::WRaw& r) -> bf16x8 {
@@ -640,7 +659,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
           const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
 #pragma unroll
           for (int b = 0; b < kSlabBlocks; ++b)
-            x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, j < mine ? aofs[b] + 2 * k0 : kSlabOutside, 0, 0);
+            x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, j < mine ? aofs[b] + akm * k0 : kSlabOutside, 0, 0);
         }
       };
       auto mul_x = [&](const u32x4 (&x)[2][kSlabBlocks], int i0) {
@@ -677,7 +696,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   // rounding points of the other GEMM kernels)
   for (int f = tid; f < mb * 256; f += kSlabWaves * 64) {
     const int b = f >> 8, l = (f >> 2) & 63, r = f & 3;
-    const int m = 16 * b + 4 * (l >> 4) + r, n = n0 + (l & 15);
+    const int m = 16 * b + 4 * (l >> 4) + r, n = a.rope.on ? rope_row(blockIdx.x, l & 15) : n0 + (l & 15);
     if (m >= M || n >= N) continue;
     float x = 0.0f, u = 0.0f;
 #pragma unroll
@@ -689,7 +708,36 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
       x *= a.scale[n];
       if constexpr (PAIR) u *= a.scale[N + n];
     }
-    uint16_t* y = a.Y + (size_t)m * a.ldy + n;
+    if (a.rope.on) {
+      // QKV with RoPE and the KV append (the rope_append_kernel arithmetic):
+      // the pair partner of row n is lane l ^ 8 of the same token
+      const int lp = l ^ 8, np = rope_row(blockIdx.x, lp & 15);
+      float xp = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kSlabWaves; ++w) xp += red[w][b][lp][r];
+      if constexpr (W8) xp *= a.scale[np];
+      const float v = a.bias ? round_bf16(round_bf16(x) + a.bias[n]) : round_bf16(x);
+      const float vp = a.bias ? round_bf16(round_bf16(xp) + a.bias[np]) : round_bf16(xp);
+      const int hd = n / kHeadDim, j = n % kHeadDim, p = a.rope.start + m;
+      const auto& at = a.rope;
+      if (hd < at.q_heads + at.kv_heads) {
+        const int jj = j & (kHeadDim / 2 - 1);
+        const float c = at.cos_tab[(size_t)p * (kHeadDim / 2) + jj], sn = at.sin_tab[(size_t)p * (kHeadDim / 2) + jj];
+        // first half: x1 c - x2 s; second half: x2 c + x1 s (x1 the first-half value)
+        const uint16_t rot = (uint16_t)(j < kHeadDim / 2 ? f32_to_bf16(v * c - vp * sn) : f32_to_bf16(v * c + vp * sn));
+        if (hd < at.q_heads)
+          at.qrot[(size_t)m * at.q_heads * kHeadDim + (size_t)hd * kHeadDim + j] = rot;
+        else
+          at.kcache[((size_t)(hd - at.q_heads) * at.max_ctx + p) * kHeadDim + j] = rot;
+      } else {
+        at.vcache[((size_t)(hd - at.q_heads - at.kv_heads) * at.max_ctx + p) * kHeadDim + j] = (uint16_t)f32_to_bf16(v);
+      }
+      continue;
+    }
+    // (k-blocked outputs and residuals: element (m, n) at ((n / 8) M + m) 8 + n % 8)
+    const size_t yo = a.kblock == 2 ? ((size_t)(n >> 3) * M + m) * 8 + (n & 7) : (size_t)m * a.ldy + n;
+    const size_t ro = a.kblock == 2 ? yo : (size_t)m * a.ldr + n;
+    uint16_t* y = a.Y + yo;
     switch (a.epi) {
       case EPI_BF16:
         *y = (uint16_t)f32_to_bf16(x);
@@ -698,7 +746,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
         *y = (uint16_t)f32_to_bf16(round_bf16(x) + a.bias[n]);
         break;
       case EPI_RESID:
-        *y = (uint16_t)f32_to_bf16(round_bf16(x) + bf16_to_f32(a.resid[(size_t)m * a.ldr + n]));
+        *y = (uint16_t)f32_to_bf16(round_bf16(x) + bf16_to_f32(a.resid[ro]));
         break;
       case EPI_SWIGLU:
         if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(x), round_bf16(u)));
@@ -926,12 +974,13 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     }
   }
   if (!tok_ok) return;
-  uint16_t* out = a.out + (size_t)tok * a.ld_out + (size_t)h * kHeadDim + 4 * quad;
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
     const uint32_t lo = f32_to_bf16(o[db][0] / l_run) | (f32_to_bf16(o[db][1] / l_run) << 16);
     const uint32_t hi = f32_to_bf16(o[db][2] / l_run) | (f32_to_bf16(o[db][3] / l_run) << 16);
-    *reinterpret_cast<uint2*>(out + 16 * db) = make_uint2(lo, hi);
+    const int d = h * kHeadDim + 16 * db + 4 * quad;  // four dimensions, within one 8-wide block
+    const size_t at = a.out_kblock ? ((size_t)(d >> 3) * a.n + tok) * 8 + (d & 7) : (size_t)tok * a.ld_out + d;
+    *reinterpret_cast<uint2*>(a.out + at) = make_uint2(lo, hi);
   }
 }
 
@@ -965,6 +1014,10 @@ int launch_slab(const PrefillGemmArgs& a, hipStream_t stream) {
 template <bool W8>
 int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   const bool pair = a.epi == EPI_SWIGLU;
+  if ((a.kblock || a.rope.on) && !(a.grp_count == nullptr && a.M <= kSlabMaxTokens))
+    return fail("prefill gemm: k-blocked operands and RoPE need the slab path (M <= 64)");
+  if (a.rope.on && (a.N != (a.rope.q_heads + 2 * a.rope.kv_heads) * kHeadDim || a.epi == EPI_SWIGLU))
+    return fail("prefill gemm: RoPE needs the QKV projection");
   if (a.grp_count == nullptr && a.M <= kSlabMaxTokens) {
     if (a.gamma && a.K > kSlabNormMaxK) return fail("slab gemm: a normalised A operand needs K <= 1024");
     return pair ? launch_slab<true, W8>(a, stream) : launch_slab<false, W8>(a, stream);
@@ -1031,8 +1084,8 @@ int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
 }
 
 int launch_embed_rows(const int32_t* tokens, int n, int vocab, const uint16_t* table, int H,
-                      uint16_t* X, hipStream_t stream) {
-  hipLaunchKernelGGL(embed_rows_kernel, dim3(n), dim3(kThreads), 0, stream, tokens, vocab, table, H, X);
+                      uint16_t* X, hipStream_t stream, int kb_rows) {
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(n), dim3(kThreads), 0, stream, tokens, vocab, table, H, X, kb_rows);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "embed launch");
 }
@@ -1049,9 +1102,12 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream) {
   if (a.q_heads % a.kv_heads != 0) return fail("prefill attention: unsupported head grouping");
   if (a.ld_out % 4 != 0) return fail("prefill attention: output rows must be 8-byte aligned");
   if (a.start < 0 || a.start + a.n > a.max_ctx) return fail("prefill attention: slots out of range");
-  hipLaunchKernelGGL(rope_append_kernel, dim3(a.n), dim3(kThreads), 0, stream, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return hip_fail(err, "rope append launch");
+  hipError_t err;
+  if (!a.rope_done) {
+    hipLaunchKernelGGL(rope_append_kernel, dim3(a.n), dim3(kThreads), 0, stream, a);
+    err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(err, "rope append launch");
+  }
   hipLaunchKernelGGL(attention_prefill_kernel, dim3(a.q_heads, (a.n + kFaRows - 1) / kFaRows), dim3(kThreads), 0,
                      stream, a);
   err = hipGetLastError();
