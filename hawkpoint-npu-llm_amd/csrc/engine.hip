@@ -12,6 +12,7 @@
 // one captured hipGraph per variant (with / without the head) serves every
 // position; the host only rewrites the control block between replays.
 #include <algorithm>
+#include <array>
 #include <map>
 #include <mutex>
 #include <string>
@@ -198,6 +199,9 @@ struct hk_engine {
   int32_t* pf_tokens = nullptr;
   float* pf_split = nullptr;   // split-K partial sums of GEMMs with few tiles
   size_t pf_split_floats = 0;
+  // per layer, MFMA-native copies of qkv (RoPE order), o, gate_up and down
+  // for the slab GEMMs of chunks up to 64 tokens (empty: row-major weights)
+  std::vector<std::array<void*, 4>> pf_native;
 };
 
 namespace {
@@ -467,6 +471,9 @@ void free_engine(hk_engine* e) {
     if (p) (void)hipFree(p);
   for (uint16_t* p : e->down_x)
     if (p) (void)hipFree(p);
+  for (auto& m : e->pf_native)
+    for (void* p : m)
+      if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -503,6 +510,22 @@ int prefill_workspace(hk_engine* e) {
                                    split_ws_need(m, d.intermediate, d.hidden, true),
                                    split_ws_need(m, d.hidden, d.intermediate, false)});
   HK_TRY(dalloc(&e->pf_split, e->pf_split_floats));
+  // the MFMA-native weight copies (every matrix of an engine shape has whole
+  // 16-row slabs: 64-wide heads, hidden and intermediate sizes multiples of 16)
+  if (d.hidden % 16 == 0 && d.intermediate % 16 == 0) {
+    const int wb = e->w8 ? 1 : 2;
+    e->pf_native.assign(d.layers, {nullptr, nullptr, nullptr, nullptr});
+    for (int l = 0; l < d.layers; ++l) {
+      const hk_layer_weights& lw = e->layers[l];
+      const struct { const void* src; int R, K, rope; } m[4] = {
+          {lw.qkv, e->qkv_rows, d.hidden, 1}, {lw.o_proj, d.hidden, QD, 0},
+          {lw.gate_up, 2 * d.intermediate, d.hidden, 0}, {lw.down_proj, d.hidden, d.intermediate, 0}};
+      for (int i = 0; i < 4; ++i) {
+        HK_CHECK(hipMalloc(&e->pf_native[l][i], (size_t)m[i].R * m[i].K * wb));
+        HK_TRY(launch_repack_mfma(m[i].src, e->pf_native[l][i], m[i].R, m[i].K, wb, m[i].rope, e->stream));
+      }
+    }
+  }
   e->pf_rows = rows;
   return 0;
 }
@@ -518,6 +541,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
   // the 16 token rows of an MFMA fragment are one 256-byte run
   const bool fused_norm = n <= kSlabMaxTokens && H <= kSlabNormMaxK;
   const int kb = fused_norm ? 2 : 0;
+  const bool slab = n <= kSlabMaxTokens, native = !e->pf_native.empty();
   HK_TRY(launch_embed_rows(tokens_dev, n, d.vocab, e->w.token_embedding, H, e->pf_x, s, fused_norm ? n : 0));
   for (int l = 0; l < d.layers; ++l) {
     const hk_layer_weights& lw = e->layers[l];
@@ -528,6 +552,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     q.eps = d.rms_eps;
     q.lda = H;
     q.W = static_cast<const uint16_t*>(lw.qkv);
+    q.Wn = fused_norm && native ? e->pf_native[l][0] : nullptr;
     q.scale = e->w8 ? lw.qkv_scale : nullptr;
     q.bias = lw.qkv_bias;
     q.Y = e->pf_qkv;
@@ -574,6 +599,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     o.A = e->pf_att;
     o.lda = QD;
     o.W = static_cast<const uint16_t*>(lw.o_proj);
+    o.Wn = slab && native ? e->pf_native[l][1] : nullptr;
     o.scale = e->w8 ? lw.o_scale : nullptr;
     o.resid = e->pf_x;
     o.ldr = H;
@@ -594,6 +620,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     g.eps = d.rms_eps;
     g.lda = H;
     g.W = static_cast<const uint16_t*>(lw.gate_up);
+    g.Wn = slab && native ? e->pf_native[l][2] : nullptr;
     g.scale = e->w8 ? lw.gate_up_scale : nullptr;
     g.Y = e->pf_act;
     g.ldy = I;
@@ -609,6 +636,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     dn.A = e->pf_act;
     dn.lda = I;
     dn.W = static_cast<const uint16_t*>(lw.down_proj);
+    dn.Wn = slab && native ? e->pf_native[l][3] : nullptr;
     dn.scale = e->w8 ? lw.down_scale : nullptr;
     dn.resid = e->pf_h1;
     dn.ldr = H;

@@ -235,6 +235,8 @@ struct PrefillGemmArgs {
   // the values to the caches at slots rope.start.. (rope_append_kernel's job;
   // Y is not written).  The slabs then take the rows of each RoPE pair
   // together (rope_row).  N = (q_heads + 2 kv_heads) * 64.
+  // Slab GEMM only: the MFMA-native copy of W (launch_repack_mfma), or null
+  const void* Wn;
   struct {
     const float* cos_tab;  // [max_ctx, 32]
     const float* sin_tab;
@@ -277,6 +279,11 @@ int launch_embed_rows(const int32_t* tokens, int n, int vocab, const uint16_t* t
                       uint16_t* X, hipStream_t stream, int kb_rows = 0);
 int launch_rmsnorm_rows(const uint16_t* X, int ldx, const uint16_t* gamma, float eps, uint16_t* out,
                         int ldo, int rows, int H, hipStream_t stream);
+// dst = the MFMA-native copy of the row-major [R, K] matrix src (weights of
+// weight_bytes bytes) for the slab GEMM: piece (16 s + r, c) of 8 weights at
+// (s (K / 8) + c) 16 + r; rope: the rows of slab s are the QKV GEMM's RoPE
+// order, so the copy serves a GEMM with rope.on.
+int launch_repack_mfma(const void* src, void* dst, int R, int K, int weight_bytes, int rope, hipStream_t stream);
 
 // Standalone RMSNorm: out = bf16((v * inv_rms) * gamma).
 int launch_rmsnorm(const uint16_t* x, const uint16_t* gamma, float eps, uint16_t* out,

@@ -505,8 +505,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   // byte offsets of this lane's weight row (and up row) and token rows at k
   // = fk; kSlabOutside for a row past the end
   const int wrow = a.rope.on ? rope_row(blockIdx.x, fr) : n0 + fr;
-  const unsigned wofs = wrow < N ? (unsigned)(wrow * K + fk) * EB : kSlabOutside;
-  const unsigned uofs = wrow < N ? (unsigned)((wrow + N) * K + fk) * EB : kSlabOutside;
+  // weight piece (8 weights) of row n at k group g: row-major, or in the
+  // MFMA-native copy Wn ([N/16][K/8][16] pieces: a fragment's 16 rows are one
+  // run); wkm: bytes from column k to column k + 1 along a row
+  const bool native = a.Wn != nullptr;
+  const unsigned pb = 8u * EB;  // bytes per piece
+  auto wpiece = [&](int n) -> unsigned {
+    return native ? (unsigned)((((n >> 4) * (K >> 3) + (fk >> 3)) * 16 + (n & 15))) * pb : (unsigned)(n * K + fk) * EB;
+  };
+  const unsigned wkm = native ? 2u * pb : (unsigned)EB;
+  // the copy holds each slab's rows in fragment order (RoPE's permutation too)
+  const int nrow = native ? n0 + fr : wrow;
+  const unsigned wofs = wrow < N ? wpiece(nrow) : kSlabOutside;
+  const unsigned uofs = wrow < N ? wpiece(nrow + N) : kSlabOutside;
   unsigned aofs[kSlabBlocks];
 #pragma unroll
   for (int b = 0; b < kSlabBlocks; ++b) {
@@ -516,7 +527,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   }
   // bytes from column k to column k + 1 of a token row (k a multiple of 8)
   const unsigned akm = a.kblock ? 2u * (unsigned)M : 2u;
-  const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, P * N * K * EB);
+  const __amdgpu_buffer_rsrc_t wr = rsrc(native ? a.Wn : a.W, P * N * K * EB);
   const __amdgpu_buffer_rsrc_t ar = rsrc(a.A, a.kblock ? M * K * 2 : ((M - 1) * a.lda + K) * 2);
 
   // loads of the batch starting at this wave's step index j0 (nontemporal
@@ -527,16 +538,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
       const int j = j0 + i;
       const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
       const bool live = j < mine;
-      const unsigned wo = live ? wofs + k0 * EB : kSlabOutside;
+      const unsigned wo = live ? wofs + k0 * wkm : kSlabOutside;
+      const unsigned uo = live ? uofs + k0 * wkm : kSlabOutside;
       if constexpr (W8) {
         bt.w[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
-        if constexpr (PAIR)
-          bt.u[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-                                                    wr, live ? uofs + k0 : kSlabOutside, 0, 2));
+        if constexpr (PAIR) bt.u[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, uo, 0, 2));
       } else {
         bt.w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2);
-        if constexpr (PAIR)
-          bt.u[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, live ? uofs + 2 * k0 : kSlabOutside, 0, 2);
+        if constexpr (PAIR) bt.u[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, uo, 0, 2);
       }
 #pragma unroll
       for (int b = 0; b < kSlabBlocks; ++b)
@@ -645,7 +654,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
       for (int i = 0; i < kSlabWPre; ++i) {
         const int j = g0 + i;
         const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
-        const unsigned wo = j < mine ? wofs + k0 * EB : kSlabOutside;
+        const unsigned wo = j < mine ? wofs + k0 * wkm : kSlabOutside;
         if constexpr (W8)
           wv[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
         else
@@ -1020,6 +1029,7 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     return fail("prefill gemm: RoPE needs the QKV projection");
   if (a.grp_count == nullptr && a.M <= kSlabMaxTokens) {
     if (a.gamma && a.K > kSlabNormMaxK) return fail("slab gemm: a normalised A operand needs K <= 1024");
+    if (a.Wn && a.N % 16) return fail("slab gemm: the MFMA-native copy needs whole 16-row slabs");
     return pair ? launch_slab<true, W8>(a, stream) : launch_slab<false, W8>(a, stream);
   }
   if (a.gamma) return fail("prefill gemm: a normalised A operand needs the slab path (M <= 64)");
@@ -1088,6 +1098,37 @@ int launch_embed_rows(const int32_t* tokens, int n, int vocab, const uint16_t* t
   hipLaunchKernelGGL(embed_rows_kernel, dim3(n), dim3(kThreads), 0, stream, tokens, vocab, table, H, X, kb_rows);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "embed launch");
+}
+
+// The MFMA-native copy of a row-major [R, K] weight matrix (R a multiple of
+// 16, K of 8): slab s (16 rows) holds, for each k group c of 8 weights, the
+// 16 pieces of its rows in fragment order at (s (K / 8) + c) 16 + r, so a
+// slab GEMM fragment load is one run.  Row r of slab s is source row
+// 16 s + r, or rope_row(s, r) for a QKV matrix whose GEMM applies RoPE.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void repack_mfma_kernel(const T* src, T* dst, int R, int K, int rope) {
+  const size_t groups = K / 8, pieces = (size_t)R * groups;
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < pieces; i += (size_t)gridDim.x * kThreads) {
+    const int slab = (int)(i / (16 * groups)), r = (int)(i & 15);
+    const size_t c = (i / 16) % groups;
+    const int row = rope ? rope_row(slab, r) : 16 * slab + r;
+    dst[i] = src[(size_t)row * groups + c];
+  }
+}
+
+int launch_repack_mfma(const void* src, void* dst, int R, int K, int weight_bytes, int rope, hipStream_t stream) {
+  if (R % 16 || K % 8 || (weight_bytes != 1 && weight_bytes != 2)) return fail("repack: R % 16, K % 8, 1 or 2 bytes");
+  if (rope && R % 64) return fail("repack: a RoPE QKV matrix has whole 64-row heads");
+  const size_t pieces = (size_t)R * (K / 8);
+  const int blocks = (int)std::min<size_t>((pieces + kThreads - 1) / kThreads, 8192);
+  if (weight_bytes == 2)
+    hipLaunchKernelGGL(repack_mfma_kernel<u32x4>, dim3(blocks), dim3(kThreads), 0, stream,
+                       static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), R, K, rope);
+  else
+    hipLaunchKernelGGL(repack_mfma_kernel<uint2>, dim3(blocks), dim3(kThreads), 0, stream,
+                       static_cast<const uint2*>(src), static_cast<uint2*>(dst), R, K, rope);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "repack launch");
 }
 
 int launch_rmsnorm_rows(const uint16_t* X, int ldx, const uint16_t* gamma, float eps, uint16_t* out,
