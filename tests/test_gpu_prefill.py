@@ -172,10 +172,12 @@ def test_prefill_continues_from_cached_prefix():
                                   (130, False), (1, True), (64, True)])
 def test_prefill_lengths_around_the_slab_gemm(n, w8):
     """Chunks of up to 64 tokens run the slab GEMMs (one workgroup per 16
-    outputs over all of K, RMSNorm applied while loading A); 65 and more take
-    the tiled GEMMs.  Last-token logits and KV slots of a 2-layer
-    Qwen2.5-0.5B-shape model with random RMSNorm gains against the oracle's
-    prefill at each length."""
+    outputs over all of K, RMSNorm applied while loading A, weights from the
+    MFMA-native copies); 65 and more take the tiled GEMMs.  Last-token logits
+    and KV slots of a 2-layer Qwen2.5-0.5B-shape model with random RMSNorm
+    gains against the oracle's prefill at each length, and a second prefill
+    of the same prompt bit for bit equal to the first (every sum is added in
+    a fixed order)."""
     from runtime.qwen_engine import QwenDecoderEngine
     from test_gpu_engine import _check_kv_slot
 
@@ -196,6 +198,8 @@ def test_prefill_lengths_around_the_slab_gemm(n, w8):
                 _check_kv_slot(engine, oracle.stage, layer, slot, 2e-2)
             k, v = engine.read_kv(layer, n)
             assert np.all(k == 0) and np.all(v == 0)
+        tok2, logits2 = engine.prefill(prompt, 0)
+        assert tok2 == tok and np.array_equal(logits2, logits)
     finally:
         engine.close()
 
