@@ -275,14 +275,17 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
     kt1 = min(kt1, kt0 + per);
   } else {
     // Workgroups go to the 8 XCDs in turn (workgroup b to XCD b % 8).  Tile
-    // t = (b % 8) * per + b / 8 gives each XCD a contiguous run of tiles, and
-    // with token tiles varying fastest within the run, an XCD works through a
-    // few weight tiles only, which its own L2 keeps while it sweeps the tokens.
+    // order t = (b % 8) * per + b / 8 gives each XCD a contiguous run.  The
+    // order walks groups of up to 12 output tiles (4 when there are more)
+    // with the output tile fastest, so the tiles an XCD holds at once share a
+    // few token tiles and a few weight tiles, which its own L2 keeps.
     const int per = (mt * ntile + 7) / 8;
     const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (t >= mt * ntile) return;
-    m0 = (t % mt) * BM;
-    n0 = (t / mt) * BN;
+    const int GN = ntile <= 12 ? ntile : 4;
+    const int grp = t / (GN * mt), gn = min(GN, ntile - grp * GN), in = t - grp * GN * mt;
+    m0 = (in / gn) * BM;
+    n0 = (grp * GN + in % gn) * BN;
   }
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
   const int fr = lane & 15, fk = (lane >> 4) * 8;

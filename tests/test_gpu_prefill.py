@@ -25,7 +25,10 @@ def _dev(array):
      (40, 896, 4864, "resid"), (1, 576, 576, "none"), (513, 64, 32, "none"), (70, 960, 576, "bias"),
      # 128-token tiles (M >= 128, K a multiple of 64): ragged M and N, and a
      # case with enough tiles for 128-wide outputs
-     (513, 896, 896, "resid"), (300, 1000, 128, "bias"), (1024, 8200, 64, "none"), (128, 64, 4864, "resid")],
+     (513, 896, 896, "resid"), (300, 1000, 128, "bias"), (1024, 8200, 64, "none"), (128, 64, 4864, "resid"),
+     # enough 128-token tiles for the XCD-grouped tile order to span
+     # several groups of output tiles: whole and ragged token tiles
+     (2048, 1152, 896, "bias"), (1500, 2048, 192, "resid")],
 )
 def test_gemm_bf16_matches_oracle(hk_lib, m, n, k, epi):
     from runtime import hip
