@@ -1593,14 +1593,20 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       if (is_q) {
         bool ok = true;
         if constexpr (S::W8) {  // before the wait: the loads have had the MLP phase to land
-          widen_w8<0, Q.nj>(pf);
-          if (is_o) widen_w8<OFF_O, O.nj>(pf);
+          if (!stager) {
+            widen_w8<0, Q.nj>(pf);
+            if (is_o) widen_w8<OFF_O, O.nj>(pf);
+          }
         }
         if (stager) {
           if (l == 0)
             stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
           else  // h from XCD 0's own reducers (reduce_h), in its L2
             ok = stage_wave<S::H, true, true, kLocal>(c, a.tact, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
+          if constexpr (S::W8) {  // the stagers' own rows, once h is staged
+            widen_w8<0, Q.nj>(pf);
+            if (is_o) widen_w8<OFF_O, O.nj>(pf);
+          }
         }
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
