@@ -26,6 +26,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short v4s16 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kTM = 64;       // tokens per tile
@@ -840,7 +841,6 @@ int split_parts(int M, int N, int K) {
 constexpr int kFaRows = 64;                 // query tokens per workgroup
 constexpr int kFaSlots = 128;               // KV slots per block
 constexpr int kFaKRow = kHeadDim + 8;       // bf16 per K row in LDS (padding)
-constexpr int kFaVRow = kFaSlots + 8;       // bf16 per V^T row in LDS
 constexpr int kFaSB = kFaSlots / 16;        // 16-slot S^T blocks per KV block
 // exp(s / 8 - m) = exp2(s * log2(e) / 8 - m'): the scores are kept in base-2
 // units so that each exponential is one v_exp_f32
@@ -848,7 +848,7 @@ constexpr float kFaScale = 0.125f * 1.4426950408889634f;
 
 __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kFaSlots][kFaKRow];  // [slot][dim]
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim][kFaVRow];  // [dim][slot]
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kFaSlots][kFaKRow];  // [slot][dim]
   const int h = blockIdx.x;
   const int nblk = (a.n + kFaRows - 1) / kFaRows;
   const int qb = nblk - 1 - (int)blockIdx.y;  // the longest blocks start first
@@ -871,27 +871,20 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     for (int kk = 0; kk < 2; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, tok_ok ? load16(qrow + 32 * kk) : zero);
   }
 
-  // tile loads; slots past the block's last one read as zero.  K: thread t
-  // takes slot t / 2, dimensions 32 (t % 2) .. + 32.  V: thread t takes the
-  // slot pair 2 (t % 64), + 1 and dimensions 16 (t / 64) .. + 16, so that it
-  // writes V^T as 32-bit words (two slots of one dimension), a wave's 64
-  // threads covering 64 consecutive words of one V^T row
+  // tile loads through buffer resources that end at the block's last slot,
+  // so later slots read as zero with no branch: thread t takes slot t / 2,
+  // dimensions 32 (t % 2) .. + 32, of K and of V (both stay [slot][dim] in
+  // LDS; the P @ V products read V transposed with ds_read_b64_tr_b16)
   const int ls = tid >> 1, ld0 = (tid & 1) * 32;
-  const int vp = tid & 63, vd = (tid >> 6) * 16;
+  const __amdgpu_buffer_rsrc_t kres = rsrc(a.kcache + kv_base * kHeadDim, (last_slot + 1) * kHeadDim * 2);
+  const __amdgpu_buffer_rsrc_t vres = rsrc(a.vcache + kv_base * kHeadDim, (last_slot + 1) * kHeadDim * 2);
   u32x4 kr[4], vr[4];
   auto load_tile = [&](int kb) {
-    const int slot = kb * kFaSlots + ls;
-    const bool ok = slot <= last_slot;
-    const size_t off = (kv_base + (ok ? slot : 0)) * kHeadDim + ld0;
+    const unsigned off = (unsigned)((kb * kFaSlots + ls) * kHeadDim + ld0) * 2u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kr[i] = ok ? load16(a.kcache + off + 8 * i) : zero;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int vs = kb * kFaSlots + 2 * vp + j;
-      const bool vok = vs <= last_slot;
-      const size_t voff = (kv_base + (vok ? vs : 0)) * kHeadDim + vd;
-      vr[2 * j] = vok ? load16(a.vcache + voff) : zero;
-      vr[2 * j + 1] = vok ? load16(a.vcache + voff + 8) : zero;
+    for (int i = 0; i < 4; ++i) {
+      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 16 * i, 0);
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 16 * i, 0);
     }
   };
 
@@ -903,12 +896,9 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
   for (int kb = 0; kb < nkv; ++kb) {
     __syncthreads();  // the previous tile has been read
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8 * i]) = kr[i];
-#pragma unroll
-    for (int d = 0; d < 16; ++d) {  // dimension vd + d of slots 2 vp, 2 vp + 1
-      const uint32_t w0 = vr[d >> 3][(d & 7) >> 1], w1 = vr[2 + (d >> 3)][(d & 7) >> 1];
-      const uint32_t pair = (d & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u)) : ((w0 & 0xffffu) | (w1 << 16));
-      *reinterpret_cast<uint32_t*>(&Vt[vd + d][2 * vp]) = pair;
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8 * i]) = kr[i];
+      *reinterpret_cast<u32x4*>(&Vs[ls][ld0 + 8 * i]) = vr[i];
     }
     __syncthreads();
     if (kb + 1 < nkv) load_tile(kb + 1);  // in flight during this tile's math
@@ -926,15 +916,28 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
       }
     }
     float mx = -INFINITY;
+    // a block whose slots all precede every token of the workgroup needs no
+    // causal mask (uniform: the block's first token and the last slot)
+    const bool full = s0 + kFaSlots - 1 <= a.start + qb * kFaRows && qb * kFaRows + kFaRows <= a.n;
+    if (full) {
 #pragma unroll
-    for (int sb = 0; sb < kFaSB; ++sb)
+      for (int sb = 0; sb < kFaSB; ++sb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int slot = s0 + 16 * sb + 4 * quad + r;
-        const float v = (tok_ok && slot <= p) ? sv[sb][r] * kFaScale : -INFINITY;
-        sv[sb][r] = v;
-        mx = fmaxf(mx, v);
-      }
+        for (int r = 0; r < 4; ++r) {
+          sv[sb][r] *= kFaScale;
+          mx = fmaxf(mx, sv[sb][r]);
+        }
+    } else {
+#pragma unroll
+      for (int sb = 0; sb < kFaSB; ++sb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int slot = s0 + 16 * sb + 4 * quad + r;
+          const float v = (tok_ok && slot <= p) ? sv[sb][r] * kFaScale : -INFINITY;
+          sv[sb][r] = v;
+          mx = fmaxf(mx, v);
+        }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
@@ -977,9 +980,19 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
       const bf16x8 plo = __builtin_bit_cast(bf16x8, u32x4{pl[0], pl[1], pl[2], pl[3]});
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const uint2 v0 = *reinterpret_cast<const uint2*>(&Vt[16 * db + col][32 * t + 4 * quad]);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(&Vt[16 * db + col][32 * t + 16 + 4 * quad]);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{v0.x, v0.y, v1.x, v1.y});
+        // V^T fragment: lane (quad, col) needs dimension 16 db + col of slots
+        // 32 t + 4 quad + 0..3 and 32 t + 16 + 4 quad + 0..3.  In each group
+        // of 16 lanes the transpose read hands lane i the values 4k + i / 4
+        // of the group's lanes' 4-element rows, position i % 4 (k = 0..3), so
+        // lane c of the group points at slot base + c / 4, dimensions
+        // 16 db + 4 (c % 4) .. + 3.
+        const int rs = 32 * t + 4 * quad + (col >> 2), rd = 16 * db + 4 * (col & 3);
+        const v4s16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s16*)&Vs[rs][rd]);
+        const v4s16 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s16*)&Vs[rs + 16][rd]);
+        const u32x2_t w0 = __builtin_bit_cast(u32x2_t, t0), w1 = __builtin_bit_cast(u32x2_t, t1);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{w0.x, w0.y, w1.x, w1.y});
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[db], 0, 0, 0);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo, o[db], 0, 0, 0);
       }
