@@ -431,19 +431,22 @@ __global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(GemvArgs a) {
   }
 }
 
-int g_cu_count = 0;
+}  // namespace
 
 int cu_count() {
-  if (g_cu_count == 0) {
+  static int count = 0;
+  if (count == 0) {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
         hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      g_cu_count = n;
+      count = n;
     else
-      g_cu_count = 256;
+      count = 256;
   }
-  return g_cu_count;
+  return count;
 }
+
+namespace {
 
 // Workgroups for a launch: one row group per wave when that fits in four
 // workgroups per CU, otherwise four per CU looping over the groups.

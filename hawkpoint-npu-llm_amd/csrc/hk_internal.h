@@ -249,6 +249,8 @@ struct PrefillGemmArgs {
 
 constexpr int kSlabMaxTokens = 64;
 constexpr int kSlabNormMaxK = 1024;
+// compute units of the current device
+int cu_count();
 
 constexpr int kSplitTarget = 256;  // workgroups the split aims for
 // float32 workspace the split-K path needs for an M x N GEMM (2N outputs

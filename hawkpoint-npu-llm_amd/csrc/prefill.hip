@@ -1080,9 +1080,13 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     return err == hipSuccess ? 0 : hip_fail(err, "split reduce launch");
   }
   if (a.grp_count == nullptr && a.M >= kBM && a.K % kBK == 0) {
-    // 128-token tiles; 128-wide outputs only when that still gives 512 tiles
-    const int mt = (a.M + kBM - 1) / kBM;
-    const bool wide = !pair && mt * ((a.N + 127) / 128) >= 512;
+    // 128-token tiles, 64 or 128 outputs wide: two workgroups fit a CU, and
+    // the wide tiles (about 1.7 times the work each) are taken when the
+    // narrow ones would need at least twice as many rounds of workgroups
+    const int mt = (a.M + kBM - 1) / kBM, slots = 2 * cu_count();
+    const int rounds64 = (mt * ((a.N + 63) / 64) + slots - 1) / slots;
+    const int rounds128 = (mt * ((a.N + 127) / 128) + slots - 1) / slots;
+    const bool wide = !pair && rounds64 >= 2 * rounds128;
     const int bn = wide ? 128 : 64;
     const dim3 g(8 * ((mt * ((a.N + bn - 1) / bn) + 7) / 8));
     if (pair)

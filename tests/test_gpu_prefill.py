@@ -28,7 +28,9 @@ def _dev(array):
      (513, 896, 896, "resid"), (300, 1000, 128, "bias"), (1024, 8200, 64, "none"), (128, 64, 4864, "resid"),
      # enough 128-token tiles for the XCD-grouped tile order to span
      # several groups of output tiles: whole and ragged token tiles
-     (2048, 1152, 896, "bias"), (1500, 2048, 192, "resid")],
+     (2048, 1152, 896, "bias"), (1500, 2048, 192, "resid"),
+     # 128-wide output tiles: 64-wide ones would take two rounds of workgroups
+     (4096, 1152, 128, "bias")],
 )
 def test_gemm_bf16_matches_oracle(hk_lib, m, n, k, epi):
     from runtime import hip
