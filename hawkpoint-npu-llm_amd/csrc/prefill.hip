@@ -184,28 +184,44 @@ __global__ __launch_bounds__(kThreads) void embed_rows_kernel(const int32_t* tok
 }
 
 // One row per workgroup: out = bf16((v * inv_rms) * gamma).
+// RMSNorm of eight bf16 inputs (one 16-byte fragment) with the token's
+// inverse rms and eight gains: bf16((x * inv) * gamma), the reference's order.
+__device__ __forceinline__ u32x4 norm8(u32x4 x, float inv, u32x4 g) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, gs[4] = {g.x, g.y, g.z, g.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = f32x2_to_bf16x2((bf_lo(xs[i]) * inv) * bf_lo(gs[i]), (bf_hi(xs[i]) * inv) * bf_hi(gs[i]));
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ float sq8(u32x4 x) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += bf_lo(xs[i]) * bf_lo(xs[i]);
+    s += bf_hi(xs[i]) * bf_hi(xs[i]);
+  }
+  return s;
+}
+
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const uint16_t* X, int ldx,
                                                                 const uint16_t* gamma, float eps,
-                                                                uint16_t* out, int ldo, int H) {
-  __shared__ float red[kThreads / 64];
-  const int row = blockIdx.x;
+                                                                uint16_t* out, int ldo, int H, int rows) {
+  // one wave per row, 16-byte pieces of 8 values (H a multiple of 8): the
+  // squares in one pass, then the row again (from the caches) normalised
+  const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
   const uint16_t* x = X + (size_t)row * ldx;
-  const int tid = threadIdx.x;
+  const int chunks = H / 8;
   float ss = 0.0f;
-  for (int j = tid; j < H; j += kThreads) {
-    const float v = bf16_to_f32(x[j]);
-    ss += v * v;
-  }
+  for (int c = lane; c < chunks; c += 64) ss += sq8(load16(x + 8 * c));
   ss = group_sum<64>(ss);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
-  float total = red[0];
-#pragma unroll
-  for (int w = 1; w < kThreads / 64; ++w) total += red[w];
-  const float inv = 1.0f / sqrtf(total / (float)H + eps);
+  const float inv = 1.0f / sqrtf(ss / (float)H + eps);
   uint16_t* o = out + (size_t)row * ldo;
-  for (int j = tid; j < H; j += kThreads)
-    o[j] = (uint16_t)f32_to_bf16((bf16_to_f32(x[j]) * inv) * bf16_to_f32(gamma[j]));
+  for (int c = lane; c < chunks; c += 64)
+    *reinterpret_cast<u32x4*>(o + 8 * c) = norm8(load16(x + 8 * c), inv, load16(gamma + 8 * c));
 }
 
 // Token i at slot p = start + i: rotated q heads to Qr[i], rotated k and raw v
@@ -443,28 +459,6 @@ constexpr int kSlabBatch = 2;                     // K steps per wave in flight 
 constexpr int kSlabLongWaves = 8;                 // waves of a long-K workgroup
 constexpr int kSlabWPre = 20;                     // its weight steps per wave requested at once
 constexpr unsigned kSlabOutside = 0x7ffffff0u;    // a byte offset past every resource
-
-// RMSNorm of eight bf16 inputs (one 16-byte fragment) with the token's
-// inverse rms and eight gains: bf16((x * inv) * gamma), the reference's order.
-__device__ __forceinline__ u32x4 norm8(u32x4 x, float inv, u32x4 g) {
-  const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, gs[4] = {g.x, g.y, g.z, g.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    o[i] = f32x2_to_bf16x2((bf_lo(xs[i]) * inv) * bf_lo(gs[i]), (bf_hi(xs[i]) * inv) * bf_hi(gs[i]));
-  return u32x4{o[0], o[1], o[2], o[3]};
-}
-
-__device__ __forceinline__ float sq8(u32x4 x) {
-  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s += bf_lo(xs[i]) * bf_lo(xs[i]);
-    s += bf_hi(xs[i]) * bf_hi(xs[i]);
-  }
-  return s;
-}
 
 // QKV rows of slab s and lane row r (0..15) when the QKV GEMM applies RoPE
 // itself: slab s covers rows 8 (s % 4) .. + 7 and 32 + 8 (s % 4) .. + 7 of
@@ -1153,8 +1147,10 @@ int launch_repack_mfma(const void* src, void* dst, int R, int K, int weight_byte
 
 int launch_rmsnorm_rows(const uint16_t* X, int ldx, const uint16_t* gamma, float eps, uint16_t* out,
                         int ldo, int rows, int H, hipStream_t stream) {
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kThreads), 0, stream, X, ldx, gamma, eps,
-                     out, ldo, H);
+  if (H % 8 || ldx % 8 || ldo % 8) return fail("rmsnorm rows: H and the row strides must be multiples of 8");
+  const int per = kThreads / 64;
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((rows + per - 1) / per), dim3(kThreads), 0, stream, X, ldx, gamma,
+                     eps, out, ldo, H, rows);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "rmsnorm rows launch");
 }
