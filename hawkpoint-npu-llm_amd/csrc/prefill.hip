@@ -392,47 +392,96 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
   }
 
   // D layout: lane holds rows 4 (lane / 16) + r, column lane % 16 of each block
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
+          const int n = n0 + wn + 16 * j + fr;
+          if (m >= a.M || n >= a.N) continue;
+          const int outs = PAIR ? 2 * a.N : a.N;
+          float* part = a.split_ws + ((size_t)blockIdx.y * a.M + m) * outs;
+          part[n] = acc[i][j][r];
+          if constexpr (PAIR) part[a.N + n] = accu[i][j][r];
+        }
+    return;
+  }
+  // The tile's outputs go through LDS (the operand buffers are free after
+  // the last barrier) so that they leave as 16-byte stores of 8 outputs of a
+  // row, with the residual rows read the same way.  LDS holds, per output,
+  // the bf16 that the epilogue's first rounding gives: the finished value
+  // for EPI_BF16 and EPI_SWIGLU, bf16(sum) (exact, the value the bias or the
+  // residual is added to) for EPI_BIAS and EPI_RESID.  The rounding points
+  // are those of the other GEMM kernels.
+  constexpr int ER = BN + 8;  // bf16 per LDS row of the tile
+  static_assert(BM * ER <= 2 * BM * kBRow, "the tile fits the A buffers");
+  uint16_t* ep = &As[0][0][0];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm + 16 * i + (lane >> 4) * 4 + r;
-        const int n = n0 + wn + 16 * j + fr;
-        if (m >= a.M || n >= a.N) continue;
+        const int ml = wm + 16 * i + (lane >> 4) * 4 + r, nl = wn + 16 * j + fr;
+        const int n = min(n0 + nl, a.N - 1);
         float v = acc[i][j][r];
-        if constexpr (SPLIT) {
-          const int outs = PAIR ? 2 * a.N : a.N;
-          float* part = a.split_ws + ((size_t)blockIdx.y * a.M + m) * outs;
-          part[n] = v;
-          if constexpr (PAIR) part[a.N + n] = accu[i][j][r];
-          continue;
-        }
         float u = 0.0f;
         if constexpr (PAIR) u = accu[i][j][r];
         if constexpr (W8) {
           v *= a.scale[n];
           if constexpr (PAIR) u *= a.scale[a.N + n];
         }
-        uint16_t* y = a.Y + (size_t)m * a.ldy + n;
-        switch (a.epi) {
-          case EPI_BF16:
-            *y = (uint16_t)f32_to_bf16(v);
-            break;
-          case EPI_BIAS:
-            *y = (uint16_t)f32_to_bf16(round_bf16(v) + a.bias[n]);
-            break;
-          case EPI_RESID:
-            *y = (uint16_t)f32_to_bf16(round_bf16(v) + bf16_to_f32(a.resid[(size_t)m * a.ldr + n]));
-            break;
-          case EPI_SWIGLU:
-            if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(v), round_bf16(u)));
-            break;
-          default:
-            break;
-        }
+        uint32_t y;
+        if constexpr (PAIR)
+          y = a.epi == EPI_SWIGLU ? f32_to_bf16(silu_mul(round_bf16(v), round_bf16(u))) : f32_to_bf16(v);
+        else
+          y = f32_to_bf16(v);
+        ep[ml * ER + nl] = (uint16_t)y;
       }
+  __syncthreads();
+  const bool add_bias = a.epi == EPI_BIAS, add_resid = a.epi == EPI_RESID;
+  for (int c = tid; c < BM * BN / 8; c += kThreads) {
+    const int ml = c / (BN / 8), nl = (c % (BN / 8)) * 8;
+    const int m = m0 + ml, n = n0 + nl;
+    if (m >= a.M || n >= a.N) continue;
+    const uint16_t* src = ep + ml * ER + nl;
+    uint16_t* y = a.Y + (size_t)m * a.ldy + n;
+    if (n + 8 > a.N) {  // a ragged last chunk of the row
+      for (int e = 0; e < a.N - n; ++e) {
+        float f = bf16_to_f32(src[e]);
+        if (add_bias) f = round_bf16(f + a.bias[n + e]);
+        if (add_resid) f = round_bf16(f + bf16_to_f32(a.resid[(size_t)m * a.ldr + n + e]));
+        y[e] = (uint16_t)f32_to_bf16(f);
+      }
+      continue;
+    }
+    u32x4 w = *reinterpret_cast<const u32x4*>(src);
+    if (add_bias || add_resid) {
+      float addend[8];
+      if (add_resid) {
+        const u32x4 rr = load16(a.resid + (size_t)m * a.ldr + n);
+        const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          addend[2 * q] = bf_lo(rw[q]);
+          addend[2 * q + 1] = bf_hi(rw[q]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) addend[e] = a.bias[n + e];
+      }
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = f32x2_to_bf16x2(bf_lo(ww[q]) + addend[2 * q], bf_hi(ww[q]) + addend[2 * q + 1]);
+      w = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    *reinterpret_cast<u32x4*>(y) = w;
+  }
 }
 
 // ---- slab GEMM: prompts of at most 64 tokens ----
