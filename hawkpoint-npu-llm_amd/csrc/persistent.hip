@@ -267,6 +267,10 @@ struct Shape {
   // without QKV/O rows (no weight prefetch queues ahead of their polls):
   // slices of xhs outputs, xhn of them
   static constexpr int xhs = 32, xhn = (H + xhs - 1) / xhs;
+  // bf16: QKV and O two rows per lane (prefetch_r2), still eight rows per
+  // wave, xq2 / xo2 chunks per row and lane
+  static constexpr int xq2 = (H / 8 + 15) / 16, xo2 = (AO / 8 + 15) / 16;
+  static constexpr bool xr2 = !W8 && xq.lpr == 8 && xo.lpr == 8 && 2 * (xq2 + xo2) <= kPf;
   // O rows take their residual from the Q stagers' copy of h
   static constexpr bool xa = xq.lpr && xo.lpr && xg.lpr == 16 && xq.nj + xo.nj <= kPf &&
                              xnq + HQ <= kXcdWg && xhn <= (kXcdWg - xnq) * kSW &&
@@ -579,7 +583,29 @@ __device__ __forceinline__ void fma8(const u32x4 w, const u32x4 x, float& a0, fl
   a1 = dot2(w.w, x.w, a1);
 }
 
-// Dot products of the prefetched row group with the staged x; every lane of
+// Two rows per lane (bf16): lanes 16 s .. 16 s + 15 of a wave take rows
+// 2 s and 2 s + 1 of its group of eight (`group`), chunks l + 16 j of both
+// rows (l = lane % 16), row 2 s in slots OFF + j and row 2 s + 1 in
+// OFF + NJ + j.  Both rows multiply the same x chunks, so a wave reads half
+// the x bytes from LDS that eight lanes per row read: when all eight waves of
+// a workgroup start a phase together, the LDS read bandwidth (128 bytes per
+// clock) is what the last wave waits for.
+template <int NJ, int OFF, int POL = kNT>
+__device__ __forceinline__ void prefetch_r2(u32x4 (&pf)[kPf], const void* W, int M, int K, int group,
+                                            bool live_wg) {
+  const int lane = threadIdx.x & 63;
+  const int l = lane & 15, row = group * 8 + 2 * (lane >> 4);
+  const __amdgpu_buffer_rsrc_t r = rsrc(W, M * K * 2);
+  const unsigned va = live_wg && row < M ? (unsigned)row * (unsigned)K * 2u + (unsigned)l * 16u : kOutside;
+  const unsigned vb = live_wg && row + 1 < M ? (unsigned)(row + 1) * (unsigned)K * 2u + (unsigned)l * 16u : kOutside;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    pf[OFF + j] = __builtin_amdgcn_raw_buffer_load_b128(r, va, j * 256, POL);
+    pf[OFF + NJ + j] = __builtin_amdgcn_raw_buffer_load_b128(r, vb, j * 256, POL);
+  }
+}
+
+
 // the row's LPR lanes ends with the sums.  All x chunks are read from LDS
 // first (a chunk past the row reads inside the staging buffer and is zeroed
 // by a select, not a branch), so the reads overlap instead of each paying
@@ -689,6 +715,29 @@ __device__ __forceinline__ void dot_group(const u32x4 (&pf)[kPf], const uint16_t
   }
 }
 
+// The sums of a prefetch_r2 group: ya for row 2 s, yb for row 2 s + 1, in
+// all 16 lanes of the pair.  Chunks past the row are zeroed through x.
+template <int NJ, int OFF>
+__device__ __forceinline__ void dot_r2(const u32x4 (&pf)[kPf], const uint16_t* xs, int K, float& ya, float& yb) {
+  static_assert((16 * NJ) * 8 <= kXMax, "x reads stay inside the staging buffer");
+  const int l = threadIdx.x & 15;
+  const int CH = K / 8;
+  u32x4 xv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) xv[j] = *reinterpret_cast<const u32x4*>(xs + (l + 16 * j) * 8);
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) xv[j] = l + 16 * j < CH ? xv[j] : zero;
+  float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    fma8(pf[OFF + j], xv[j], a0, a1);
+    fma8(pf[OFF + NJ + j], xv[j], b0, b1);
+  }
+  ya = wave_sum<16>(a0 + a1);
+  yb = wave_sum<16>(b0 + b1);
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float clipped = fminf(fmaxf(g, -80.0f), 80.0f);
   const float denom = 1.0f + expf(-clipped);
@@ -796,6 +845,13 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   // so every exponential below is one v_exp_f32 (2^x); the split-KV maxima
   // are kept in the same base
   const float scale = 0.125f * 1.44269504088896341f;
+  // A wave whose 32 slots all lie past the chunk's n live ones (short
+  // contexts) would compute zero scores' exponentials and a zero P @ V; it
+  // only publishes an empty (max, sum) pair, which leaves the LDS to the live
+  // waves, and the merge below reads the live slot groups only.
+  const bool wave_live = c.wave * 2 * kSlotsPV < n;
+  float mw = -INFINITY, sw = 0.0f;
+  if (wave_live) {
   float dot;
   {
     // q and k are bf16: v_dot2 on packed pairs, exact products, float sums
@@ -825,9 +881,9 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   // barrier then merges the eight waves by log-sum-exp.  (A wave without
   // live slots has max -inf and contributes exp(-inf) = 0; every chunk has a
   // live slot, so the merged max is finite.)
-  const float mw = wave_max64(sc);
+  mw = wave_max64(sc);
   const float e = live ? __builtin_amdgcn_exp2f(sc - mw) : 0.0f;
-  const float sw = wave_sum<64>(half == 0 ? e : 0.0f);  // each slot once
+  sw = wave_sum<64>(half == 0 ? e : 0.0f);  // each slot once
   if (half == 0) pr[si] = e;
   // the P @ V reads below take probabilities written by other lanes of this
   // wave only; a wave's LDS accesses complete in order
@@ -854,6 +910,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   }
   acc[gi * kHeadDim + 2 * dp] = o0;
   acc[gi * kHeadDim + 2 * dp + 1] = o1;
+  }
   if (c.lane == 0) {
     c.sm->red[0][c.wave] = mw;
     c.sm->red[1][c.wave] = sw;
@@ -872,7 +929,8 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   float o = 0.0f;
   if (tid < kHeadDim) {
 #pragma unroll
-    for (int k = 0; k < kGroupsPV; ++k) o = fmaf(acc[k * kHeadDim + tid], fw[k / kGroupsPerWave], o);
+    for (int k = 0; k < kGroupsPV; ++k)
+      if (k * kSlotsPV < n) o = fmaf(acc[k * kHeadDim + tid], fw[k / kGroupsPerWave], o);
   }
   if (nsplit == 1) o *= __builtin_amdgcn_rcpf(sum);  // a single chunk normalises here
   uint32_t* out = a.tattn + (size_t)h * kHeadDim;
@@ -971,7 +1029,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
 template <int RPW, int POL = kSc1, int NW = kCW>
 __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t word, bool row_lead,
                                              __amdgpu_buffer_rsrc_t tagged_buf, unsigned first,
-                                             int valid_rows, unsigned pad, bool then_load) {
+                                             int valid_rows, unsigned pad, bool then_load, int row_in_wave = -1) {
   static_assert(NW * RPW <= kCW * 16, "gather buffer too small");
   // word offsets into the tagged-activation buffer (a buffer store with a
   // 32-bit offset holds fewer registers than a 64-bit address)
@@ -979,7 +1037,7 @@ __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t wor
   uint32_t v = 0;
   unsigned old = 0;
   if (producer) {
-    const int sub = c.lane / (64 / RPW);
+    const int sub = row_in_wave >= 0 ? row_in_wave : c.lane / (64 / RPW);
     if (row_lead) c.sm->out_val[c.wave * RPW + sub] = word;
     if (c.lane == 0) old = atomicAdd(&c.sm->out_count, 1u);
     old = __shfl(old, 0, 64);
@@ -1561,14 +1619,34 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
   if (attn) {
     constexpr PhaseCfg Q = S::xq, O = S::xo;
     // register slots: Q rows from 0, O rows after them; W8 rows are loaded
-    // into the upper half of twice their slots and widened there (widen_w8)
+    // into the upper half of twice their slots and widened there (widen_w8);
+    // bf16 rows two per lane (R2: prefetch_r2, dot_r2)
+    constexpr bool R2 = S::xr2;
     constexpr int WQ = S::W8 ? 2 : 1;
-    constexpr int RQ = 64 / Q.lpr, RO = 64 / O.lpr, OFF_O = WQ * Q.nj;
+    constexpr int RQ = 64 / Q.lpr, RO = 64 / O.lpr, OFF_O = R2 ? 2 * S::xq2 : WQ * Q.nj;
     constexpr int LQ = S::W8 ? Q.nj : 0, LO = OFF_O + (S::W8 ? O.nj : 0);  // where the loads land
+    static_assert(!R2 || (RQ == 8 && RO == 8), "two rows per lane keep eight rows per wave");
     const bool is_q = rank < S::xnq, is_o = rank < S::xno;
-    const int row_q = c.gw * RQ + c.lane / Q.lpr, row_o = c.gw * RO + c.lane / O.lpr;
+    // R2: lanes 0 and 1 of each 16-lane pair hold its two rows' outputs
+    const int sub2 = 2 * (c.lane >> 4) + (c.lane & 1);
+    const int row_q = R2 ? c.gw * 8 + sub2 : c.gw * RQ + c.lane / Q.lpr;
+    const int row_o = R2 ? c.gw * 8 + sub2 : c.gw * RO + c.lane / O.lpr;
     const int fo = rank * kPW * RO;
-    const bool lq = c.lane % Q.lpr == 0, lo = c.lane % O.lpr == 0;
+    const bool lq = R2 ? (c.lane & 15) < 2 : c.lane % Q.lpr == 0;
+    const bool lo = R2 ? (c.lane & 15) < 2 : c.lane % O.lpr == 0;
+    const int sub_q = R2 ? sub2 : -1;
+    auto prefetch_q = [&](const PersistentLayer& w, bool live) {
+      if constexpr (R2)
+        prefetch_r2<S::xq2, 0>(pf, w.qkv, S::QKV, S::H, c.gw, live);
+      else
+        prefetch<Q.lpr, Q.nj, false, LQ, S::EB>(pf, w.qkv, S::QKV, S::H, c.gw, live);
+    };
+    auto prefetch_o = [&](const PersistentLayer& w, bool live) {
+      if constexpr (R2)
+        prefetch_r2<S::xo2, OFF_O>(pf, w.o, S::H, S::AO, c.gw, live);
+      else
+        prefetch<O.lpr, O.nj, false, LO, S::EB>(pf, w.o, S::H, S::AO, c.gw, live);
+    };
     const int res_o = min(row_o, S::H - 1);
     const unsigned bias_off = is_q && row_q < S::QKV ? (unsigned)row_q * 4u : kOutside;
     const bool pq = is_q, po = is_o;
@@ -1580,8 +1658,8 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       sq = row_scale<Q.lpr>(sm.layers[0].qkv_scale, S::QKV, c.gw, pq);
       so = row_scale<O.lpr>(sm.layers[0].o_scale, S::H, c.gw, po);
     }
-    prefetch<Q.lpr, Q.nj, false, LQ, S::EB>(pf, sm.layers[0].qkv, S::QKV, S::H, c.gw, pq);
-    prefetch<O.lpr, O.nj, false, LO, S::EB>(pf, sm.layers[0].o, S::H, S::AO, c.gw, po);
+    prefetch_q(sm.layers[0], pq);
+    prefetch_o(sm.layers[0], po);
     float bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                  bias_rsrc<S>(sm.layers[0].qkv_bias), bias_off, 0, 0));
     for (int l = 0; l < L; ++l) {
@@ -1614,12 +1692,18 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
       {  // all eight waves; the rows go straight to XCD 0's L2 (only the
          // attention tasks there poll them): each row's first lane stores it,
          // the other lanes the wave's pad word, one store per wave
-        dot_group<Q.lpr, Q.nj, false, 0, S::EB, S::W8>(pf, sm.xs[buf], S::H, acc, accu);
+        if constexpr (R2) {
+          float ya, yb;
+          dot_r2<S::xq2, 0>(pf, sm.xs[buf], S::H, ya, yb);
+          acc = (c.lane & 1) ? yb : ya;
+        } else {
+          dot_group<Q.lpr, Q.nj, false, 0, S::EB, S::W8>(pf, sm.xs[buf], S::H, acc, accu);
+        }
         if constexpr (S::W8) acc *= sq;
         const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
         if constexpr (LONG) {  // to the MLP workgroups: gathered, one writer per workgroup
           publish_rows<RQ, kSc1, kPW>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + rank * kPW * RQ,
-                                      S::QKV - rank * kPW * RQ, pad, true);
+                                      S::QKV - rank * kPW * RQ, pad, true, sub_q);
         } else {
           const unsigned dst = is_q && lq && row_q < S::QKV ? o_qkv + (unsigned)row_q : pad;
           __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_of(ep + 1)), tbuf, dst * 4u, 0, 0);
@@ -1642,10 +1726,16 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
       }
       {  // all eight waves
-        dot_group<O.lpr, O.nj, false, OFF_O, S::EB, S::W8>(pf, sm.xs[buf], S::AO, acc, accu);
+        if constexpr (R2) {
+          float ya, yb;
+          dot_r2<S::xo2, OFF_O>(pf, sm.xs[buf], S::AO, ya, yb);
+          acc = (c.lane & 1) ? yb : ya;
+        } else {
+          dot_group<O.lpr, O.nj, false, OFF_O, S::EB, S::W8>(pf, sm.xs[buf], S::AO, acc, accu);
+        }
         if constexpr (S::W8) acc *= so;
         publish_rows<RO, kSc1, kPW>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
-                                    lo, tbuf, o_h1 + fo, S::H - fo, pad, true);
+                                    lo, tbuf, o_h1 + fo, S::H - fo, pad, true, sub_q);
       }
       if (is_o) buf ^= 1;
       // the next layer's QKV and O rows go out once this layer's attention
@@ -1656,10 +1746,10 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         sq = row_scale<Q.lpr>(nx.qkv_scale, S::QKV, c.gw, pq && more);
         so = row_scale<O.lpr>(nx.o_scale, S::H, c.gw, po && more);
       }
-      prefetch<Q.lpr, Q.nj, false, LQ, S::EB>(pf, nx.qkv, S::QKV, S::H, c.gw, pq && more);
+      prefetch_q(nx, pq && more);
       bias_q = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              bias_rsrc<S>(nx.qkv_bias), bias_off, 0, 0));
-      prefetch<O.lpr, O.nj, false, LO, S::EB>(pf, nx.o, S::H, S::AO, c.gw, po && more);
+      prefetch_o(nx, po && more);
       // ---- h = h1 + down(act) from the MLP XCDs' partials, on the stager
       // waves of the workgroups without rows (an abandoned wait ends every
       // later wait of the launch through the error word) ----

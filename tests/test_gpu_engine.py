@@ -276,8 +276,9 @@ def test_xcd_split_two_chunk_attention():
 @pytest.mark.parametrize("w8", [False, True], ids=["bf16", "w8"])
 def test_xcd_split_agrees_with_undivided_step(monkeypatch, w8):
     """The split and undivided kernels sum the QKV and O rows over different
-    lane groups (8 lanes per row against 16 and 64), so they agree to float
-    tolerance; the greedy ids agree up to a near-tie.  The second run also
+    lane groups (split: 16 lanes per pair of bf16 rows, 8 lanes per W8 row;
+    undivided: 16 and 64 lanes per row), so they agree to float tolerance;
+    the greedy ids agree up to a near-tie.  The second run also
     alternates the two split forms (attention on XCD 0 below 768, on the MLP
     XCDs above), which share tags, epochs and flags with each other and with
     the undivided kernel from launch to launch."""
