@@ -58,6 +58,8 @@
 //   reports the error and clears the tags and flags.
 //
 // Rounding points are those of the separate kernels (gemv.hip, attention.hip).
+#include <type_traits>
+
 #include "hk_common.h"
 #include "hk_internal.h"
 
@@ -928,9 +930,14 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   constexpr int kGroupsPerWave = 64 / kHalf;
   float o = 0.0f;
   if (tid < kHeadDim) {
+    // every group's word is read at once (no branch between the reads, so
+    // they overlap); groups past the live slots hold stale values and are
+    // replaced by zero before the product
+    float av[kGroupsPV];
 #pragma unroll
-    for (int k = 0; k < kGroupsPV; ++k)
-      if (k * kSlotsPV < n) o = fmaf(acc[k * kHeadDim + tid], fw[k / kGroupsPerWave], o);
+    for (int k = 0; k < kGroupsPV; ++k) av[k] = acc[k * kHeadDim + tid];
+#pragma unroll
+    for (int k = 0; k < kGroupsPV; ++k) o = fmaf(k * kSlotsPV < n ? av[k] : 0.0f, fw[k / kGroupsPerWave], o);
   }
   if (nsplit == 1) o *= __builtin_amdgcn_rcpf(sum);  // a single chunk normalises here
   uint32_t* out = a.tattn + (size_t)h * kHeadDim;
@@ -1040,7 +1047,7 @@ __device__ __forceinline__ void publish_rows(Ctx& c, bool producer, uint32_t wor
     const int sub = row_in_wave >= 0 ? row_in_wave : c.lane / (64 / RPW);
     if (row_lead) c.sm->out_val[c.wave * RPW + sub] = word;
     if (c.lane == 0) old = atomicAdd(&c.sm->out_count, 1u);
-    old = __shfl(old, 0, 64);
+    old = __builtin_amdgcn_readlane(old, 0);
     if (old % NW == NW - 1 && c.lane < NW * RPW && c.lane < valid_rows) {
       v = c.sm->out_val[c.lane];
       dst = first + c.lane;
@@ -1078,42 +1085,59 @@ __device__ __forceinline__ void lm_head_phase(Ctx& c, u32x4 (&pf)[kPf], int buf,
     __syncthreads();
     return sm.abort == 0;
   };
-  // ---- H: LM head over all eight waves, double-buffered row groups; every
-  // wave runs the same (even) number of iterations, past-the-end groups read
-  // zero and store to the pad ----
+  // ---- H: LM head over all eight waves.  Wave w of the grid takes row
+  // groups w, w + stride, ...; the register slots hold a ring of D row groups
+  // (D - 1 of them in flight while one is multiplied), and the compute waves
+  // request the first D - 1 before they wait for the final h.  Every wave
+  // runs the same number of groups (a multiple of D); past-the-end groups
+  // read zero and store to the pad ----
   constexpr int HL = S::head_lpr, HNJ = S::head_nj, HRPW = 64 / HL;
+  constexpr int D = kPf / HNJ >= 4 ? 4 : kPf / HNJ;
+  static_assert(D >= 2, "LM head rows too long for two row groups in flight");
   const int groups = (a.vocab + HRPW - 1) / HRPW;
   const int stride = kPersistentGrid * kPW;
   const int iters = (groups + stride - 1) / stride;
   float* const lpad = a.logits + a.vocab + c.wg * kPW + c.wave;
-  u32x4 wb[kPf];
-  int grp = c.wg * kPW + c.wave;
-  if (!stager) prefetch<HL, HNJ, false, 0, 2, kHeadPol>(pf, a.lm_head, a.vocab, S::H, grp, true);
+  const int grp0 = c.wg * kPW + c.wave;
+  auto head_load = [&](auto slot, int k) {  // row group k of this wave into ring slot `slot`
+    prefetch<HL, HNJ, false, decltype(slot)::value * HNJ, 2, kHeadPol>(pf, a.lm_head, a.vocab, S::H,
+                                                                        grp0 + k * stride, true);
+  };
+  auto first_loads = [&]() {
+    head_load(std::integral_constant<int, 0>{}, 0);
+    if constexpr (D > 2) head_load(std::integral_constant<int, 1>{}, 1);
+    if constexpr (D > 3) head_load(std::integral_constant<int, 2>{}, 2);
+  };
+  if (!stager) first_loads();
   {
     bool ok = true;
     if (stager) ok = stage_wave<S::H, true, false>(c, a.th, tag_of(ep_layers), a.final_norm, sm.xs[buf], nullptr);
     if (!handoff(ok)) return;
     normalise_staged<S::H>(c, sm.xs[buf], a.eps);
   }
-  if (stager) prefetch<HL, HNJ, false, 0, 2, kHeadPol>(pf, a.lm_head, a.vocab, S::H, grp, true);
+  if (stager) first_loads();
   const uint16_t* xh = sm.xs[buf];
   unsigned long long best = 0ull;
   const int sub = c.lane / HL;
-  auto finish = [&](int g) {
-    const int row = g * HRPW + sub;
+  auto finish = [&](int k) {
+    const int row = (grp0 + k * stride) * HRPW + sub;
     const bool valid = row < a.vocab;
     stg(valid ? a.logits + row : lpad, acc);
     best = umax64(best, valid ? argmax_key(acc, (uint32_t)row) : 0ull);
   };
-  for (int it = 0; it < iters; it += 2) {
-    prefetch<HL, HNJ, false, 0, 2, kHeadPol>(wb, a.lm_head, a.vocab, S::H, grp + stride, true);
-    dot_group<HL, HNJ, false, 0>(pf, xh, S::H, acc, accu);
-    finish(grp);
-    grp += stride;
-    prefetch<HL, HNJ, false, 0, 2, kHeadPol>(pf, a.lm_head, a.vocab, S::H, grp + stride, true);
-    dot_group<HL, HNJ, false, 0>(wb, xh, S::H, acc, accu);
-    finish(grp);
-    grp += stride;
+  // step d of a round: request group k + D - 1 into the slot group k - 1
+  // left, then multiply group k (slot d)
+  auto ring_step = [&](auto d, int k) {
+    constexpr int DD = decltype(d)::value;
+    head_load(std::integral_constant<int, (DD + D - 1) % D>{}, k + D - 1);
+    dot_group<HL, HNJ, false, DD * HNJ>(pf, xh, S::H, acc, accu);
+    finish(k);
+  };
+  for (int k = 0; k < iters; k += D) {
+    ring_step(std::integral_constant<int, 0>{}, k);
+    ring_step(std::integral_constant<int, 1>{}, k + 1);
+    if constexpr (D > 2) ring_step(std::integral_constant<int, 2>{}, k + 2);
+    if constexpr (D > 3) ring_step(std::integral_constant<int, 3>{}, k + 3);
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) best = umax64(best, shfl_xor_u64(best, m));
@@ -1575,6 +1599,12 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
   }
   const PersistentArgs& a = args;
   const int L = a.layers;
+  // the epoch, token and position go out with the layer table's loads, so
+  // their latencies overlap
+  unsigned* my_flag = a.progress + (size_t)c.wg * kFlagStride;
+  const unsigned base = ld_c32(my_flag);
+  const int token = ldg(&a.ctrl->token);
+  const int p = ldg(&a.ctrl->position);
   {
     constexpr int kWords = sizeof(PersistentLayer) / 8;
     const unsigned long long* src = reinterpret_cast<const unsigned long long*>(a.w);
@@ -1582,7 +1612,6 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     for (int i = threadIdx.x; i < L * kWords; i += kPT) dst[i] = ldg(src + i);
   }
   __syncthreads();
-  unsigned* my_flag = a.progress + (size_t)c.wg * kFlagStride;
   // the XCD-local hand-offs are only coherent if the workgroups that share
   // them share an L2: leave (the launch is abandoned) if this workgroup is
   // not on the XCD the split assumes
@@ -1592,9 +1621,6 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     if (threadIdx.x == 0) give_up(a);
     return;
   }
-  const unsigned base = ld_c32(my_flag);
-  const int token = ldg(&a.ctrl->token);
-  const int p = ldg(&a.ctrl->position);
   const uint16_t* x0 = token >= 0 ? a.embed + (size_t)min(token, a.vocab - 1) * S::H : a.h;
   const bool attn = c.wg % kXcds == 0;
   // rank of the workgroup within its side, and its compute waves' indices
@@ -1726,6 +1752,10 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!handoff(ok)) return;
       }
       {  // all eight waves
+        // the residual goes out before the dot products' LDS reads, so its
+        // latency overlaps them
+        const float res_h = sm.raw_h[res_o];
+        asm volatile("" ::: "memory");
         if constexpr (R2) {
           float ya, yb;
           dot_r2<S::xo2, OFF_O>(pf, sm.xs[buf], S::AO, ya, yb);
@@ -1734,7 +1764,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
           dot_group<O.lpr, O.nj, false, OFF_O, S::EB, S::W8>(pf, sm.xs[buf], S::AO, acc, accu);
         }
         if constexpr (S::W8) acc *= so;
-        publish_rows<RO, kSc1, kPW>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + sm.raw_h[res_o]), tag_of(ep + 3)),
+        publish_rows<RO, kSc1, kPW>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + res_h), tag_of(ep + 3)),
                                     lo, tbuf, o_h1 + fo, S::H - fo, pad, true, sub_q);
       }
       if (is_o) buf ^= 1;
