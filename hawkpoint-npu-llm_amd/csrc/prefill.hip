@@ -519,18 +519,20 @@ __device__ __forceinline__ int rope_row(int s, int r) {
 
 // One batch of a wave's K steps: weight fragments (raw int8 for W8, widened
 // just before the product) and the token fragments of every block.
-template <bool PAIR, bool W8, int B>
+template <bool PAIR, bool W8, int B, int NB>
 struct SlabBatch {
   using WRaw = typename std::conditional<W8, u32x2_t, u32x4>::type;
   WRaw w[B], u[PAIR ? B : 1];
-  u32x4 x[B][kSlabBlocks];
+  u32x4 x[B][NB];
 };
 
 // WAVES 16 for K up to 16 batches of steps; WAVES kSlabLongWaves for longer
 // K (non-normalised A): each wave then requests the weights of up to
 // kSlabWPre of its steps at once (one HBM latency for all of them) and
-// streams the token fragments two steps at a time, double buffered.
-template <bool PAIR, bool NORM, bool W8, int WAVES>
+// streams the token fragments two steps at a time, double buffered.  NB: the
+// prompt's 16-token blocks (a 40-token prompt takes three: a quarter fewer
+// token loads, products and LDS sums than the four a 64-token prompt needs).
+template <bool PAIR, bool NORM, bool W8, int WAVES, int NB = kSlabBlocks>
 __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a) {
   constexpr int kSlabWaves = WAVES;
   constexpr int P = PAIR ? 2 : 1;
@@ -538,8 +540,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   // SwiGLU pairs without the norm keep one step per batch (two batches of
   // two would not fit the registers of 16 waves)
   constexpr int B = PAIR && !NORM ? 1 : kSlabBatch;
-  using Batch = SlabBatch<PAIR, W8, B>;
-  __shared__ f32x4 red[kSlabWaves][P * kSlabBlocks][64];
+  using Batch = SlabBatch<PAIR, W8, B, NB>;
+  __shared__ f32x4 red[kSlabWaves][P * NB][64];
   __shared__ float ssq[NORM ? kSlabWaves : 1][kSlabMaxTokens];
   __shared__ float inv_s[kSlabMaxTokens];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -565,9 +567,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   const int nrow = native ? n0 + fr : wrow;
   const unsigned wofs = wrow < N ? wpiece(nrow) : kSlabOutside;
   const unsigned uofs = wrow < N ? wpiece(nrow + N) : kSlabOutside;
-  unsigned aofs[kSlabBlocks];
+  unsigned aofs[NB];
 #pragma unroll
-  for (int b = 0; b < kSlabBlocks; ++b) {
+  for (int b = 0; b < NB; ++b) {
     const int t = 16 * b + fr;
     aofs[b] = t >= M ? kSlabOutside
               : a.kblock ? (unsigned)(((fk >> 3) * M + t) * 16) : (unsigned)(t * a.lda + fk) * 2u;
@@ -595,7 +597,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
         if constexpr (PAIR) bt.u[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, uo, 0, 2);
       }
 #pragma unroll
-      for (int b = 0; b < kSlabBlocks; ++b)
+      for (int b = 0; b < NB; ++b)
         bt.x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, live ? aofs[b] + akm * k0 : kSlabOutside, 0, 0);
     }
   };
@@ -607,9 +609,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
       return __builtin_bit_cast(bf16x8, r);
   };
 
-  f32x4 acc[kSlabBlocks], accu[PAIR ? kSlabBlocks : 1];
+  f32x4 acc[NB], accu[PAIR ? NB : 1];
 #pragma unroll
-  for (int b = 0; b < kSlabBlocks; ++b) {
+  for (int b = 0; b < NB; ++b) {
     acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (PAIR) accu[b] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -619,7 +621,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
       const bf16x8 w = widen(bt.w[i]);
       const bf16x8 wu = PAIR ? widen(bt.u[i]) : w;
 #pragma unroll
-      for (int b = 0; b < kSlabBlocks; ++b) {  // blocks past the last token hold zeros
+      for (int b = 0; b < NB; ++b) {  // blocks past the last token hold zeros
         const bf16x8 xa = __builtin_bit_cast(bf16x8, bt.x[i][b]);
         acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, w, acc[b], 0, 0, 0);
         if constexpr (PAIR) accu[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wu, accu[b], 0, 0, 0);
@@ -640,7 +642,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
     // squares of this lane's fragments, per token row; the four lanes of a
     // row hold its four 8-wide k groups
 #pragma unroll
-    for (int b = 0; b < kSlabBlocks; ++b) {
+    for (int b = 0; b < NB; ++b) {
       float sq = 0.0f;
 #pragma unroll
       for (int i = 0; i < B; ++i) sq += sq8(bt.x[i][b]);
@@ -657,7 +659,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
     }
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < kSlabBlocks; ++b) {
+    for (int b = 0; b < NB; ++b) {
       const float inv = inv_s[16 * b + fr];
 #pragma unroll
       for (int i = 0; i < B; ++i) bt.x[i][b] = norm8(bt.x[i][b], inv, g[i]);
@@ -707,23 +709,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
         else
           wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2);
       }
-      u32x4 x0[2][kSlabBlocks], x1[2][kSlabBlocks];
-      auto load_x = [&](u32x4 (&x)[2][kSlabBlocks], int j0) {
+      u32x4 x0[2][NB], x1[2][NB];
+      auto load_x = [&](u32x4 (&x)[2][NB], int j0) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int j = j0 + i;
           const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
 #pragma unroll
-          for (int b = 0; b < kSlabBlocks; ++b)
+          for (int b = 0; b < NB; ++b)
             x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, j < mine ? aofs[b] + akm * k0 : kSlabOutside, 0, 0);
         }
       };
-      auto mul_x = [&](const u32x4 (&x)[2][kSlabBlocks], int i0) {
+      auto mul_x = [&](const u32x4 (&x)[2][NB], int i0) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const bf16x8 w = widen(wv[i0 + i]);
 #pragma unroll
-          for (int b = 0; b < kSlabBlocks; ++b)
+          for (int b = 0; b < NB; ++b)
             acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x[i][b]), w, acc[b], 0, 0, 0);
         }
       };
@@ -741,9 +743,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   }
 
 #pragma unroll
-  for (int b = 0; b < kSlabBlocks; ++b) {
+  for (int b = 0; b < NB; ++b) {
     red[wave][b][lane] = acc[b];
-    if constexpr (PAIR) red[wave][kSlabBlocks + b][lane] = accu[b];
+    if constexpr (PAIR) red[wave][NB + b][lane] = accu[b];
   }
   __syncthreads();
 
@@ -758,7 +760,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
 #pragma unroll
     for (int w = 0; w < kSlabWaves; ++w) {
       x += red[w][b][l][r];
-      if constexpr (PAIR) u += red[w][kSlabBlocks + b][l][r];
+      if constexpr (PAIR) u += red[w][NB + b][l][r];
     }
     if constexpr (W8) {
       x *= a.scale[n];
@@ -1060,20 +1062,40 @@ size_t split_ws_need(int M, int N, int K, bool pair) {
 }
 
 namespace {
-template <bool PAIR, bool W8>
-int launch_slab(const PrefillGemmArgs& a, hipStream_t stream) {
+// NB: 16-token blocks of the prompt
+template <bool PAIR, bool W8, int NB>
+void launch_slab_nb(const PrefillGemmArgs& a, hipStream_t stream) {
   const dim3 grid((a.N + 15) / 16);
   const bool long_k = a.K / 32 > 16 * kSlabBatch;
-  if (a.gamma)
-    hipLaunchKernelGGL((gemm_slab_kernel<PAIR, true, W8, 16>), grid, dim3(16 * 64), 0, stream, a);
-  else if constexpr (!PAIR) {
+  if (a.gamma) {
+    hipLaunchKernelGGL((gemm_slab_kernel<PAIR, true, W8, 16, NB>), grid, dim3(16 * 64), 0, stream, a);
+  } else if constexpr (!PAIR) {
     if (long_k)
-      hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, kSlabLongWaves>), grid, dim3(kSlabLongWaves * 64), 0,
-                         stream, a);
+      hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, kSlabLongWaves, NB>), grid, dim3(kSlabLongWaves * 64),
+                         0, stream, a);
     else
-      hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, 16>), grid, dim3(16 * 64), 0, stream, a);
+      hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, 16, NB>), grid, dim3(16 * 64), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((gemm_slab_kernel<true, false, W8, 16>), grid, dim3(16 * 64), 0, stream, a);
+    hipLaunchKernelGGL((gemm_slab_kernel<true, false, W8, 16, NB>), grid, dim3(16 * 64), 0, stream, a);
+  }
+}
+
+template <bool PAIR, bool W8>
+int launch_slab(const PrefillGemmArgs& a, hipStream_t stream) {
+  static_assert(kSlabBlocks == 4, "one instantiation per block count");
+  switch ((a.M + 15) / 16) {
+    case 1:
+      launch_slab_nb<PAIR, W8, 1>(a, stream);
+      break;
+    case 2:
+      launch_slab_nb<PAIR, W8, 2>(a, stream);
+      break;
+    case 3:
+      launch_slab_nb<PAIR, W8, 3>(a, stream);
+      break;
+    default:
+      launch_slab_nb<PAIR, W8, 4>(a, stream);
+      break;
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "slab gemm launch");

@@ -173,12 +173,14 @@ def test_prefill_continues_from_cached_prefix():
         engine.close()
 
 
-@pytest.mark.parametrize("n,w8", [(1, False), (16, False), (17, False), (63, False), (64, False), (65, False),
-                                  (130, False), (1, True), (64, True)])
+@pytest.mark.parametrize("n,w8", [(1, False), (16, False), (17, False), (32, False), (33, False), (48, False),
+                                  (49, False), (63, False), (64, False), (65, False), (130, False), (1, True),
+                                  (17, True), (40, True), (64, True)])
 def test_prefill_lengths_around_the_slab_gemm(n, w8):
     """Chunks of up to 64 tokens run the slab GEMMs (one workgroup per 16
     outputs over all of K, RMSNorm applied while loading A, weights from the
-    MFMA-native copies); 65 and more take the tiled GEMMs.  Last-token logits
+    MFMA-native copies, compiled for one to four 16-token blocks: the lengths
+    cover each block count's edges); 65 and more take the tiled GEMMs.  Last-token logits
     and KV slots of a 2-layer Qwen2.5-0.5B-shape model with random RMSNorm
     gains against the oracle's prefill at each length, and a second prefill
     of the same prompt bit for bit equal to the first (every sum is added in
