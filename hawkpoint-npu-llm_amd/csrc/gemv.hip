@@ -11,7 +11,8 @@
 // non-temporal loads; the first group's loads are issued *before* the
 // prologue, so the RMSNorm/x staging latency hides under the HBM fetch, and a
 // wave that owns several groups loads the next while reducing the current.
-// x lives in LDS as float32.  Partial sums are reduced across the LPR lanes
+// x lives in LDS as float32 (for int8 rows also as packed bf16 pairs, for
+// v_dot2 on the widened weights).  Partial sums are reduced across the LPR lanes
 // with butterfly shuffles.  The LM-head form also keeps a running argmax key
 // per workgroup (no atomics); launch_argmax_finalize reduces those keys.
 //
@@ -35,7 +36,8 @@ constexpr unsigned kGemvOutside = 0x7ffffff0u;  // a byte offset past every buff
 // Stage x (optionally RMS-normalised) into LDS as float32.
 // RMSNorm follows cpu_backend.py:71-76: v = f32(bf16 x); mean of v*v in f32;
 // inv = 1 / sqrt(mean + eps); out = bf16((v * inv) * gamma).
-__device__ __forceinline__ void stage_x(const GemvArgs& a, float* xs, float* red) {
+// With xp, also as packed bf16 pairs (every staged value is bf16-exact).
+__device__ __forceinline__ void stage_x(const GemvArgs& a, float* xs, float* red, uint32_t* xp = nullptr) {
   const int tid = threadIdx.x;
   const int K = a.K;
   const uint16_t* x = a.x;
@@ -55,6 +57,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, float* xs, float* red
     const float v0 = bf_lo(w), v1 = bf_hi(w);
     xs[2 * i] = v0;
     xs[2 * i + 1] = v1;
+    if (xp) xp[i] = w;
     if (copy) reinterpret_cast<uint32_t*>(a.x_copy)[i] = w;
     ss += v0 * v0;
     ss += v1 * v1;
@@ -71,38 +74,47 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, float* xs, float* red
   const uint32_t* g2 = reinterpret_cast<const uint32_t*>(a.gamma);
   for (int i = tid; i < K / 2; i += kThreads) {
     const uint32_t g = ldg(g2 + i);
-    xs[2 * i] = round_bf16((xs[2 * i] * inv) * bf_lo(g));
-    xs[2 * i + 1] = round_bf16((xs[2 * i + 1] * inv) * bf_hi(g));
+    const float n0 = round_bf16((xs[2 * i] * inv) * bf_lo(g)), n1 = round_bf16((xs[2 * i + 1] * inv) * bf_hi(g));
+    xs[2 * i] = n0;
+    xs[2 * i + 1] = n1;
+    if (xp) xp[i] = (__float_as_uint(n0) >> 16) | (__float_as_uint(n1) & 0xffff0000u);
   }
 }
 
-template <bool W8>
-__device__ __forceinline__ void fma_chunk(const u32x4 w, const float* xs, int c, float& a0,
-                                          float& a1) {
-  if constexpr (!W8) {
-    const float4* xv = reinterpret_cast<const float4*>(xs + c * 8);
-    const float4 p = xv[0], q = xv[1];
-    a0 = fmaf(bf_lo(w.x), p.x, a0);
-    a1 = fmaf(bf_hi(w.x), p.y, a1);
-    a0 = fmaf(bf_lo(w.y), p.z, a0);
-    a1 = fmaf(bf_hi(w.y), p.w, a1);
-    a0 = fmaf(bf_lo(w.z), q.x, a0);
-    a1 = fmaf(bf_hi(w.z), q.y, a1);
-    a0 = fmaf(bf_lo(w.w), q.z, a0);
-    a1 = fmaf(bf_hi(w.w), q.w, a1);
-  } else {
-    const float4* xv = reinterpret_cast<const float4*>(xs + c * 16);
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float4 p = xv[k];
-      const int32_t v = (int32_t)words[k];
-      a0 = fmaf((float)((v << 24) >> 24), p.x, a0);
-      a1 = fmaf((float)((v << 16) >> 24), p.y, a1);
-      a0 = fmaf((float)((v << 8) >> 24), p.z, a0);
-      a1 = fmaf((float)(v >> 24), p.w, a1);
-    }
-  }
+// Sixteen int8 weights (one chunk) times x as packed bf16 pairs (xp): each
+// weight pair widened exactly to a bf16 pair (i8pair_bf16), then
+// v_dot2_f32_bf16 (exact products, float32 sums) -- two VALU instructions per
+// weight, and half the LDS bytes of float32 x.
+typedef __bf16 gemv_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gemv_bf16x2, w), __builtin_bit_cast(gemv_bf16x2, x), c,
+                                         false);
+}
+__device__ __forceinline__ void dot_chunk_i8(const u32x4 w, const uint32_t* xp, int c, float& a0, float& a1) {
+  const u32x4 xa = *reinterpret_cast<const u32x4*>(xp + 8 * c);
+  const u32x4 xb = *reinterpret_cast<const u32x4*>(xp + 8 * c + 4);
+  a0 = dot2_bf16(i8pair_bf16(w.x, 0), xa.x, a0);
+  a1 = dot2_bf16(i8pair_bf16(w.x, 2), xa.y, a1);
+  a0 = dot2_bf16(i8pair_bf16(w.y, 0), xa.z, a0);
+  a1 = dot2_bf16(i8pair_bf16(w.y, 2), xa.w, a1);
+  a0 = dot2_bf16(i8pair_bf16(w.z, 0), xb.x, a0);
+  a1 = dot2_bf16(i8pair_bf16(w.z, 2), xb.y, a1);
+  a0 = dot2_bf16(i8pair_bf16(w.w, 0), xb.z, a0);
+  a1 = dot2_bf16(i8pair_bf16(w.w, 2), xb.w, a1);
+}
+
+// Eight bf16 weights (one chunk) times x as float32.
+__device__ __forceinline__ void fma_chunk(const u32x4 w, const float* xs, int c, float& a0, float& a1) {
+  const float4* xv = reinterpret_cast<const float4*>(xs + c * 8);
+  const float4 p = xv[0], q = xv[1];
+  a0 = fmaf(bf_lo(w.x), p.x, a0);
+  a1 = fmaf(bf_hi(w.x), p.y, a1);
+  a0 = fmaf(bf_lo(w.y), p.z, a0);
+  a1 = fmaf(bf_hi(w.y), p.w, a1);
+  a0 = fmaf(bf_lo(w.z), q.x, a0);
+  a1 = fmaf(bf_hi(w.z), q.y, a1);
+  a0 = fmaf(bf_lo(w.w), q.z, a0);
+  a1 = fmaf(bf_hi(w.w), q.w, a1);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -157,6 +169,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   extern __shared__ float smem[];
   float* xs = smem;
   float* red = smem + a.K;
+  uint32_t* xp = reinterpret_cast<uint32_t*>(smem + a.K + 8);  // W8: x as packed bf16 pairs
   __shared__ unsigned long long wave_keys[kWaves];
 
   constexpr int RPW = 64 / LPR;
@@ -180,10 +193,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   // group past the matrix takes an offset past the resource and reads zero.
   // With a branch around each load the compiler waited for all of them
   // (the next group's too) before the first product.  The host keeps the
-  // matrix below 2 GiB (32-bit offsets).
+  // matrix below 2 GiB (32-bit offsets).  (int8 rows keep the branches:
+  // measured, the branch-free form took their GEMVs 5-25% longer, all but
+  // the LM head's.)
   const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, (int)((PAIR ? 2 : 1) * pair_off));
-  // (int8 rows keep the branches: measured, the branch-free form took their
-  // GEMVs 10-25% longer)
   auto load = [&](int g, int base, u32x4 (&w)[NJ], u32x4 (&u)[PAIR ? NJ : 1]) {
     const int row = g * RPW + sub;
     const bool live = g < groups && row < a.M;
@@ -196,34 +209,32 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         w[j] = ok ? load_stream16(wrow + (size_t)c * 16) : zero;
         if constexpr (PAIR) u[j] = ok ? load_stream16(wrow + pair_off + (size_t)c * 16) : zero;
       }
-    } else {
-      const unsigned rofs = (unsigned)((size_t)(live ? row : 0) * row_bytes);
+      return;
+    }
+    const unsigned rofs = (unsigned)((size_t)(live ? row : 0) * row_bytes);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int c = base + l + j * LPR;
-        const unsigned off = live && c < CH ? rofs + (unsigned)c * 16u : kGemvOutside;
-        w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2);
-        if constexpr (PAIR)
-          u[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, off == kGemvOutside ? off : off + (unsigned)pair_off, 0, 2);
-      }
+    for (int j = 0; j < NJ; ++j) {
+      const int c = base + l + j * LPR;
+      const unsigned off = live && c < CH ? rofs + (unsigned)c * 16u : kGemvOutside;
+      w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2);
+      if constexpr (PAIR)
+        u[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, off == kGemvOutside ? off : off + (unsigned)pair_off, 0, 2);
     }
   };
-  // bf16: chunks past the row hold zero weights and their x index is
-  // clamped, so the products read a finite x and need no branch
+  // chunks past the row hold zero weights and their x index is clamped, so
+  // the products read a finite x and need no branch
   auto dot = [&](int base, const u32x4 (&w)[NJ], const u32x4 (&u)[PAIR ? NJ : 1], float& a0,
                  float& a1, float& b0, float& b1) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int c = base + l + j * LPR;
+      const int cx = c < CH ? c : 0;
       if constexpr (W8) {
-        if (c < CH) {
-          fma_chunk<W8>(w[j], xs, c, a0, a1);
-          if constexpr (PAIR) fma_chunk<W8>(u[j], xs, c, b0, b1);
-        }
+        dot_chunk_i8(w[j], xp, cx, a0, a1);
+        if constexpr (PAIR) dot_chunk_i8(u[j], xp, cx, b0, b1);
       } else {
-        const int cx = c < CH ? c : 0;
-        fma_chunk<W8>(w[j], xs, cx, a0, a1);
-        if constexpr (PAIR) fma_chunk<W8>(u[j], xs, cx, b0, b1);
+        fma_chunk(w[j], xs, cx, a0, a1);
+        if constexpr (PAIR) fma_chunk(u[j], xs, cx, b0, b1);
       }
     }
   };
@@ -231,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   unsigned long long best = 0ull;
   int g = blockIdx.x * kWaves + wave;
   load(g, 0, wa, ua);
-  stage_x(a, xs, red);
+  stage_x(a, xs, red, W8 ? xp : nullptr);
   __syncthreads();
 
   if (single_pass) {
@@ -480,7 +491,8 @@ int resident_per_cu(size_t lds) {
 template <int LPR, int NJ, bool W8, bool PAIR>
 int launch_cfg(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
   constexpr int RPW = 64 / LPR;
-  const size_t lds = (size_t)(a.K + 8) * sizeof(float);
+  // x as float32 and a reduction scratch; W8 also x as packed bf16 pairs
+  const size_t lds = (size_t)(a.K + 8) * sizeof(float) + (W8 ? (size_t)a.K * 2 : 0);
   const int needed = ((a.M + RPW - 1) / RPW + kWaves - 1) / kWaves;
   int cap = cu_count() * resident_per_cu<LPR, NJ, W8, PAIR>(lds);
   if (cap > kMaxPartialKeys) cap = kMaxPartialKeys;
