@@ -11,8 +11,9 @@
 // non-temporal loads; the first group's loads are issued *before* the
 // prologue, so the RMSNorm/x staging latency hides under the HBM fetch, and a
 // wave that owns several groups loads the next while reducing the current.
-// x lives in LDS as float32 (for int8 rows also as packed bf16 pairs, for
-// v_dot2 on the widened weights).  Partial sums are reduced across the LPR lanes
+// x lives in LDS as packed bf16 pairs (and float32 for the RMSNorm
+// prologue); the dot products run on v_dot2_f32_bf16 (int8 weights widened
+// to bf16 pairs first).  Partial sums are reduced across the LPR lanes
 // with butterfly shuffles.  The LM-head form also keeps a running argmax key
 // per workgroup (no atomics); launch_argmax_finalize reduces those keys.
 //
@@ -103,18 +104,13 @@ __device__ __forceinline__ void dot_chunk_i8(const u32x4 w, const uint32_t* xp, 
   a1 = dot2_bf16(i8pair_bf16(w.w, 2), xb.w, a1);
 }
 
-// Eight bf16 weights (one chunk) times x as float32.
-__device__ __forceinline__ void fma_chunk(const u32x4 w, const float* xs, int c, float& a0, float& a1) {
-  const float4* xv = reinterpret_cast<const float4*>(xs + c * 8);
-  const float4 p = xv[0], q = xv[1];
-  a0 = fmaf(bf_lo(w.x), p.x, a0);
-  a1 = fmaf(bf_hi(w.x), p.y, a1);
-  a0 = fmaf(bf_lo(w.y), p.z, a0);
-  a1 = fmaf(bf_hi(w.y), p.w, a1);
-  a0 = fmaf(bf_lo(w.z), q.x, a0);
-  a1 = fmaf(bf_hi(w.z), q.y, a1);
-  a0 = fmaf(bf_lo(w.w), q.z, a0);
-  a1 = fmaf(bf_hi(w.w), q.w, a1);
+// Eight bf16 weights (one chunk) times x as packed bf16 pairs: four v_dot2.
+__device__ __forceinline__ void dot_chunk_bf16(const u32x4 w, const uint32_t* xp, int c, float& a0, float& a1) {
+  const u32x4 x = *reinterpret_cast<const u32x4*>(xp + 4 * c);
+  a0 = dot2_bf16(w.x, x.x, a0);
+  a1 = dot2_bf16(w.y, x.y, a1);
+  a0 = dot2_bf16(w.z, x.z, a0);
+  a1 = dot2_bf16(w.w, x.w, a1);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -233,8 +229,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         dot_chunk_i8(w[j], xp, cx, a0, a1);
         if constexpr (PAIR) dot_chunk_i8(u[j], xp, cx, b0, b1);
       } else {
-        fma_chunk(w[j], xs, cx, a0, a1);
-        if constexpr (PAIR) fma_chunk(u[j], xs, cx, b0, b1);
+        dot_chunk_bf16(w[j], xp, cx, a0, a1);
+        if constexpr (PAIR) dot_chunk_bf16(u[j], xp, cx, b0, b1);
       }
     }
   };
@@ -242,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   unsigned long long best = 0ull;
   int g = blockIdx.x * kWaves + wave;
   load(g, 0, wa, ua);
-  stage_x(a, xs, red, W8 ? xp : nullptr);
+  stage_x(a, xs, red, xp);
   __syncthreads();
 
   if (single_pass) {
@@ -492,7 +488,7 @@ template <int LPR, int NJ, bool W8, bool PAIR>
 int launch_cfg(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
   constexpr int RPW = 64 / LPR;
   // x as float32 and a reduction scratch; W8 also x as packed bf16 pairs
-  const size_t lds = (size_t)(a.K + 8) * sizeof(float) + (W8 ? (size_t)a.K * 2 : 0);
+  const size_t lds = (size_t)(a.K + 8) * sizeof(float) + (size_t)a.K * 2;
   const int needed = ((a.M + RPW - 1) / RPW + kWaves - 1) / kWaves;
   int cap = cu_count() * resident_per_cu<LPR, NJ, W8, PAIR>(lds);
   if (cap > kMaxPartialKeys) cap = kMaxPartialKeys;
