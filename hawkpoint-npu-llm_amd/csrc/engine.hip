@@ -174,6 +174,7 @@ struct hk_engine {
   bool xcd_split = false;
   int next_pos = 0;
   std::vector<uint16_t*> down_x;         // per layer, down_proj regrouped for the split
+  std::vector<uint16_t*> wide;           // W8 split: per layer, QKV then O as bf16 (PersistentLayer::qkv_wide)
   unsigned long long* wpart = nullptr;   // the split's partial down products
   unsigned long long* xpart = nullptr;
   PersistentLayer* players = nullptr;  // device copy of the layer pointers
@@ -470,6 +471,8 @@ void free_engine(hk_engine* e) {
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   for (uint16_t* p : e->down_x)
+    if (p) (void)hipFree(p);
+  for (uint16_t* p : e->wide)
     if (p) (void)hipFree(p);
   for (auto& m : e->pf_native)
     for (void* p : m)
@@ -833,7 +836,7 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
         pl[l] = {static_cast<const uint16_t*>(lw.qkv),     lw.qkv_bias,
                  static_cast<const uint16_t*>(lw.o_proj),  static_cast<const uint16_t*>(lw.gate_up),
                  static_cast<const uint16_t*>(lw.down_proj), lw.input_norm, lw.post_attn_norm,
-                 nullptr, lw.qkv_scale, lw.o_scale, lw.gate_up_scale, lw.down_scale};
+                 nullptr, lw.qkv_scale, lw.o_scale, lw.gate_up_scale, lw.down_scale, nullptr, nullptr};
       }
       if (e->xcd_split) {
         // the split fuses down_proj into the gate/up workgroups: a regrouped
@@ -845,6 +848,20 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
           HK_TRY(launch_regroup_down(e->layers[l].down_proj, e->down_x[l], d.hidden, d.intermediate, w8,
                                      e->stream));
           pl[l].down_x = e->down_x[l];
+        }
+        if (w8) {
+          // XCD 0's stager waves read their QKV and O rows as bf16 (exact
+          // copies of the int8 values): QKV rows x hidden, then hidden x
+          // attention width, per layer
+          const size_t nq = (size_t)e->qkv_rows * d.hidden, no = (size_t)d.hidden * d.q_heads * kHeadDim;
+          e->wide.assign(d.layers, nullptr);
+          for (int l = 0; l < d.layers; ++l) {
+            HK_TRY(dalloc(&e->wide[l], nq + no));
+            HK_TRY(launch_widen_i8(e->layers[l].qkv, e->wide[l], nq, e->stream));
+            HK_TRY(launch_widen_i8(e->layers[l].o_proj, e->wide[l] + nq, no, e->stream));
+            pl[l].qkv_wide = e->wide[l];
+            pl[l].o_wide = e->wide[l] + nq;
+          }
         }
         HK_TRY(dalloc(&e->wpart, (size_t)kPersistentGrid * d.hidden));
         HK_CHECK(hipMemset(e->wpart, 0, (size_t)kPersistentGrid * d.hidden * 8));

@@ -123,6 +123,12 @@ struct PersistentLayer {
   const float* o_scale;
   const float* gate_up_scale;
   const float* down_scale;
+  // W8 under the XCD split (null otherwise): the int8 QKV and O weights as
+  // bf16 (each value exact), which XCD 0's stager waves load in place of
+  // their int8 rows, so they need not widen them between their poll and the
+  // hand-off (see launch_widen_i8)
+  const uint16_t* qkv_wide;
+  const uint16_t* o_wide;
 };
 
 struct PersistentArgs {
@@ -185,6 +191,8 @@ int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t strea
 // down_x for the XCD split from down [H, I] (bf16, or int8 when w8; I a
 // multiple of 4, H of 8, or of 16 for int8).
 int launch_regroup_down(const void* down, void* down_x, int H, int I, bool w8, hipStream_t stream);
+// dst[i] = bf16(src[i]) for n int8 values (exact).
+int launch_widen_i8(const void* src, void* dst, size_t n, hipStream_t stream);
 
 // ---- batched prefill (prefill.hip) ----
 

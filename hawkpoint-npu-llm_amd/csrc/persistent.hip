@@ -641,6 +641,24 @@ __device__ __forceinline__ void widen_w8(u32x4 (&pf)[kPf]) {
   }
 }
 
+// A W8 row group loaded from its bf16 copy (PersistentLayer::qkv_wide) straight
+// into the layout widen_w8 produces: the NJ raw chunks of lane l (16 weights
+// at columns 16 (l + LPR j)) become slots OFF + 2j and OFF + 2j + 1.
+template <int LPR, int NJ, int OFF>
+__device__ __forceinline__ void prefetch_wide(u32x4 (&pf)[kPf], const uint16_t* Wb, int M, int K, int group,
+                                              bool live_wg) {
+  const int lane = threadIdx.x & 63;
+  const int l = lane % LPR, row = group * (64 / LPR) + lane / LPR;
+  const bool live = live_wg && row < M;
+  const __amdgpu_buffer_rsrc_t r = rsrc(Wb, M * K * 2);
+  const unsigned voff = live ? (unsigned)row * (unsigned)K * 2u + (unsigned)l * 32u : kOutside;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    pf[OFF + 2 * j] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, j * LPR * 32, kNT);
+    pf[OFF + 2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, j * LPR * 32 + 16, kNT);
+  }
+}
+
 // EB 1 with WIDE: the rows' int8 chunks were widened by widen_w8 (chunk j in
 // slots OFF + 2j, OFF + 2j + 1; with PAIR the up rows' from OFF + 2 NJ).
 template <int LPR, int NJ, bool PAIR, int OFF, int EB = 2, bool WIDE = false>
@@ -1661,16 +1679,29 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
     const bool lq = R2 ? (c.lane & 15) < 2 : c.lane % Q.lpr == 0;
     const bool lo = R2 ? (c.lane & 15) < 2 : c.lane % O.lpr == 0;
     const int sub_q = R2 ? sub2 : -1;
+    // W8: the stager waves load their rows from the bf16 copies, already in
+    // the widened layout (they poll before their rows could be widened; the
+    // compute waves widen theirs while they wait)
     auto prefetch_q = [&](const PersistentLayer& w, bool live) {
       if constexpr (R2)
         prefetch_r2<S::xq2, 0>(pf, w.qkv, S::QKV, S::H, c.gw, live);
-      else
+      else if constexpr (S::W8) {
+        if (stager)
+          prefetch_wide<Q.lpr, Q.nj, 0>(pf, w.qkv_wide, S::QKV, S::H, c.gw, live);
+        else
+          prefetch<Q.lpr, Q.nj, false, LQ, S::EB>(pf, w.qkv, S::QKV, S::H, c.gw, live);
+      } else
         prefetch<Q.lpr, Q.nj, false, LQ, S::EB>(pf, w.qkv, S::QKV, S::H, c.gw, live);
     };
     auto prefetch_o = [&](const PersistentLayer& w, bool live) {
       if constexpr (R2)
         prefetch_r2<S::xo2, OFF_O>(pf, w.o, S::H, S::AO, c.gw, live);
-      else
+      else if constexpr (S::W8) {
+        if (stager)
+          prefetch_wide<O.lpr, O.nj, OFF_O>(pf, w.o_wide, S::H, S::AO, c.gw, live);
+        else
+          prefetch<O.lpr, O.nj, false, LO, S::EB>(pf, w.o, S::H, S::AO, c.gw, live);
+      } else
         prefetch<O.lpr, O.nj, false, LO, S::EB>(pf, w.o, S::H, S::AO, c.gw, live);
     };
     const int res_o = min(row_o, S::H - 1);
@@ -1707,10 +1738,6 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
             stage_wave_plain<S::H>(c, x0, lw.in_norm, sm.xs[buf], sm.raw_h);
           else  // h from XCD 0's own reducers (reduce_h), in its L2
             ok = stage_wave<S::H, true, true, kLocal>(c, a.tact, tag_of(ep), lw.in_norm, sm.xs[buf], sm.raw_h);
-          if constexpr (S::W8) {  // the stagers' own rows, once h is staged
-            widen_w8<0, Q.nj>(pf);
-            if (is_o) widen_w8<OFF_O, O.nj>(pf);
-          }
         }
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
@@ -2031,6 +2058,18 @@ __global__ void regroup_down_kernel(const T* __restrict__ down, T* __restrict__ 
   }
 }
 }  // namespace
+
+__global__ void widen_i8_kernel(const int8_t* __restrict__ src, uint16_t* __restrict__ dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = (uint16_t)(__float_as_uint((float)src[i]) >> 16);  // |q| <= 127: exact in bf16
+}
+
+int launch_widen_i8(const void* src, void* dst, size_t n, hipStream_t stream) {
+  hipLaunchKernelGGL(widen_i8_kernel, dim3(1024), dim3(256), 0, stream, static_cast<const int8_t*>(src),
+                     static_cast<uint16_t*>(dst), n);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "widen_i8 launch");
+}
 
 int launch_regroup_down(const void* down, void* down_x, int H, int I, bool w8, hipStream_t stream) {
   if (!down || !down_x || H <= 0 || I <= 0 || H % (w8 ? 16 : 8) != 0 || I % 4 != 0)
