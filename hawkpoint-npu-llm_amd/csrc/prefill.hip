@@ -532,8 +532,10 @@ struct SlabBatch {
 // streams the token fragments two steps at a time, double buffered.  NB: the
 // prompt's 16-token blocks (a 40-token prompt takes three: a quarter fewer
 // token loads, products and LDS sums than the four a 64-token prompt needs).
-template <bool PAIR, bool NORM, bool W8, int WAVES, int NB = kSlabBlocks>
+// TWO (gate/up with more slabs than CUs): a workgroup may take a second slab.
+template <bool PAIR, bool NORM, bool W8, int WAVES, int NB = kSlabBlocks, bool TWO = false>
 __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a) {
+  static_assert(!TWO || (PAIR && NORM), "second slabs for gate/up with the norm");
   constexpr int kSlabWaves = WAVES;
   constexpr int P = PAIR ? 2 : 1;
   constexpr int EB = W8 ? 1 : 2;  // bytes per weight
@@ -629,10 +631,36 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
     }
   };
 
+  // SwiGLU with the norm and more slabs than workgroups (gate/up): workgroup
+  // b also takes slab s2 = b + gridDim.x when there is one.  Its weights are
+  // requested with the first slab's and its products reuse the normalised
+  // token fragments, so it costs no second start, token loads or norm; each
+  // slab's arithmetic is that of a workgroup of its own.
+  const int s2 = blockIdx.x + gridDim.x;
+  const bool two = TWO && s2 * 16 < N;  // uniform
+  Batch nbt;
+  typename Batch::WRaw w2[TWO ? B : 1], u2[TWO ? B : 1];
   if constexpr (NORM) {
     // one batch holds every step of the wave (the host keeps K <= 32 steps)
-    Batch bt;
+    Batch& bt = nbt;
     load(bt, 0);
+    if constexpr (TWO) {
+      const unsigned wofs2 = two ? wpiece(s2 * 16 + fr) : kSlabOutside;
+      const unsigned uofs2 = two ? wpiece(s2 * 16 + fr + N) : kSlabOutside;
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * i));
+        const bool live = two && i < mine;
+        const unsigned wo = live ? wofs2 + k0 * wkm : kSlabOutside, uo = live ? uofs2 + k0 * wkm : kSlabOutside;
+        if constexpr (W8) {
+          w2[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
+          u2[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, uo, 0, 2));
+        } else {
+          w2[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2);
+          u2[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, uo, 0, 2);
+        }
+      }
+    }
     u32x4 g[B];
     const __amdgpu_buffer_rsrc_t gr = rsrc(a.gamma, K * 2);
 #pragma unroll
@@ -742,75 +770,99 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
     }
   }
 
+  for (int pass = 0; pass < 2; ++pass) {
+    const int s = pass ? s2 : (int)blockIdx.x, ns = 16 * s;
+    if (pass) {
+      if (!two) break;
+      __syncthreads();  // the first slab's sums have been read
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    red[wave][b][lane] = acc[b];
-    if constexpr (PAIR) red[wave][NB + b][lane] = accu[b];
-  }
-  __syncthreads();
-
-  // values f = t, t + 64 WAVES, ... of [mb][64 lanes][4 rows] on thread t,
-  // each summed over the waves in wave order, then the epilogue (the
-  // rounding points of the other GEMM kernels)
-  for (int f = tid; f < mb * 256; f += kSlabWaves * 64) {
-    const int b = f >> 8, l = (f >> 2) & 63, r = f & 3;
-    const int m = 16 * b + 4 * (l >> 4) + r, n = a.rope.on ? rope_row(blockIdx.x, l & 15) : n0 + (l & 15);
-    if (m >= M || n >= N) continue;
-    float x = 0.0f, u = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kSlabWaves; ++w) {
-      x += red[w][b][l][r];
-      if constexpr (PAIR) u += red[w][NB + b][l][r];
-    }
-    if constexpr (W8) {
-      x *= a.scale[n];
-      if constexpr (PAIR) u *= a.scale[N + n];
-    }
-    if (a.rope.on) {
-      // QKV with RoPE and the KV append (the rope_append_kernel arithmetic):
-      // the pair partner of row n is lane l ^ 8 of the same token
-      const int lp = l ^ 8, np = rope_row(blockIdx.x, lp & 15);
-      float xp = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kSlabWaves; ++w) xp += red[w][b][lp][r];
-      if constexpr (W8) xp *= a.scale[np];
-      const float v = a.bias ? round_bf16(round_bf16(x) + a.bias[n]) : round_bf16(x);
-      const float vp = a.bias ? round_bf16(round_bf16(xp) + a.bias[np]) : round_bf16(xp);
-      const int hd = n / kHeadDim, j = n % kHeadDim, p = a.rope.start + m;
-      const auto& at = a.rope;
-      if (hd < at.q_heads + at.kv_heads) {
-        const int jj = j & (kHeadDim / 2 - 1);
-        const float c = at.cos_tab[(size_t)p * (kHeadDim / 2) + jj], sn = at.sin_tab[(size_t)p * (kHeadDim / 2) + jj];
-        // first half: x1 c - x2 s; second half: x2 c + x1 s (x1 the first-half value)
-        const uint16_t rot = (uint16_t)(j < kHeadDim / 2 ? f32_to_bf16(v * c - vp * sn) : f32_to_bf16(v * c + vp * sn));
-        if (hd < at.q_heads)
-          at.qrot[(size_t)m * at.q_heads * kHeadDim + (size_t)hd * kHeadDim + j] = rot;
-        else
-          at.kcache[((size_t)(hd - at.q_heads) * at.max_ctx + p) * kHeadDim + j] = rot;
-      } else {
-        at.vcache[((size_t)(hd - at.q_heads - at.kv_heads) * at.max_ctx + p) * kHeadDim + j] = (uint16_t)f32_to_bf16(v);
+      for (int b = 0; b < NB; ++b) {
+        acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (PAIR) accu[b] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      continue;
+      if constexpr (TWO) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const bf16x8 w = widen(w2[i]), wu = widen(u2[i]);
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const bf16x8 xa = __builtin_bit_cast(bf16x8, nbt.x[i][b]);
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, w, acc[b], 0, 0, 0);
+            accu[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wu, accu[b], 0, 0, 0);
+          }
+        }
+      }
     }
-    // (k-blocked outputs and residuals: element (m, n) at ((n / 8) M + m) 8 + n % 8)
-    const size_t yo = a.kblock == 2 ? ((size_t)(n >> 3) * M + m) * 8 + (n & 7) : (size_t)m * a.ldy + n;
-    const size_t ro = a.kblock == 2 ? yo : (size_t)m * a.ldr + n;
-    uint16_t* y = a.Y + yo;
-    switch (a.epi) {
-      case EPI_BF16:
-        *y = (uint16_t)f32_to_bf16(x);
-        break;
-      case EPI_BIAS:
-        *y = (uint16_t)f32_to_bf16(round_bf16(x) + a.bias[n]);
-        break;
-      case EPI_RESID:
-        *y = (uint16_t)f32_to_bf16(round_bf16(x) + bf16_to_f32(a.resid[ro]));
-        break;
-      case EPI_SWIGLU:
-        if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(x), round_bf16(u)));
-        break;
-      default:
-        break;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      red[wave][b][lane] = acc[b];
+      if constexpr (PAIR) red[wave][NB + b][lane] = accu[b];
+    }
+    __syncthreads();
+
+    // values f = t, t + 64 WAVES, ... of [mb][64 lanes][4 rows] on thread t,
+    // each summed over the waves in wave order, then the epilogue (the
+    // rounding points of the other GEMM kernels)
+    for (int f = tid; f < mb * 256; f += kSlabWaves * 64) {
+      const int b = f >> 8, l = (f >> 2) & 63, r = f & 3;
+      const int m = 16 * b + 4 * (l >> 4) + r, n = a.rope.on ? rope_row(s, l & 15) : ns + (l & 15);
+      if (m >= M || n >= N) continue;
+      float x = 0.0f, u = 0.0f;
+  #pragma unroll
+      for (int w = 0; w < kSlabWaves; ++w) {
+        x += red[w][b][l][r];
+        if constexpr (PAIR) u += red[w][NB + b][l][r];
+      }
+      if constexpr (W8) {
+        x *= a.scale[n];
+        if constexpr (PAIR) u *= a.scale[N + n];
+      }
+      if (a.rope.on) {
+        // QKV with RoPE and the KV append (the rope_append_kernel arithmetic):
+        // the pair partner of row n is lane l ^ 8 of the same token
+        const int lp = l ^ 8, np = rope_row(s, lp & 15);
+        float xp = 0.0f;
+  #pragma unroll
+        for (int w = 0; w < kSlabWaves; ++w) xp += red[w][b][lp][r];
+        if constexpr (W8) xp *= a.scale[np];
+        const float v = a.bias ? round_bf16(round_bf16(x) + a.bias[n]) : round_bf16(x);
+        const float vp = a.bias ? round_bf16(round_bf16(xp) + a.bias[np]) : round_bf16(xp);
+        const int hd = n / kHeadDim, j = n % kHeadDim, p = a.rope.start + m;
+        const auto& at = a.rope;
+        if (hd < at.q_heads + at.kv_heads) {
+          const int jj = j & (kHeadDim / 2 - 1);
+          const float c = at.cos_tab[(size_t)p * (kHeadDim / 2) + jj], sn = at.sin_tab[(size_t)p * (kHeadDim / 2) + jj];
+          // first half: x1 c - x2 s; second half: x2 c + x1 s (x1 the first-half value)
+          const uint16_t rot = (uint16_t)(j < kHeadDim / 2 ? f32_to_bf16(v * c - vp * sn) : f32_to_bf16(v * c + vp * sn));
+          if (hd < at.q_heads)
+            at.qrot[(size_t)m * at.q_heads * kHeadDim + (size_t)hd * kHeadDim + j] = rot;
+          else
+            at.kcache[((size_t)(hd - at.q_heads) * at.max_ctx + p) * kHeadDim + j] = rot;
+        } else {
+          at.vcache[((size_t)(hd - at.q_heads - at.kv_heads) * at.max_ctx + p) * kHeadDim + j] = (uint16_t)f32_to_bf16(v);
+        }
+        continue;
+      }
+      // (k-blocked outputs and residuals: element (m, n) at ((n / 8) M + m) 8 + n % 8)
+      const size_t yo = a.kblock == 2 ? ((size_t)(n >> 3) * M + m) * 8 + (n & 7) : (size_t)m * a.ldy + n;
+      const size_t ro = a.kblock == 2 ? yo : (size_t)m * a.ldr + n;
+      uint16_t* y = a.Y + yo;
+      switch (a.epi) {
+        case EPI_BF16:
+          *y = (uint16_t)f32_to_bf16(x);
+          break;
+        case EPI_BIAS:
+          *y = (uint16_t)f32_to_bf16(round_bf16(x) + a.bias[n]);
+          break;
+        case EPI_RESID:
+          *y = (uint16_t)f32_to_bf16(round_bf16(x) + bf16_to_f32(a.resid[ro]));
+          break;
+        case EPI_SWIGLU:
+          if constexpr (PAIR) *y = (uint16_t)f32_to_bf16(silu_mul(round_bf16(x), round_bf16(u)));
+          break;
+        default:
+          break;
+      }
     }
   }
 }
@@ -1065,10 +1117,17 @@ namespace {
 // NB: 16-token blocks of the prompt
 template <bool PAIR, bool W8, int NB>
 void launch_slab_nb(const PrefillGemmArgs& a, hipStream_t stream) {
-  const dim3 grid((a.N + 15) / 16);
+  const int slabs = (a.N + 15) / 16;
+  const dim3 grid(slabs);
   const bool long_k = a.K / 32 > 16 * kSlabBatch;
   if (a.gamma) {
-    hipLaunchKernelGGL((gemm_slab_kernel<PAIR, true, W8, 16, NB>), grid, dim3(16 * 64), 0, stream, a);
+    // gate/up with more slabs than CUs (up to twice as many): one workgroup
+    // per CU, some of them taking a second slab
+    const int cus = cu_count();
+    if (PAIR && slabs > cus && slabs <= 2 * cus)
+      hipLaunchKernelGGL((gemm_slab_kernel<PAIR, true, W8, 16, NB, PAIR>), dim3(cus), dim3(16 * 64), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gemm_slab_kernel<PAIR, true, W8, 16, NB>), grid, dim3(16 * 64), 0, stream, a);
   } else if constexpr (!PAIR) {
     if (long_k)
       hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, kSlabLongWaves, NB>), grid, dim3(kSlabLongWaves * 64),
