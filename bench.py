@@ -294,7 +294,10 @@ def main():
         first, _ = engine.step_token(prompt[-1], PROMPT - 1, logits=True, want_logits_array=False)
         return first
 
-    def timed(fn, reps=5):
+    def timed(fn, reps=5, warm=0):
+        # median wall time of `reps` calls after `warm` untimed ones
+        for _ in range(warm):
+            fn()
         times, out = [], None
         for _ in range(reps):
             t0 = time.perf_counter()
@@ -307,7 +310,7 @@ def main():
         probe(engine, meta, args.kernel_launches, PROMPT - 1)
         return
     first_pp, ttft_pp = timed(prefill_per_position, 3)
-    first, ttft = timed(lambda: engine.prefill(prompt, 0, want_logits_array=False)[0])
+    first, ttft = timed(lambda: engine.prefill(prompt, 0, want_logits_array=False)[0], 20, 2)
     if first != first_pp:
         log(f"note: batched and per-position prefill pick {first} / {first_pp} (near-tie)")
     prefill_flops = 2.0 * PROMPT * layer_params(meta)
@@ -389,7 +392,7 @@ def main():
     # 31 greedy steps (32 tokens), median of 5 runs
     log("building the W8 engine (per-row int8 quantisation of the same weights)")
     w8 = QwenDecoderEngine(model, context_length=4096, w8=True)
-    w8_first, w8_ttft = timed(lambda: w8.prefill(prompt, 0, want_logits_array=False)[0], 3)
+    w8_first, w8_ttft = timed(lambda: w8.prefill(prompt, 0, want_logits_array=False)[0], 20, 2)
     w8.generate(w8_first, PROMPT, RUN)  # captures the step graph
     w8_runs = []
     for _ in range(5):
