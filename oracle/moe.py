@@ -6,7 +6,7 @@ The reference offloads only the expert projections given expert ids (the GGML
 ``MUL_MAT_ID`` path, ``ollama-xdna/backend/ggml-xdna.cpp:1301-1441``, and the
 Colibri expert group, ``colibri-xdna/backend/backend_xdna.cpp:316-348``: gate,
 up, ``silu(g) * u``, down).  The router, top-k and the weighted combine live in
-upstream ggml / Colibri, which are not vendored, so the block is
+upstream ggml / Colibri, which the reference does not vendor, so the block is
 defined here, with the decode layer's rounding points
 (``npu_llm/runtime/cpu_backend.py:151-171``):
 
