@@ -938,14 +938,20 @@ int split_parts(int M, int N, int K) {
 constexpr int kFaRows = 64;                 // query tokens per workgroup
 constexpr int kFaSlots = 128;               // KV slots per block
 constexpr int kFaKRow = kHeadDim + 8;       // bf16 per K row in LDS (padding)
-constexpr int kFaSB = kFaSlots / 16;        // 16-slot S^T blocks per KV block
 // exp(s / 8 - m) = exp2(s * log2(e) / 8 - m'): the scores are kept in base-2
 // units so that each exponential is one v_exp_f32
 constexpr float kFaScale = 0.125f * 1.4426950408889634f;
 
+// KS: KV slots per block, kFaSlots, or 64 when the whole context fits 64
+// slots (a short prompt from slot 0: half the products of a 128-slot block,
+// whose second half is masked; the masked slots add exact zeros, so both
+// forms give the same result).
+template <int KS>
 __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kFaSlots][kFaKRow];  // [slot][dim]
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kFaSlots][kFaKRow];  // [slot][dim]
+  constexpr int kSB = KS / 16;  // 16-slot S^T blocks per KV block
+  static_assert(KS == 64 || KS == kFaSlots, "64 or kFaSlots slots per block");
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[KS][kFaKRow];  // [slot][dim]
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[KS][kFaKRow];  // [slot][dim]
   const int h = blockIdx.x;
   const int nblk = (a.n + kFaRows - 1) / kFaRows;
   const int qb = nblk - 1 - (int)blockIdx.y;  // the longest blocks start first
@@ -956,7 +962,7 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
   const bool tok_ok = tok < a.n;
   const int p = a.start + (tok_ok ? tok : 0);
   const int last_slot = a.start + min(qb * kFaRows + kFaRows - 1, a.n - 1);
-  const int nkv = last_slot / kFaSlots + 1;
+  const int nkv = last_slot / KS + 1;
   const size_t kv_base = (size_t)g * a.max_ctx;
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
@@ -977,7 +983,8 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
   const __amdgpu_buffer_rsrc_t vres = rsrc(a.vcache + kv_base * kHeadDim, (last_slot + 1) * kHeadDim * 2);
   u32x4 kr[4], vr[4];
   auto load_tile = [&](int kb) {
-    const unsigned off = (unsigned)((kb * kFaSlots + ls) * kHeadDim + ld0) * 2u;
+    // (threads 2 KS .. hold no slot of a 64-slot block: their offsets lie past the resources)
+    const unsigned off = ls < KS ? (unsigned)((kb * KS + ls) * kHeadDim + ld0) * 2u : 0x7ffffff0u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       kr[i] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 16 * i, 0);
@@ -992,19 +999,21 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
   load_tile(0);
   for (int kb = 0; kb < nkv; ++kb) {
     __syncthreads();  // the previous tile has been read
+    if (ls < KS) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8 * i]) = kr[i];
-      *reinterpret_cast<u32x4*>(&Vs[ls][ld0 + 8 * i]) = vr[i];
+      for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8 * i]) = kr[i];
+        *reinterpret_cast<u32x4*>(&Vs[ls][ld0 + 8 * i]) = vr[i];
+      }
     }
     __syncthreads();
     if (kb + 1 < nkv) load_tile(kb + 1);  // in flight during this tile's math
 
     // S^T blocks: lane holds slots s0 + 16 sb + 4 quad + r of token `tok`
-    const int s0 = kb * kFaSlots;
-    f32x4 sv[kFaSB];
+    const int s0 = kb * KS;
+    f32x4 sv[kSB];
 #pragma unroll
-    for (int sb = 0; sb < kFaSB; ++sb) {
+    for (int sb = 0; sb < kSB; ++sb) {
       sv[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
@@ -1015,10 +1024,10 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     float mx = -INFINITY;
     // a block whose slots all precede every token of the workgroup needs no
     // causal mask (uniform: the block's first token and the last slot)
-    const bool full = s0 + kFaSlots - 1 <= a.start + qb * kFaRows && qb * kFaRows + kFaRows <= a.n;
+    const bool full = s0 + KS - 1 <= a.start + qb * kFaRows && qb * kFaRows + kFaRows <= a.n;
     if (full) {
 #pragma unroll
-      for (int sb = 0; sb < kFaSB; ++sb)
+      for (int sb = 0; sb < kSB; ++sb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           sv[sb][r] *= kFaScale;
@@ -1026,7 +1035,7 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
         }
     } else {
 #pragma unroll
-      for (int sb = 0; sb < kFaSB; ++sb)
+      for (int sb = 0; sb < kSB; ++sb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int slot = s0 + 16 * sb + 4 * quad + r;
@@ -1042,7 +1051,7 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float rs = 0.0f;
 #pragma unroll
-    for (int sb = 0; sb < kFaSB; ++sb)
+    for (int sb = 0; sb < kSB; ++sb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float e = __builtin_amdgcn_exp2f(sv[sb][r] - m_use);
@@ -1062,7 +1071,7 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     // hi, its top 16 bits, and lo, the top 16 bits of the exact remainder
     // P - hi; together they carry about 16 significant bits.
 #pragma unroll
-    for (int t = 0; t < kFaSB / 2; ++t) {
+    for (int t = 0; t < kSB / 2; ++t) {
       uint32_t ph[4], pl[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -1295,8 +1304,11 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream) {
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "rope append launch");
   }
-  hipLaunchKernelGGL(attention_prefill_kernel, dim3(a.q_heads, (a.n + kFaRows - 1) / kFaRows), dim3(kThreads), 0,
-                     stream, a);
+  const dim3 grid(a.q_heads, (a.n + kFaRows - 1) / kFaRows);
+  if (a.start + a.n <= 64)
+    hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(attention_prefill_kernel<kFaSlots>, grid, dim3(kThreads), 0, stream, a);
   err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "prefill attention launch");
 }
