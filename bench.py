@@ -4,10 +4,11 @@
 Workload: the Qwen2.5-0.5B-shaped decoder (24 layers, hidden 896, 14/2 heads,
 SwiGLU 4864, vocab 151936, tied bf16 LM head, qkv bias) with seeded random
 N(0, 0.02) bf16 weights.  A 40-token random prompt is prefilled position by
-position (the reference's prefill, npu_llm/runtime/generate.py:1110-1125),
-then greedy decode runs in 31-step runs at positions 40..70, i.e. 32 tokens
-per run with the prefill's token, the reference's "40-token prompt, 32
-tokens" protocol.  One step = one decode token: every layer, the final norm,
+position (the reference's prefill, npu_llm/runtime/generate.py:1110-1125,
+timed as per_position_ms) and in one batched chunk (the TTFT); greedy
+decode then runs in 31-step runs at positions 40..70, each continuing from
+the batched prefill's KV cache, i.e. 32 tokens per run with the prefill's
+token, the reference's "40-token prompt, 32 tokens" protocol.  One step = one decode token: every layer, the final norm,
 the LM head and the argmax, with weights and KV resident in HBM.
 
 value = timed steps / wall seconds between two stream synchronisations, the
@@ -253,9 +254,14 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--cpu-steps-one-thread", type=int, default=4)
     ap.add_argument("--no-smollm", action="store_true", help="skip the SmolLM2-135M decode line")
-    ap.add_argument("--workload", choices=("decode", "experts", "gemv", "prefill"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "experts", "gemv", "prefill", "phases"), default="decode",
                     help="experts: the GGML MUL_MAT_ID / Colibri expert-group shims; gemv: the isolated "
-                    "GEMVs; prefill: batched prefills of 40 and 4064 tokens (each prints its own JSON line)")
+                    "GEMVs; prefill: batched prefills of 40 and 4064 tokens; phases: the per-layer phase "
+                    "table of the decode step from lib/libhk_phases.so (each prints its own JSON line)")
+    ap.add_argument("--phases-model", choices=("qwen", "qwen-w8", "smollm"), default="qwen",
+                    help="phases: the decoder whose step is stamped")
+    ap.add_argument("--phases-long", action="store_true",
+                    help="phases: a 4064-token prompt, decode at positions 4064..4094 (the long form)")
     ap.add_argument("--probe", action="store_true",
                     help="only the counter-calibration workload: decode-step launches, then "
                     "4 device copies of 256 MiB")
@@ -272,6 +278,9 @@ def main():
         return
     if args.workload == "prefill":
         prefill_main(args)
+        return
+    if args.workload == "phases":
+        phases_main(args)
         return
 
     import numpy as np
@@ -442,8 +451,8 @@ def main():
         "config": {
             "workload": "Qwen2.5-0.5B-shape decoder (24L, H896, 14q/2kv heads, I4864, V151936, "
             "tied head, qkv bias), seeded N(0,0.02) bf16 weights, batch 1, 40-token random prompt "
-            f"prefilled per position, greedy decode from position 40 in runs of up to {RUN} steps; value = "
-            f"median of {len(run_tok_s)} timed runs",
+            f"prefilled in one batched chunk, greedy decode from position 40 in runs of up to {RUN} steps "
+            f"continuing from that KV cache; value = median of {len(run_tok_s)} timed runs",
             "batch": 1,
             "prompt_tokens": PROMPT,
             "decode_positions": [PROMPT, last_pos],
@@ -564,6 +573,113 @@ def gemv_main(args):
     hip.init(0)
     out = gemv_microbench()
     print(json.dumps({"workload": "gemv", "gemv_microbench": out}), flush=True)
+
+
+def phases_main(args):
+    """Per-layer phase table of the XCD-split decode step, from the clock
+    stamps that lib/libhk_phases.so (persistent.hip built with
+    -DHK_PHASE_STAMPS) writes at fixed points of each layer: a prompt
+    prefilled in one batch, two untimed 31-step runs, then the stamps of one
+    more run's last launch (position prompt + 30).  Each segment is the mean
+    over layers 1..L-2 of one phase's span, from the last producer of its
+    input (the maximum over workgroups) to the median or last consumer."""
+    import ctypes
+
+    import numpy as np
+
+    lib_path = ROOT / "hawkpoint-npu-llm_amd" / "lib" / "libhk_phases.so"
+    if not lib_path.is_file():
+        raise SystemExit(f"{lib_path} not found: build it with `python hawkpoint-npu-llm_amd/csrc/build.py`")
+    os.environ["HK_LIB"] = str(lib_path)
+    from runtime import hip
+    from runtime.qwen_engine import QwenDecoderEngine
+    from runtime.synthetic import QWEN25_05B, SMOLLM2_135M, SyntheticModel
+
+    shape = SMOLLM2_135M if args.phases_model == "smollm" else QWEN25_05B
+    model = SyntheticModel(shape, seed=0)
+    meta = model.metadata
+    n = 4064 if args.phases_long else (35 if args.phases_model == "smollm" else PROMPT)
+    rng = np.random.default_rng(12)
+    prompt = [int(t) for t in rng.integers(0, meta["vocab_size"], n)]
+    engine = QwenDecoderEngine(model, context_length=4096, w8=args.phases_model == "qwen-w8")
+    lib = hip.lib()
+    lib.hk_phase_stamps.restype = ctypes.c_int
+    lib.hk_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+    ph = np.zeros((256, 32, 16), dtype=np.uint64)
+    at = np.zeros((256, 32, 8), dtype=np.uint64)
+    try:
+        first, _ = engine.prefill(prompt, want_logits_array=False)
+        steps = min(RUN, 4095 - n)
+        kind = engine.step_kind(n + steps - 1)
+        engine.generate(first, n, steps)
+        engine.generate(first, n, steps)
+        hip.check(lib.hk_phase_stamps(None, None, 1), "clear stamps")
+        engine.generate(first, n, steps)
+        hip.check(lib.hk_phase_stamps(ph.ctypes.data, at.ctypes.data, 0), "read stamps")
+    finally:
+        engine.close()
+    T = ph.astype(np.int64) * 10  # 100 MHz clock, ns
+    A = at.astype(np.int64) * 10
+    L = min(meta["layers"], 32)
+    wg = np.arange(256)
+    x0 = wg % 8 == 0
+
+    def sel(layer, slot, mask=None):
+        v = T[:, layer, slot]
+        m = v > 0
+        if mask is not None:
+            m &= mask
+        return v[m]
+
+    def med(layer, slot, mask=None):
+        v = sel(layer, slot, mask)
+        return float(np.median(v)) if v.size else float("nan")
+
+    def last(layer, slot, mask=None):
+        v = sel(layer, slot, mask)
+        return float(v.max()) if v.size else float("nan")
+
+    segments = [
+        ("h -> QKV input staged + RMSNorm (XCD 0)", lambda l: med(l, 0) - last(l - 1, 9)),
+        ("QKV dot products + store", lambda l: last(l, 1, x0) - med(l, 0)),
+        ("QKV store -> last attention task done", lambda l: last(l, 2) - last(l, 1, x0)),
+        ("attention -> O input staged", lambda l: med(l, 3) - last(l, 2)),
+        ("O dot products + publish", lambda l: last(l, 4, x0) - med(l, 3)),
+        ("O -> h1 staged across XCDs + RMSNorm", lambda l: med(l, 5) - last(l, 4, x0)),
+        ("gate/up + SwiGLU + down partial + barrier", lambda l: last(l, 6) - med(l, 5)),
+        ("workgroup partial store", lambda l: last(l, 7) - last(l, 6)),
+        ("per-XCD reduction (median)", lambda l: med(l, 8, ~x0) - last(l, 7)),
+        ("per-XCD reduction (last)", lambda l: last(l, 8, ~x0) - last(l, 7)),
+        ("XCD-0 reduction + residual (median)", lambda l: med(l, 9) - last(l, 8, ~x0)),
+        ("XCD-0 reduction + residual (last)", lambda l: last(l, 9) - last(l, 8, ~x0)),
+        ("layer", lambda l: med(l + 1, 0) - med(l, 0)),
+    ]
+    layers = range(1, L - 1)
+    table = {}
+    for name, fn in segments:
+        vals = [fn(l) for l in layers]
+        vals = [v for v in vals if np.isfinite(v)]
+        table[name] = round(float(np.mean(vals)), 1) if vals else None
+    attn_names = ["start", "q/k/v polled", "scores", "softmax", "merge barrier", "stored (one chunk)",
+                  "stored (merged)", "partial published"]
+    attn = {}
+    for k, name in enumerate(attn_names):
+        vals = []
+        for l in layers:
+            v = A[:, l, k]
+            v = v[v > 0]
+            q = last(l, 1, x0)
+            if v.size and np.isfinite(q):
+                vals.append(float(np.median(v)) - q)
+        attn[name] = round(float(np.mean(vals)), 1) if vals else None
+    out = {"workload": "phases", "model": args.phases_model, "prompt_tokens": n, "step_kind": kind,
+           "positions": [n, n + steps - 1], "layers_averaged": [1, L - 2],
+           "ns_per_layer": table, "attention_task_ns_after_last_qkv_store": attn}
+    for name, v in table.items():
+        log(f"{name:45s} {v if v is not None else '-':>8} ns")
+    for name, v in attn.items():
+        log(f"  attention: {name:32s} {v if v is not None else '-':>8} ns after the last QKV store")
+    print(json.dumps(out), flush=True)
 
 
 def prefill_main(args):

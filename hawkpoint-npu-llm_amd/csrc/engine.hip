@@ -491,10 +491,20 @@ int dalloc(T** p, size_t count) {
 // GEMM has (tokens / 64) x (outputs / 64) tiles to spread over the CUs.
 constexpr int kPrefillRows = 4096;
 
-int prefill_workspace(hk_engine* e) {
-  if (e->pf_rows) return 0;
+// Frees the prefill row buffers (null ones are skipped) and marks the
+// workspace absent, so the next prefill allocates it from nothing.
+void free_prefill_buffers(hk_engine* e) {
+  auto drop = [](auto*& p) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+  };
+  drop(e->pf_x), drop(e->pf_h1), drop(e->pf_xn), drop(e->pf_qkv), drop(e->pf_q);
+  drop(e->pf_att), drop(e->pf_act), drop(e->pf_tokens), drop(e->pf_split);
+  e->pf_rows = 0;
+}
+
+int alloc_prefill_buffers(hk_engine* e, int rows) {
   const hk_model_desc& d = e->d;
-  const int rows = std::min(kPrefillRows, (int)d.max_context);
   const size_t r = rows;
   HK_TRY(dalloc(&e->pf_x, r * d.hidden));
   HK_TRY(dalloc(&e->pf_h1, r * d.hidden));
@@ -513,23 +523,60 @@ int prefill_workspace(hk_engine* e) {
                                    split_ws_need(m, d.intermediate, d.hidden, true),
                                    split_ws_need(m, d.hidden, d.intermediate, false)});
   HK_TRY(dalloc(&e->pf_split, e->pf_split_floats));
-  // the MFMA-native weight copies (every matrix of an engine shape has whole
-  // 16-row slabs: 64-wide heads, hidden and intermediate sizes multiples of 16)
-  if (d.hidden % 16 == 0 && d.intermediate % 16 == 0) {
-    const int wb = e->w8 ? 1 : 2;
-    e->pf_native.assign(d.layers, {nullptr, nullptr, nullptr, nullptr});
-    for (int l = 0; l < d.layers; ++l) {
-      const hk_layer_weights& lw = e->layers[l];
-      const struct { const void* src; int R, K, rope; } m[4] = {
-          {lw.qkv, e->qkv_rows, d.hidden, 1}, {lw.o_proj, d.hidden, QD, 0},
-          {lw.gate_up, 2 * d.intermediate, d.hidden, 0}, {lw.down_proj, d.hidden, d.intermediate, 0}};
-      for (int i = 0; i < 4; ++i) {
-        HK_CHECK(hipMalloc(&e->pf_native[l][i], (size_t)m[i].R * m[i].K * wb));
-        HK_TRY(launch_repack_mfma(m[i].src, e->pf_native[l][i], m[i].R, m[i].K, wb, m[i].rope, e->stream));
+  return 0;
+}
+
+// The row buffers of a prefill chunk, allocated on the first prefill.  On a
+// failure nothing stays allocated, so a retry starts over instead of
+// overwriting (and leaking) what an earlier attempt got.
+int prefill_workspace(hk_engine* e) {
+  if (e->pf_rows) return 0;
+  const int rows = std::min(kPrefillRows, (int)e->d.max_context);
+  const int rc = alloc_prefill_buffers(e, rows);
+  if (rc != 0) {
+    free_prefill_buffers(e);
+    return rc;
+  }
+  e->pf_rows = rows;
+  return 0;
+}
+
+void free_native_copies(hk_engine* e) {
+  for (auto& m : e->pf_native)
+    for (void*& p : m) {
+      if (p) (void)hipFree(p);
+      p = nullptr;
+    }
+  e->pf_native.clear();
+}
+
+// The MFMA-native weight copies the slab GEMMs read (chunks of at most
+// kSlabMaxTokens tokens), made the first time such a chunk runs: an engine
+// that only prefills long prompts never holds them.  Every matrix of an
+// engine shape has whole 16-row slabs (64-wide heads, hidden and
+// intermediate sizes multiples of 16).  On a failure every copy is freed, so
+// prefill_chunk then reads the row-major weights and a later chunk retries.
+int native_copies(hk_engine* e) {
+  const hk_model_desc& d = e->d;
+  if (!e->pf_native.empty() || d.hidden % 16 != 0 || d.intermediate % 16 != 0) return 0;
+  const int wb = e->w8 ? 1 : 2, QD = d.q_heads * kHeadDim;
+  e->pf_native.assign(d.layers, {nullptr, nullptr, nullptr, nullptr});
+  for (int l = 0; l < d.layers; ++l) {
+    const hk_layer_weights& lw = e->layers[l];
+    const struct { const void* src; int R, K, rope; } m[4] = {
+        {lw.qkv, e->qkv_rows, d.hidden, 1}, {lw.o_proj, d.hidden, QD, 0},
+        {lw.gate_up, 2 * d.intermediate, d.hidden, 0}, {lw.down_proj, d.hidden, d.intermediate, 0}};
+    for (int i = 0; i < 4; ++i) {
+      const hipError_t err = hipMalloc(&e->pf_native[l][i], (size_t)m[i].R * m[i].K * wb);
+      int rc = err == hipSuccess ? 0 : hip_fail(err, "hipMalloc");
+      if (rc == 0) rc = launch_repack_mfma(m[i].src, e->pf_native[l][i], m[i].R, m[i].K, wb, m[i].rope, e->stream);
+      if (rc != 0) {
+        if (err != hipSuccess) e->pf_native[l][i] = nullptr;
+        free_native_copies(e);
+        return rc;
       }
     }
   }
-  e->pf_rows = rows;
   return 0;
 }
 
@@ -966,6 +1013,7 @@ int hk_engine_prefill(hk_engine* e, const int32_t* tokens_host, int32_t n, int32
     HK_TRY(prefill_workspace(e));
     for (int c0 = 0; c0 < n; c0 += e->pf_rows) {
       const int m = std::min(e->pf_rows, n - c0);
+      if (m <= kSlabMaxTokens) HK_TRY(native_copies(e));
       HK_CHECK(hipMemcpyAsync(e->pf_tokens, tokens_host + c0, m * sizeof(int32_t),
                               hipMemcpyHostToDevice, e->stream));
       HK_TRY(prefill_chunk(e, e->pf_tokens, m, start + c0));

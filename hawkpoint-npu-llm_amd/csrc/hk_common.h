@@ -136,4 +136,32 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
   return 0xffffffffu - (uint32_t)(key & 0xffffffffu);
 }
 
+// Eight float32 probabilities as three bf16 terms each, packed in pairs as
+// the 8-element B operand of a bf16 MFMA (element e in the half e % 2 of
+// word e / 2): hi holds each value's top 8 significant bits, mid those of
+// the exact remainder, lo those of the remainder after that.  Each
+// truncation leaves a remainder that float32 represents exactly, so
+// hi + mid + lo is the value itself (24 significant bits; values are
+// probabilities in [0, 1], so mid and lo stay normal or tiny enough not
+// to matter).  A P @ V product summed over the three terms with bf16 V
+// gives float32 P @ V, up to the float32 summation order.
+__device__ __forceinline__ void split3_bf16(const float (&p)[8], u32x4& hi, u32x4& mid, u32x4& lo) {
+  uint32_t t[8][3];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t a = __float_as_uint(p[e]) & 0xffff0000u;
+    const float r = p[e] - __uint_as_float(a);
+    const uint32_t b = __float_as_uint(r) & 0xffff0000u;
+    t[e][0] = a;
+    t[e][1] = b;
+    t[e][2] = __float_as_uint(r - __uint_as_float(b)) & 0xffff0000u;
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    hi[w] = (t[2 * w][0] >> 16) | t[2 * w + 1][0];
+    mid[w] = (t[2 * w][1] >> 16) | t[2 * w + 1][1];
+    lo[w] = (t[2 * w][2] >> 16) | t[2 * w + 1][2];
+  }
+}
+
 }  // namespace hk

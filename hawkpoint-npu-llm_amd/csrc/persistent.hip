@@ -64,6 +64,46 @@
 #include "hk_internal.h"
 
 namespace hk {
+
+// ---- phase stamps (built in only with -DHK_PHASE_STAMPS: lib/libhk_phases.so) ----
+// Thread 0 of each workgroup (or the thread named) writes the 100 MHz
+// real-time clock at fixed points of each of the first kStampLayers layers
+// of the XCD-split step; hk_phase_stamps copies the tables to the host.
+// Slots of hk_stamp_phase (per workgroup and layer):
+//   0 Q input staged and normalised     1 QKV rows stored
+//   2 attention task done               3 O input staged
+//   4 O rows published                  5 h1 staged and normalised (MLP)
+//   6 gate/up + down partial + barrier  7 workgroup partial stored
+//   8 XCD reduction done                9 h reduction done (XCD 0)
+//  10 QKV dot products done            11 O dot products done
+//  12 gate/up dot products done        13 down partial done
+// and of hk_stamp_attn (attention task): 0 start, 1 q/k/v polled, 2 scores,
+// 3 softmax, 4 merge barrier, 5 single-chunk store, 6 merged store,
+// 7 partial published.
+constexpr int kStampLayers = 32, kStampSlots = 16, kStampAttn = 8;
+#ifdef HK_PHASE_STAMPS
+__device__ unsigned long long hk_stamp_phase[kPersistentGrid][kStampLayers][kStampSlots];
+__device__ unsigned long long hk_stamp_attn[kPersistentGrid][kStampLayers][kStampAttn];
+#define HK_STAMP_BY(tid, l, k)                                                                       \
+  do {                                                                                               \
+    if (threadIdx.x == (tid) && (l) < kStampLayers)                                                  \
+      hk_stamp_phase[blockIdx.x][l][k] = __builtin_amdgcn_s_memrealtime();                           \
+  } while (0)
+#define HK_STAMP_ATTN(l, k)                                                                          \
+  do {                                                                                               \
+    if (threadIdx.x == 0 && (l) < kStampLayers)                                                      \
+      hk_stamp_attn[blockIdx.x][l][k] = __builtin_amdgcn_s_memrealtime();                            \
+  } while (0)
+#else
+#define HK_STAMP_BY(tid, l, k) \
+  do {                         \
+  } while (0)
+#define HK_STAMP_ATTN(l, k) \
+  do {                      \
+  } while (0)
+#endif
+#define HK_STAMP(l, k) HK_STAMP_BY(0, l, k)
+
 namespace {
 
 constexpr int kPT = kPersistentThreads;  // threads per workgroup (one workgroup per CU)
@@ -788,6 +828,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   const __amdgpu_buffer_rsrc_t kc = rsrc(a.kcache + head_base * kHeadDim, p * kHeadDim * 2);
   const __amdgpu_buffer_rsrc_t vc = rsrc(a.vcache + head_base * kHeadDim, p * kHeadDim * 2);
 
+  HK_STAMP_ATTN(l, 0);
   // Cached K half-row of this thread's slot (two threads per slot, one per
   // 32 dimensions) and V words of its slot group (rows written by earlier
   // launches) go out before the new q/k/v are polled.
@@ -860,6 +901,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     }
   }
   if (__syncthreads_or(!ok)) return false;
+  HK_STAMP_ATTN(l, 1);
 
   // scores in base 2: head_dim ** -0.5 (1/8 for head_dim 64) times log2(e),
   // so every exponential below is one v_exp_f32 (2^x); the split-KV maxima
@@ -893,6 +935,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     dot = d0 + d1;
   }
   dot = dpp_plus<0xb1>(dot);  // the two halves of the slot (neighbouring lanes)
+  HK_STAMP_ATTN(l, 2);
   const bool live = si < n;
   const float sc = live ? dot * scale : -INFINITY;
   // Softmax and P @ V per wave, flash-style: a wave's 32 slots are exactly
@@ -908,6 +951,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   // the P @ V reads below take probabilities written by other lanes of this
   // wave only; a wave's LDS accesses complete in order
   __builtin_amdgcn_wave_barrier();
+  HK_STAMP_ATTN(l, 3);
 
   // probabilities of slots past the chunk's live ones are zero, and so are
   // their value words, so the loop needs no bounds test; the four 16-byte
@@ -936,6 +980,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     c.sm->red[1][c.wave] = sw;
   }
   __syncthreads();
+  HK_STAMP_ATTN(l, 4);
   float m = c.sm->red[0][0];
 #pragma unroll
   for (int w = 1; w < kPW; ++w) m = fmaxf(m, c.sm->red[0][w]);
@@ -968,6 +1013,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   };
   if (nsplit == 1) {
     if (tid < kHeadDim) store_out(tagged(f32_to_bf16(o), tag_a));
+    HK_STAMP_ATTN(l, 5);
     return true;
   }
 
@@ -978,6 +1024,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   // carries the epoch.
   const __amdgpu_buffer_rsrc_t prs =
       rsrc(a.partial + (size_t)h * a.max_splits * kPartStride, a.max_splits * kPartStride * 8);
+  HK_STAMP_ATTN(l, 7);
   if (s != nsplit - 1) {
     if (tid < kPartStride) {
       const float v = tid < kHeadDim ? o : tid == kHeadDim ? m : sum;
@@ -1036,6 +1083,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     }
     fold(m, sum, o);  // this task's own chunk, the last
     if (ok) store_out(tagged(f32_to_bf16(r / lsum), tag_a));
+    HK_STAMP_ATTN(l, 6);
   }
   return !__syncthreads_or(!ok);
 }
@@ -1741,6 +1789,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         }
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
+        HK_STAMP(l, 0);
       }
       {  // all eight waves; the rows go straight to XCD 0's L2 (only the
          // attention tasks there poll them): each row's first lane stores it,
@@ -1753,13 +1802,16 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
           dot_group<Q.lpr, Q.nj, false, 0, S::EB, S::W8>(pf, sm.xs[buf], S::H, acc, accu);
         }
         if constexpr (S::W8) acc *= sq;
+        HK_STAMP(l, 10);
         const uint32_t y = lw.qkv_bias ? f32_to_bf16(round_bf16(acc) + bias_q) : f32_to_bf16(acc);
         if constexpr (LONG) {  // to the MLP workgroups: gathered, one writer per workgroup
           publish_rows<RQ, kSc1, kPW>(c, is_q, tagged(y, tag_of(ep + 1)), lq, tbuf, o_qkv + rank * kPW * RQ,
                                       S::QKV - rank * kPW * RQ, pad, true, sub_q);
+          HK_STAMP(l, 1);
         } else {
           const unsigned dst = is_q && lq && row_q < S::QKV ? o_qkv + (unsigned)row_q : pad;
           __builtin_amdgcn_raw_buffer_store_b32(tagged(y, tag_of(ep + 1)), tbuf, dst * 4u, 0, 0);
+          HK_STAMP(l, 1);
         }
       }
       if (is_q) buf ^= 1;
@@ -1769,6 +1821,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (!attention_task<S, kLocal, 4>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2),
                                           ptag_of(ep + 2)))
           return;
+        HK_STAMP(l, 2);
       }
       // ---- O: h1 to the MLP side ----
       if (is_o) {
@@ -1777,6 +1830,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
           ok = stage_wave<S::AO, false, false, LONG ? kSc1 : kLocal>(c, a.tattn, tag_of(ep + 2), nullptr,
                                                                      sm.xs[buf], nullptr);
         if (!handoff(ok)) return;
+        HK_STAMP(l, 3);
       }
       {  // all eight waves
         // the residual goes out before the dot products' LDS reads, so its
@@ -1791,8 +1845,10 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
           dot_group<O.lpr, O.nj, false, OFF_O, S::EB, S::W8>(pf, sm.xs[buf], S::AO, acc, accu);
         }
         if constexpr (S::W8) acc *= so;
+        HK_STAMP(l, 11);
         publish_rows<RO, kSc1, kPW>(c, is_o, tagged(f32_to_bf16(round_bf16(acc) + res_h), tag_of(ep + 3)),
                                     lo, tbuf, o_h1 + fo, S::H - fo, pad, true, sub_q);
+        HK_STAMP(l, 4);
       }
       if (is_o) buf ^= 1;
       // the next layer's QKV and O rows go out once this layer's attention
@@ -1814,6 +1870,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
           !reduce_h<S>(c, hslice, ptag_of(ep + 4), tag_of(ep + 3), tag_of(ep + 5), a.tact, lw.down_scale) &&
           c.lane == 0)
         sm.abort = 1;
+      if (hslice < S::xhn) HK_STAMP_BY(kCW * 64, l, 9);
     }
   } else {
     constexpr PhaseCfg G = S::xg;
@@ -1874,15 +1931,19 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         if (stager) ok = stage_wave<S::H, true, false>(c, a.th1, tag_of(ep + 3), lw.post_norm, sm.xs[buf], nullptr);
         if (!handoff(ok)) return;
         normalise_staged<S::H>(c, sm.xs[buf], a.eps);
+        HK_STAMP(l, 5);
         if (!stager) {
           dot_group<G.lpr, G.nj, true, 0, S::EB, S::W8>(pf, sm.xs[buf], S::H, acc, accu);
+          HK_STAMP(l, 12);
           if constexpr (S::W8) {
             acc *= sg;
             accu *= su;
           }
           down_partial<S, OFF_D, S::W8>(pf, f32_to_bf16(silu_mul(round_bf16(acc), round_bf16(accu))), sm.wsum[c.wave]);
+          HK_STAMP(l, 13);
         }
         __syncthreads();
+        HK_STAMP(l, 6);
         // the workgroup's partial: thread t adds outputs 2t, 2t + 1 over the
         // compute waves, in order
         if (threadIdx.x < S::H / 2) {
@@ -1897,6 +1958,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
           __builtin_amdgcn_raw_buffer_store_b128(words, rsrc(a.wpart, kPersistentGrid * S::H * 8),
                                                  (c.wg * S::H + 2 * t) * 8, 0, 0);
         }
+        HK_STAMP(l, 7);
         buf ^= 1;
       }
       // ---- this workgroup's outputs of the XCD's sum (stager wave 0); the
@@ -1905,6 +1967,7 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         bool ok = true;
         if (c.wave == kCW) ok = reduce_xcd<S>(c, xcd, jx, nprod, pt);
         if (!handoff(ok)) return;
+        HK_STAMP(l, 8);
       }
       if constexpr (!LONG) {
         scales_g(nx, pg && more);
@@ -2097,3 +2160,27 @@ int launch_persistent_step(int shape, const PersistentArgs& a, hipStream_t strea
 }
 
 }  // namespace hk
+
+#ifdef HK_PHASE_STAMPS
+// The phase stamps (see hk_stamp_phase): `phase` gets [256][32][16] and
+// `attn` [256][32][8] 64-bit clock values (either may be null), from the last
+// launch that wrote each one; with `clear` both tables are zeroed afterwards
+// (synchronously), so the next copy shows only later launches.  Only in the
+// library built with -DHK_PHASE_STAMPS; call it with no launch in flight.
+extern "C" int hk_phase_stamps(void* phase, void* attn, int clear) {
+  if (hipDeviceSynchronize() != hipSuccess) return hk::fail("hk_phase_stamps: device synchronise failed");
+  if (phase && hipMemcpyFromSymbol(phase, HIP_SYMBOL(hk::hk_stamp_phase), sizeof(hk::hk_stamp_phase)) != hipSuccess)
+    return hk::fail("hk_phase_stamps: copy failed");
+  if (attn && hipMemcpyFromSymbol(attn, HIP_SYMBOL(hk::hk_stamp_attn), sizeof(hk::hk_stamp_attn)) != hipSuccess)
+    return hk::fail("hk_phase_stamps: copy failed");
+  if (clear) {
+    void *ph = nullptr, *at = nullptr;
+    if (hipGetSymbolAddress(&ph, HIP_SYMBOL(hk::hk_stamp_phase)) != hipSuccess ||
+        hipGetSymbolAddress(&at, HIP_SYMBOL(hk::hk_stamp_attn)) != hipSuccess ||
+        hipMemset(ph, 0, sizeof(hk::hk_stamp_phase)) != hipSuccess ||
+        hipMemset(at, 0, sizeof(hk::hk_stamp_attn)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+      return hk::fail("hk_phase_stamps: clear failed");
+  }
+  return 0;
+}
+#endif

@@ -1067,23 +1067,20 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     // O^T[16 db + 4 quad + r][tok] += sum over the block's slots of V^T P^T,
     // 32 slots per bf16 MFMA: k index 8 quad + e stands for slot
     // 32 t + 16 (e / 4) + 4 quad + e % 4, the 8 P values this lane holds for
-    // blocks 2t, 2t + 1.  P (finite, in [0, 1]) goes in as two bf16 terms:
-    // hi, its top 16 bits, and lo, the top 16 bits of the exact remainder
-    // P - hi; together they carry about 16 significant bits.
+    // blocks 2t, 2t + 1.  P (finite, in [0, 1]) goes in as three bf16 terms
+    // (split3_bf16), which together are the float32 P exactly; with two
+    // (16 significant bits) about one output in 200 rounded to another bf16
+    // value than the float32 P @ V.
 #pragma unroll
     for (int t = 0; t < kSB / 2; ++t) {
-      uint32_t ph[4], pl[4];
+      float pv[8];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float p0 = sv[2 * t + (e >> 2)][e & 3], p1 = sv[2 * t + (e >> 2)][(e & 3) + 1];
-        const uint32_t u0 = __float_as_uint(p0) & 0xffff0000u, u1 = __float_as_uint(p1) & 0xffff0000u;
-        const uint32_t r0 = __float_as_uint(p0 - __uint_as_float(u0));
-        const uint32_t r1 = __float_as_uint(p1 - __uint_as_float(u1));
-        ph[e >> 1] = (u0 >> 16) | u1;
-        pl[e >> 1] = (r0 >> 16) | (r1 & 0xffff0000u);
-      }
-      const bf16x8 phi = __builtin_bit_cast(bf16x8, u32x4{ph[0], ph[1], ph[2], ph[3]});
-      const bf16x8 plo = __builtin_bit_cast(bf16x8, u32x4{pl[0], pl[1], pl[2], pl[3]});
+      for (int e = 0; e < 8; ++e) pv[e] = sv[2 * t + (e >> 2)][e & 3];
+      u32x4 ph, pm, pl;
+      split3_bf16(pv, ph, pm, pl);
+      const bf16x8 phi = __builtin_bit_cast(bf16x8, ph);
+      const bf16x8 pmid = __builtin_bit_cast(bf16x8, pm);
+      const bf16x8 plo = __builtin_bit_cast(bf16x8, pl);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         // V^T fragment: lane (quad, col) needs dimension 16 db + col of slots
@@ -1099,8 +1096,9 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
             (__attribute__((address_space(3))) v4s16*)&Vs[rs + 16][rd]);
         const u32x2_t w0 = __builtin_bit_cast(u32x2_t, t0), w1 = __builtin_bit_cast(u32x2_t, t1);
         const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{w0.x, w0.y, w1.x, w1.y});
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[db], 0, 0, 0);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo, o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pmid, o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[db], 0, 0, 0);
       }
     }
   }

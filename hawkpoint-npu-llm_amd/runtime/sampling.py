@@ -265,13 +265,20 @@ def filter_top_k(logits, top_k):
 def filter_top_p(logits, top_p):
     """Nucleus: in descending order of probability a token survives while the
     mass of the tokens before it is below ``top_p``, so the token that crosses
-    the threshold stays, and so does the best one always."""
+    the threshold stays, and so does the best one always.
+
+    The order and the test are the contract of ``sampling.py:380-394``, so a
+    seeded request keeps the reference's tokens also when equal scores sit at
+    the nucleus edge: numpy's default (ascending, unstable) argsort read
+    backwards -- equal scores come in whatever order that call gives them,
+    not by id -- and the mass before token i taken as ``cumsum[i] - p[i]``
+    (not ``cumsum[i-1]``, which can round the other way)."""
     if top_p < 1.0:
-        order = np.argsort(-logits, kind="stable")
+        order = np.argsort(logits)[::-1]
         p = _softmax(logits[order])
-        mass_before = np.concatenate(([0.0], np.cumsum(p)[:-1]))
-        dropped = order[1:][mass_before[1:] >= top_p]
-        logits[dropped] = -np.inf
+        inside = np.cumsum(p) - p < top_p
+        inside[0] = True
+        logits[order[~inside]] = -np.inf
     return logits
 
 

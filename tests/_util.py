@@ -1,6 +1,8 @@
 """Helpers shared by the tests (not a test module)."""
 
+import json
 import sys
+from pathlib import Path
 
 import numpy as np
 
@@ -61,3 +63,34 @@ def check_bf16(y_bits, ref_bits, sum_bound, exact_frac=0.97):
                                  f"got {y[worst]!r}, want {ref[worst]!r}")
     exact = (np.asarray(y_bits) == np.asarray(ref_bits)).mean()
     assert exact >= exact_frac, f"only {exact:.4f} bit-exact"
+
+
+def check_kv_slot(engine, stage, layer, slot, tol):
+    """KV slot `slot` of `layer` holds the oracle's key and value rows: each
+    KV head within rel-L2 `tol` of the oracle's same head and far from every
+    other head (a head written to the wrong place fails), nothing zero."""
+    from oracle import bf16
+
+    k, v = engine.read_kv(layer, slot)
+    worst = 0.0
+    for got_bits, want_bits in ((k, stage.key_cache[layer][:, slot]), (v, stage.value_cache[layer][:, slot])):
+        got, want = bf16.from_bits(got_bits), bf16.from_bits(want_bits)
+        assert np.all(np.any(got_bits != 0, axis=-1)), f"layer {layer} slot {slot}: a head row is empty"
+        for h in range(got.shape[0]):
+            err = rel_l2(got[h], want[h])
+            worst = max(worst, err)
+            assert err <= tol, f"layer {layer} slot {slot} head {h}: rel-L2 {err:.3e}"
+            for h2 in range(got.shape[0]):
+                if h2 != h:
+                    assert rel_l2(got[h], want[h2]) > 0.5, f"layer {layer} slot {slot}: head {h} looks like {h2}"
+    return worst
+
+
+_FLOORS = {row["label"]: row["rel_l2"] for row in json.loads(
+    (Path(__file__).resolve().parent / "golden" / "order_sensitivity.json").read_text())}
+
+
+def full_depth_tol(label):
+    """1.3 times the oracle's own summation-order floor for this workload
+    (the oracle against itself with exactly rounded projections)."""
+    return 1.3 * _FLOORS[label]

@@ -6,12 +6,14 @@ validate_engine_npu.py):
 - teacher-forced: both sides see the oracle's token sequence; per-step logits
   must agree within rel-L2 <= 1e-2 and the argmax must agree unless the
   oracle's top-2 gap is below 2**-7 relative (a bf16 near-tie);
-  at full depth (24 / 30 layers) the oracle itself moves by 1.4-1.6% rel-L2
+  at full depth (24 / 30 layers) the oracle itself moves by 1.4-1.7% rel-L2
   when only its float32 summation order changes (tests/golden/
   order_sensitivity.json, made by order_sensitivity.py there), so no
-  reordered implementation can meet 1e-2 there; full-depth models are held
-  to 2.5e-2 and the 1e-2 bound is checked on 4-layer models of the same width
-  (floor 0.65-0.7%);
+  reordered implementation can meet 1e-2 there; each full-depth model is
+  held to 1.3 times its own measured floor (SmolLM2 1.84e-2, Qwen 2.06e-2,
+  Qwen W8 2.20e-2, and the floors of the 4064-token workload for it) and
+  the 1e-2 bound is checked on 4-layer models of the same width (floor
+  0.65-0.7%);
 - free-running greedy: the engine's own generated ids equal the oracle's up to
   the first near-tie step;
 - KV slot indexing: slot p is written at step p only (slots above the last
@@ -23,7 +25,7 @@ import os
 import numpy as np
 import pytest
 
-from _util import announce, near_tie, rel_l2
+from _util import announce, check_kv_slot as _check_kv_slot, full_depth_tol, near_tie, rel_l2
 from oracle import bf16
 from oracle.cpu_backend import OracleDecoder
 from runtime.synthetic import QWEN25_05B, SMOLLM2_135M, SyntheticModel
@@ -102,32 +104,14 @@ def _check_decode(model, prompt, new_tokens, context, *, w8=False, label="", tol
         engine.close()
 
 
-def _check_kv_slot(engine, stage, layer, slot, tol):
-    """KV slot `slot` of `layer` holds the oracle's key and value rows: each
-    KV head within rel-L2 `tol` of the oracle's same head and far from every
-    other head (a head written to the wrong place fails), nothing zero."""
-    k, v = engine.read_kv(layer, slot)
-    worst = 0.0
-    for got_bits, want_bits in ((k, stage.key_cache[layer][:, slot]), (v, stage.value_cache[layer][:, slot])):
-        got, want = bf16.from_bits(got_bits), bf16.from_bits(want_bits)
-        assert np.all(np.any(got_bits != 0, axis=-1)), f"layer {layer} slot {slot}: a head row is empty"
-        for h in range(got.shape[0]):
-            err = rel_l2(got[h], want[h])
-            worst = max(worst, err)
-            assert err <= tol, f"layer {layer} slot {slot} head {h}: rel-L2 {err:.3e}"
-            for h2 in range(got.shape[0]):
-                if h2 != h:
-                    assert rel_l2(got[h], want[h2]) > 0.5, f"layer {layer} slot {slot}: head {h} looks like {h2}"
-    return worst
-
-
-FULL_DEPTH_TOL = 2.5e-2  # 1.6-1.8x the oracle's own summation-order floor
+SMOL_TOL = full_depth_tol("smollm2-135m full depth, last prompt position")
+QWEN_TOL = full_depth_tol("qwen2.5-0.5b full depth, last prompt position")
+QWEN_W8_TOL = full_depth_tol("qwen2.5-0.5b W8 full depth, last prompt position")
 
 
 def test_smollm_135m_shape_decode(smol_model):
     """SmolLM2-135M shape: 35-token prompt, greedy 16 tokens, 64-slot context."""
-    _check_decode(smol_model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m",
-                  tol=FULL_DEPTH_TOL)
+    _check_decode(smol_model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m", tol=SMOL_TOL)
 
 
 def test_smollm_4_layer_decode_within_1e2():
@@ -137,8 +121,7 @@ def test_smollm_4_layer_decode_within_1e2():
 
 def test_qwen_05b_shape_decode(qwen_model):
     """Qwen2.5-0.5B shape: 40-token prompt, greedy 32 tokens (slots 0..70)."""
-    _check_decode(qwen_model, _prompt(151936, 40, 12), 32, 72, label="qwen2.5-0.5b",
-                  tol=FULL_DEPTH_TOL)
+    _check_decode(qwen_model, _prompt(151936, 40, 12), 32, 72, label="qwen2.5-0.5b", tol=QWEN_TOL)
 
 
 def test_qwen_4_layer_decode_within_1e2():
@@ -149,7 +132,7 @@ def test_qwen_4_layer_decode_within_1e2():
 def test_qwen_05b_shape_w8_decode(qwen_model):
     """W8 layer projections (int8 + per-row scale), bf16 LM head."""
     _check_decode(qwen_model, _prompt(151936, 40, 13), 32, 72, w8=True, label="qwen2.5-0.5b-w8",
-                  tol=FULL_DEPTH_TOL)
+                  tol=QWEN_W8_TOL)
 
 
 def test_qwen_4_layer_w8_decode_within_1e2():
@@ -248,6 +231,7 @@ def test_xcd_split_is_selected_by_context():
             engine.close()
     finally:
         del os.environ["HK_XCD_SPLIT"]
+
 
 
 def test_undivided_step_short_context(monkeypatch):
@@ -465,6 +449,18 @@ def test_long_form_at_context_4096_matches_oracle(w8):
     model = SyntheticModel(QWEN25_05B, seed=21, layers=2)
     _check_prefill_decode(model, _prompt(151936, 4064, 31), 9, 4096, kinds=("xcd_split_long",), w8=w8,
                           label="qwen-2L-4064")
+
+
+@pytest.mark.parametrize("w8", [False, True], ids=["bf16", "w8"])
+def test_full_depth_context_4096_matches_oracle(qwen_model, w8):
+    """The context-4096 workload at full depth (24 layers): a 4064-token
+    prompt in one batched prefill against the oracle's, then four
+    teacher-forced decode steps at positions 4064..4067 on the long form of
+    the split step, logits within 1.3 times the oracle's own summation-order
+    floor for this workload, and KV slots checked per head."""
+    label = f"qwen2.5-0.5b{' W8' if w8 else ''} full depth, 4064-token prefill + 4 steps"
+    _check_prefill_decode(qwen_model, _prompt(151936, 4064, 31), 5, 4096, kinds=("xcd_split_long",), w8=w8,
+                          label="qwen-24L-4064", tol=full_depth_tol(label))
 
 
 def test_split_forms_across_position_768_match_oracle():

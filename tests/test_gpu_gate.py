@@ -20,17 +20,29 @@ then spread like a trained model's (standard deviation near 4) and a 0.5 gap
 is as strict as it is on the reference's model; with unit gains nearly every
 position would be a near-tie.
 
-The bars: neither path may have a hard miss at all (the reference allows the
-engine one more than the chunked path), and the engine must agree with the
-oracle at least as well as the per-kernel path in the sense that matters for
-a float-order difference: its teacher-forced logits' mean rel-L2 to the
-oracle is at most 1.1 times the per-kernel path's.  The reference's top-1
-count bar (within 6 of the chunked path) is reported but not asserted: on
-these random-init models a quarter of the positions have a top-2 gap below
-0.5, and the count moves with flips at gaps below 0.07 that only the float32
-summation order decides (measured on SmolLM2-135M bf16: engine 369/378 and
-per-kernel 376/378, all misses at gaps of 0.003-0.067, while the engine's
-logits were the closer of the two, mean rel-L2 1.260e-2 against 1.271e-2).
+The bars:
+- neither path may have a hard miss at all (the reference allows the engine
+  one more than the chunked path);
+- every miss of the engine is a near-tie in the sense of its parity
+  contract: the oracle's top-2 gap is below 2^-7 of its top logit's
+  magnitude (on these models |top1| is 15-22, so that is a gap of about
+  0.12-0.17, tighter than the reference's absolute 0.5).  The per-kernel
+  path, in the role of the reference's chunked path, is held to the
+  reference's own rule for it (no hard miss): at full depth the oracle moves
+  by 1.4-1.7% rel-L2 under a change of float32 summation order alone, and
+  a miss of that path at a gap of 0.87% of |top1| has been seen (SmolLM2 W8,
+  gap 0.142 at |top1| 16.2);
+- the engine agrees with the oracle at least as well as the per-kernel path
+  in the sense that matters for a float-order difference: its teacher-forced
+  logits' mean rel-L2 to the oracle is at most 1.1 times the per-kernel
+  path's;
+- the reference's top-1 count bar (within 6 of the chunked path), on every
+  configuration but SmolLM2-135M bf16.  There the count moves with flips at
+  gaps below 0.07 that only the float32 summation order decides (measured:
+  engine 369/378 and per-kernel 376/378, all misses at gaps of 0.003-0.067,
+  i.e. below 0.0041 of |top1|, while the engine's logits were the closer of
+  the two, mean rel-L2 1.260e-2 against 1.271e-2), so for that one the count
+  is reported and the near-tie bar above holds its misses instead.
 """
 
 import numpy as np
@@ -51,6 +63,7 @@ PROMPTS = [
     "Translate 'good morning' into French and Spanish.",
 ]
 NEAR_TIE = 0.5
+NEAR_TIE_REL = 2.0 ** -7
 TOKENS = 31
 TOLERANCE = 6
 CONTEXT = 64
@@ -85,7 +98,7 @@ def _agreement(model, w8, sequences, references, oracle_logits):
 
     engine = QwenDecoderEngine(model, context_length=CONTEXT, w8=w8)
     exact = total = 0
-    hard, soft, errors = [], [], []
+    hard, soft, errors, not_tie = [], [], [], []
     try:
         kind = engine.step_kind(CONTEXT - 2)
         for index, sequence in enumerate(sequences):
@@ -98,13 +111,17 @@ def _agreement(model, w8, sequences, references, oracle_logits):
                 total += 1
                 if int(np.argmax(logits)) == want["top_token_ids"][0]:
                     exact += 1
-                elif want["top_logit_margin"] >= NEAR_TIE:
-                    hard.append((index, position, round(want["top_logit_margin"], 3)))
+                    continue
+                gap = want["top_logit_margin"]
+                if gap >= NEAR_TIE_REL * abs(float(np.max(ref))):
+                    not_tie.append((index, position, round(gap, 4), round(float(np.max(ref)), 3)))
+                if gap >= NEAR_TIE:
+                    hard.append((index, position, round(gap, 3)))
                 else:
-                    soft.append(round(want["top_logit_margin"], 3))
+                    soft.append(round(gap, 3))
     finally:
         engine.close()
-    return kind, exact, total, hard, soft, errors
+    return kind, exact, total, hard, soft, errors, not_tie
 
 
 @pytest.mark.parametrize("family,w8", [("smollm", True), ("smollm", False), ("qwen", False), ("qwen", True)],
@@ -121,12 +138,16 @@ def test_six_prompt_agreement_gate(family, w8, monkeypatch, tmp_path):
     chunked = _agreement(model, w8, sequences, references, oracle_logits)
     monkeypatch.delenv("HK_PERSISTENT")
     engine = _agreement(model, w8, sequences, references, oracle_logits)
-    for name, (kind, exact, total, hard, soft, errors) in (("per-kernel", chunked), ("engine", engine)):
+    for name, (kind, exact, total, hard, soft, errors, _) in (("per-kernel", chunked), ("engine", engine)):
         announce(f"  {name} ({kind}): top-1 {exact}/{total}, hard misses {hard}, near-tie misses (gaps) "
                  f"{sorted(soft)}, logits rel-L2 mean {np.mean(errors):.3e} max {np.max(errors):.3e}")
     assert chunked[0] != engine[0], "the two runs took the same step form"
     assert not engine[3] and not chunked[3], "a hard miss: the oracle's top-2 gap was at least 0.5"
+    assert not engine[6], f"an engine miss outside the near-ties (gap >= 2^-7 |top1|): {engine[6]}"
     assert np.mean(engine[5]) <= 1.1 * np.mean(chunked[5])
-    if engine[1] + TOLERANCE < chunked[1]:
-        announce(f"  (the reference's count bar would not hold: {engine[1]} + {TOLERANCE} < {chunked[1]}, "
-                 f"all misses near-ties)")
+    if family == "smollm" and not w8:
+        if engine[1] + TOLERANCE < chunked[1]:
+            announce(f"  (the reference's count bar does not hold here: {engine[1]} + {TOLERANCE} < {chunked[1]}, "
+                     f"every miss a near-tie)")
+    else:
+        assert engine[1] + TOLERANCE >= chunked[1], "the reference's top-1 count bar"

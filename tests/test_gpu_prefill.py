@@ -5,7 +5,7 @@ arithmetic, and whole-model prefill against the oracle's per-position prefill
 import numpy as np
 import pytest
 
-from _util import announce, check_bf16, fwd_bound, near_tie, rel_l2
+from _util import announce, check_bf16, check_kv_slot, full_depth_tol, fwd_bound, near_tie, rel_l2
 from oracle import bf16
 from oracle.cpu_backend import OracleDecoder
 from runtime.synthetic import QWEN25_05B, SMOLLM2_135M, SyntheticModel
@@ -79,14 +79,14 @@ def _prefill_case(model, prompt, new_tokens, context, tol, label, w8=False):
         announce(f"  prefill logits rel-L2 {err:.3e}, token {tok} oracle {ref_tokens[0]}")
         assert err <= tol
         assert tok == ref_tokens[0] or near_tie(ref_logits[0])
-        # KV slots of the prompt against the oracle's caches
+        # KV slots of the prompt against the oracle's caches: each head
+        # within twice the logits bound of the oracle's same head and far
+        # from every other head
+        worst = 0.0
         for layer in (0, model.metadata["layers"] - 1):
-            for slot in (0, len(prompt) - 1):
-                k, v = engine.read_kv(layer, slot)
-                rk = bf16.from_bits(oracle.stage.key_cache[layer][:, slot])
-                rv = bf16.from_bits(oracle.stage.value_cache[layer][:, slot])
-                assert np.abs(bf16.from_bits(k) - rk).max() <= 0.05 * np.abs(rk).max() + 1e-3
-                assert np.abs(bf16.from_bits(v) - rv).max() <= 0.05 * np.abs(rv).max() + 1e-3
+            for slot in sorted({0, len(prompt) // 2, len(prompt) - 1}):
+                worst = max(worst, check_kv_slot(engine, oracle.stage, layer, slot, 2 * tol))
+        announce(f"  KV slots: worst per-head rel-L2 {worst:.3e}")
         if tok == ref_tokens[0] and new_tokens > 1:
             gen = engine.generate(tok, len(prompt), new_tokens - 1)
             for i, (a, b) in enumerate(zip(gen, ref_tokens[1:])):
@@ -114,7 +114,24 @@ def test_prefill_smollm_4_layer():
 
 def test_prefill_qwen_full_depth():
     model = SyntheticModel(QWEN25_05B, seed=0)
-    _prefill_case(model, _prompt(151936, 40, 12), 4, 72, 2.5e-2, "qwen2.5-0.5b")
+    _prefill_case(model, _prompt(151936, 40, 12), 4, 72,
+                  full_depth_tol("qwen2.5-0.5b full depth, last prompt position"), "qwen2.5-0.5b")
+
+
+# A shape wider than the slab GEMMs' fused RMSNorm takes (hidden > 1024):
+# chunks of up to 64 tokens then run the slab GEMMs on row-major
+# activations, with separate RMSNorm and RoPE/KV-append launches.
+WIDE_1152 = dict(QWEN25_05B, hidden_size=1152, intermediate_size=3072, attention_heads=18, kv_heads=3,
+                 layers=2, vocab_size=4096)
+
+
+@pytest.mark.parametrize("n", [1, 17, 64])
+def test_prefill_hidden_1152_short_prompts(n):
+    """Hidden 1152 (18 query heads, 3 KV heads, intermediate 3072): prompts of
+    1, 17 and 64 tokens against the oracle, logits, greedy continuation and
+    KV slots per head."""
+    model = SyntheticModel(WIDE_1152, seed=8)
+    _prefill_case(model, _prompt(4096, n, 40 + n), 4, 72, 1e-2, f"hidden-1152-2L-{n}")
 
 
 def test_prefill_long_prompt():

@@ -97,6 +97,57 @@ def test_top_p_keeps_the_token_that_crosses_the_threshold():
     assert np.isfinite(out[0]) and np.isneginf(out[1:]).all()
 
 
+def test_top_p_takes_ties_in_the_order_of_numpys_argsort_reversed():
+    # The reference orders by the ascending default argsort read backwards
+    # (sampling.py:388), which is not the stable descending order: with three
+    # ties of p = e / (3e + 1) = 0.297 each, top_p 0.5 keeps the first two
+    # ties of that order, whichever ids they are, and the crossing token too.
+    x = np.array([1.0, 1.0, 1.0, 0.0], dtype=np.float32)
+    order = np.argsort(x)[::-1]
+    out = filter_top_p(x.copy(), 0.5)
+    assert sorted(np.flatnonzero(np.isfinite(out)).tolist()) == sorted(order[:2].tolist())
+    two = 2 * math.e / (3 * math.e + 1)
+    out = filter_top_p(x.copy(), two + 1e-3)  # just above two ties' mass: the third stays
+    assert np.flatnonzero(np.isfinite(out)).tolist() == [0, 1, 2]
+
+
+def test_top_p_on_tied_scores_follows_the_documented_rule():
+    # heavily tied scores (rounded to 0.5; up to 200 of them, where numpy's
+    # argsort does not keep ties in id order): along numpy's argsort read
+    # backwards, a token stays exactly when the probability mass before it is
+    # below top_p (the first always)
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        n = int(rng.integers(2, 200))
+        x = (np.round(rng.normal(size=n) * 2) / 2).astype(np.float32)
+        top_p = float(rng.uniform(0.05, 0.95))
+        out = filter_top_p(x.copy(), top_p)
+        order = np.argsort(x)[::-1]
+        e = np.exp(x.astype(np.float64) - x.max())
+        p = e / e.sum()
+        mass = 0.0
+        for rank, i in enumerate(order):
+            kept = bool(np.isfinite(out[i]))
+            if rank == 0:
+                assert kept
+            elif abs(mass - top_p) > 1e-6:  # away from float32 rounding of the edge
+                assert kept == (mass < top_p), (x.tolist(), top_p, i)
+            mass += p[i]
+
+
+def test_seeded_draws_on_tied_scores_repeat_across_samplers():
+    # bf16-valued scores tie often; two samplers with one seed draw the same
+    # tokens, and every draw lies inside the nucleus the filter keeps
+    rng = np.random.default_rng(5)
+    x = (np.round(rng.normal(size=12) * 4) / 4).astype(np.float32)
+    p = SamplingParams.build(temperature=1.0, top_p=0.7, seed=99)
+    a, b = Sampler(p, vocab_size=12), Sampler(p, vocab_size=12)
+    keep = np.isfinite(filter_top_p(x.copy(), 0.7))
+    for _ in range(200):
+        t = a.select(x)
+        assert t == b.select(x) and keep[t]
+
+
 def test_sampler_draws_from_the_filtered_distribution_reproducibly():
     logits = np.log(np.array([0.6, 0.3, 0.1], dtype=np.float32))
     p = SamplingParams.build(temperature=1.0, top_k=2, seed=1234)
