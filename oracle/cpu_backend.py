@@ -183,11 +183,21 @@ class CPUDecoderStage:
         out = np.einsum("kqs,ksd->kqd", probabilities, values, optimize=True)
         return round_f32(out.reshape(-1))
 
+    # prompts of at least this many rows score their attention with batched
+    # BLAS matrix products instead of ``attention``'s einsum (minutes instead
+    # of hours for 4096-token prompts at full depth); only the float32
+    # summation order differs
+    BLAS_ROWS = 256
+
     def attention_rows(self, qkv_rows, layer, start, block=256):
         """``attention`` for rows at positions start..start+n-1 at once: every
         row's RoPE and KV append first, then each row attends to slots
         0..its position (causal), as n calls of ``attention`` in order would.
-        Rows are scored in blocks of ``block`` to bound the score matrix."""
+        Rows are scored in blocks of ``block`` to bound the score matrix.
+        Below ``BLAS_ROWS`` rows the products are ``attention``'s own einsum
+        contractions, which sum each output in the order the per-position
+        calls do (the two agree bit for bit); from ``BLAS_ROWS`` rows they are
+        batched matrix products."""
         d = self.head_dim
         nq = self.q_heads * d
         nkv = self.kv_heads * d
@@ -214,17 +224,28 @@ class CPUDecoderStage:
         out = np.empty((n, self.q_heads, d), dtype=np.float32)
         grouped = query.reshape(n, self.kv_heads, self.q_per_kv, d)
         slots = np.arange(end)
+        blas = n >= self.BLAS_ROWS
+        keys_t = np.ascontiguousarray(keys.transpose(0, 2, 1)) if blas else None  # [kvh, d, end]
         for r0 in range(0, n, block):
             r1 = min(n, r0 + block)
+            rows = r1 - r0
             q = grouped[r0:r1].transpose(1, 0, 2, 3)          # [kvh, rows, qpk, d]
-            scores = np.einsum("krqd,ksd->krqs", q, keys, optimize=True) * d**-0.5
+            if blas:  # [kvh, rows * qpk, d] @ [kvh, d, end]
+                q = np.ascontiguousarray(q).reshape(self.kv_heads, -1, d)
+                scores = (np.matmul(q, keys_t) * d**-0.5).reshape(self.kv_heads, rows, self.q_per_kv, end)
+            else:
+                scores = np.einsum("krqd,ksd->krqs", q, keys, optimize=True) * d**-0.5
             future = slots[None, :] > positions[r0:r1, None]  # [rows, end]
-            scores[:, future[:, None, :].repeat(self.q_per_kv, axis=1)] = -np.inf
+            scores += np.where(future, -np.inf, 0.0).astype(np.float32)[None, :, None, :]
             scores -= np.max(scores, axis=-1, keepdims=True)
             probabilities = np.exp(scores)
             probabilities /= np.sum(probabilities, axis=-1, keepdims=True)
-            o = np.einsum("krqs,ksd->krqd", probabilities, values, optimize=True)
-            out[r0:r1] = o.transpose(1, 0, 2, 3).reshape(r1 - r0, self.q_heads, d)
+            if blas:
+                o = np.matmul(probabilities.reshape(self.kv_heads, -1, end), values).reshape(
+                    self.kv_heads, rows, self.q_per_kv, d)
+            else:
+                o = np.einsum("krqs,ksd->krqd", probabilities, values, optimize=True)
+            out[r0:r1] = o.transpose(1, 0, 2, 3).reshape(rows, self.q_heads, d)
         return round_f32(out.reshape(n, -1))
 
     def layer_rows(self, hidden_rows, layer, start):
@@ -329,12 +350,13 @@ class OracleDecoder:
         logits = self.stage.logits(hidden)
         return decode_result(logits), logits
 
-    def prefill(self, prompt_ids, start=0, compute_logits=True):
+    def prefill(self, prompt_ids, start=0, compute_logits=True, progress=None):
         """Every prompt token at slots start..start+n-1 with logits at the last
         one, like ``decode_token`` position by position (generate.py:1110-1125)
         but with each layer applied to all rows at once (matrix products and
         causal attention); only float32 summation orders differ.  Returns
-        ``(next_token, logits)`` or ``(None, None)``."""
+        ``(next_token, logits)`` or ``(None, None)``.  ``progress(layer)``, if
+        given, is called after each layer (long prompts take minutes)."""
         ids = [int(t) for t in prompt_ids]
         if not ids:
             raise ValueError("prefill needs at least one token")
@@ -343,6 +365,8 @@ class OracleDecoder:
         hidden = round_f32(self._embedding[np.asarray(ids)])
         for layer in range(self.layers):
             hidden = self.stage.layer_rows(hidden, layer, start)
+            if progress is not None:
+                progress(layer)
         if not compute_logits:
             return None, None
         logits = self.stage.logits(hidden[-1])

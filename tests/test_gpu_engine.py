@@ -393,7 +393,10 @@ def _check_prefill_decode(model, prompt, new_tokens, context, *, kinds, w8=False
     n = len(prompt)
     announce(f"prefill+decode parity {label}: prompt {n} new {new_tokens} ctx {context} w8={w8}")
     oracle = OracleDecoder(model, context, w8=w8)
-    first, lg0 = oracle.prefill(prompt)
+    layers = model.metadata["layers"]
+    # a long prompt at full depth keeps the oracle busy for minutes: a line per layer
+    progress = (lambda layer: announce(f"  oracle prefill: layer {layer + 1}/{layers}")) if n * layers > 20000 else None
+    first, lg0 = oracle.prefill(prompt, progress=progress)
     ref_tokens, ref_logits = [first], [lg0]
     while len(ref_tokens) < new_tokens:
         tok, lg = oracle.decode_token(ref_tokens[-1], n + len(ref_tokens) - 1)

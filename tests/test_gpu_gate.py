@@ -23,15 +23,16 @@ position would be a near-tie.
 The bars:
 - neither path may have a hard miss at all (the reference allows the engine
   one more than the chunked path);
-- every miss of the engine is a near-tie in the sense of its parity
-  contract: the oracle's top-2 gap is below 2^-7 of its top logit's
-  magnitude (on these models |top1| is 15-22, so that is a gap of about
-  0.12-0.17, tighter than the reference's absolute 0.5).  The per-kernel
-  path, in the role of the reference's chunked path, is held to the
-  reference's own rule for it (no hard miss): at full depth the oracle moves
-  by 1.4-1.7% rel-L2 under a change of float32 summation order alone, and
-  a miss of that path at a gap of 0.87% of |top1| has been seen (SmolLM2 W8,
-  gap 0.142 at |top1| 16.2);
+- every miss of either path is explained by float32 summation order: the
+  oracle's top-2 gap there is below 2^-7 of its top logit's magnitude (the
+  parity contract's near-tie) or below four standard deviations of the
+  gap's movement under a change of summation order alone at that position
+  (sqrt(2) times the per-logit standard deviation of the oracle against
+  itself with exactly rounded sums, tests/golden/gate_order_floor.json).
+  The 2^-7 near-tie alone cannot be met at full depth: the exact-sum oracle
+  itself flips the argmax at a gap of 0.0095 |top1| on the Qwen2.5-0.5B W8
+  sequences, and the per-position noise there is about 0.085 (a gap
+  standard deviation near 0.12);
 - the engine agrees with the oracle at least as well as the per-kernel path
   in the sense that matters for a float-order difference: its teacher-forced
   logits' mean rel-L2 to the oracle is at most 1.1 times the per-kernel
@@ -42,8 +43,11 @@ The bars:
   engine 369/378 and per-kernel 376/378, all misses at gaps of 0.003-0.067,
   i.e. below 0.0041 of |top1|, while the engine's logits were the closer of
   the two, mean rel-L2 1.260e-2 against 1.271e-2), so for that one the count
-  is reported and the near-tie bar above holds its misses instead.
+  is reported and the bar above holds its misses instead.
 """
+
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -64,6 +68,8 @@ PROMPTS = [
 ]
 NEAR_TIE = 0.5
 NEAR_TIE_REL = 2.0 ** -7
+ORDER_SIGMAS = 4.0
+FLOOR = Path(__file__).resolve().parent / "golden" / "gate_order_floor.json"
 TOKENS = 31
 TOLERANCE = 6
 CONTEXT = 64
@@ -93,12 +99,16 @@ def _sequences(model, oracle, tmp_path):
     return sequences, references, logits
 
 
-def _agreement(model, w8, sequences, references, oracle_logits):
+def _agreement(model, w8, sequences, references, oracle_logits, noise):
+    """Teacher-forced agreement of one step form with the oracle.  Returns
+    (step kind, top-1 count, positions, hard misses, gaps of the other
+    misses, per-position logits rel-L2, misses that neither the 2^-7
+    near-tie nor the summation-order noise explains)."""
     from runtime.qwen_engine import QwenDecoderEngine
 
     engine = QwenDecoderEngine(model, context_length=CONTEXT, w8=w8)
     exact = total = 0
-    hard, soft, errors, not_tie = [], [], [], []
+    hard, soft, errors, unexplained = [], [], [], []
     try:
         kind = engine.step_kind(CONTEXT - 2)
         for index, sequence in enumerate(sequences):
@@ -113,15 +123,17 @@ def _agreement(model, w8, sequences, references, oracle_logits):
                     exact += 1
                     continue
                 gap = want["top_logit_margin"]
-                if gap >= NEAR_TIE_REL * abs(float(np.max(ref))):
-                    not_tie.append((index, position, round(gap, 4), round(float(np.max(ref)), 3)))
+                sigma = np.sqrt(2.0) * noise[total - 1]
+                if gap >= max(NEAR_TIE_REL * abs(float(np.max(ref))), ORDER_SIGMAS * sigma):
+                    unexplained.append((index, position, round(gap, 4), round(float(np.max(ref)), 3),
+                                        round(gap / sigma, 2)))
                 if gap >= NEAR_TIE:
                     hard.append((index, position, round(gap, 3)))
                 else:
                     soft.append(round(gap, 3))
     finally:
         engine.close()
-    return kind, exact, total, hard, soft, errors, not_tie
+    return kind, exact, total, hard, soft, errors, unexplained
 
 
 @pytest.mark.parametrize("family,w8", [("smollm", True), ("smollm", False), ("qwen", False), ("qwen", True)],
@@ -134,16 +146,21 @@ def test_six_prompt_agreement_gate(family, w8, monkeypatch, tmp_path):
     margins = np.array([r["top_logit_margin"] for ref in references for r in ref])
     announce(f"  {len(margins)} positions, oracle top-2 gap median {np.median(margins):.3f}, "
              f"{(margins < NEAR_TIE).mean():.0%} below {NEAR_TIE}")
+    floor = json.loads(FLOOR.read_text())[f"{family}-{'w8' if w8 else 'bf16'}"]
+    assert floor["sequences"] == [list(map(int, q)) for q in sequences], "the noise fixture's sequences differ"
+    noise = np.asarray(floor["noise"])
     monkeypatch.setenv("HK_PERSISTENT", "0")
-    chunked = _agreement(model, w8, sequences, references, oracle_logits)
+    chunked = _agreement(model, w8, sequences, references, oracle_logits, noise)
     monkeypatch.delenv("HK_PERSISTENT")
-    engine = _agreement(model, w8, sequences, references, oracle_logits)
+    engine = _agreement(model, w8, sequences, references, oracle_logits, noise)
     for name, (kind, exact, total, hard, soft, errors, _) in (("per-kernel", chunked), ("engine", engine)):
         announce(f"  {name} ({kind}): top-1 {exact}/{total}, hard misses {hard}, near-tie misses (gaps) "
                  f"{sorted(soft)}, logits rel-L2 mean {np.mean(errors):.3e} max {np.max(errors):.3e}")
     assert chunked[0] != engine[0], "the two runs took the same step form"
     assert not engine[3] and not chunked[3], "a hard miss: the oracle's top-2 gap was at least 0.5"
-    assert not engine[6], f"an engine miss outside the near-ties (gap >= 2^-7 |top1|): {engine[6]}"
+    for name, run in (("per-kernel", chunked), ("engine", engine)):
+        assert not run[6], (f"{name} misses that neither the 2^-7 near-tie nor {ORDER_SIGMAS:g} sigma of "
+                            f"summation-order noise explains (sequence, position, gap, top1, gap/sigma): {run[6]}")
     assert np.mean(engine[5]) <= 1.1 * np.mean(chunked[5])
     if family == "smollm" and not w8:
         if engine[1] + TOLERANCE < chunked[1]:

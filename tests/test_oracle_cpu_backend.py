@@ -351,6 +351,31 @@ def test_prefill_rows_matches_per_position_decode(w8):
         assert np.linalg.norm(logits - f64) / np.linalg.norm(f64) < 2e-2
 
 
+def test_prefill_rows_blas_products_agree_with_the_einsum():
+    """From CPUDecoderStage.BLAS_ROWS rows the batched attention takes BLAS
+    matrix products instead of the einsum contractions; on the same 300 rows
+    (two KV blocks of scores, a nonzero start) the two agree to one bf16 step
+    per output or, where P @ V cancels to almost nothing, to 1e-5 absolute
+    (values are ~0.5 here); nearly all bit for bit; and the KV caches they
+    write are identical (the append precedes the scores)."""
+    model = SyntheticModel(TINY, seed=9, std=0.15)
+    rng = np.random.default_rng(23)
+    outs, caches = [], []
+    for blas_rows in (10 ** 9, 1):
+        dec = OracleDecoder(model, 320)
+        st = dec.stage
+        st.BLAS_ROWS = blas_rows
+        qkv = np.asarray(rng.normal(size=(300, (st.q_heads + 2 * st.kv_heads) * st.head_dim)) * 0.5, np.float32)
+        rng = np.random.default_rng(23)  # the same rows for both
+        outs.append(st.attention_rows(qkv, 0, 7, block=256))
+        caches.append((st.key_cache[0].copy(), st.value_cache[0].copy()))
+    from _util import bf16_ulp_diff
+    from oracle.bf16 import to_bits
+    diff = bf16_ulp_diff(to_bits(outs[0]), to_bits(outs[1]))
+    assert np.all((diff <= 1) | (np.abs(outs[0] - outs[1]) <= 1e-5)) and (diff == 0).mean() >= 0.99
+    assert np.array_equal(caches[0][0], caches[1][0]) and np.array_equal(caches[0][1], caches[1][1])
+
+
 def test_prefill_rows_blocks_and_offset_start():
     """Rows scored in several blocks, a prompt starting at a nonzero slot, and
     a continuation after an earlier prefill give the per-position result."""
