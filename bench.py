@@ -168,8 +168,10 @@ def gemv_microbench(launches=200):
     """Isolated batch-1 GEMVs at the Qwen2.5-0.5B projection shapes, bf16 and
     W8 (int8 + per-row scale) weights, float32 output.  Each shape rotates
     through enough distinct weight copies to exceed 512 MiB, so the 256 MB
-    Infinity Cache cannot serve them; timed with HIP events around the
-    enqueued launches.  Bytes per launch = weights (+ scales) + x + y."""
+    Infinity Cache cannot serve them; timed with HIP events around one graph
+    replay of the launches (directly enqueued, each launch would cost the
+    host about as long as the kernel runs).  Bytes per launch = weights
+    (+ scales) + x + y."""
     import ctypes
 
     import numpy as np
@@ -192,15 +194,24 @@ def gemv_microbench(launches=200):
                 data, scale = quantize_rows(from_bf16(to_bits(w)))
             wbytes = data.nbytes
             copies = max(2, -(-ROTATE_BYTES // wbytes))
+            # the copies sit 4 KiB-aligned in one allocation, so every shape
+            # sees the same page mapping (separate allocations of a few
+            # hundred KB each timed up to 2x apart from run to run)
+            stride = -(-wbytes // 4096) * 4096
             first = hip.DeviceBuffer.from_array(data)
-            bufs = [first] + [hip.DeviceBuffer(wbytes) for _ in range(copies - 1)]
-            for b in bufs[1:]:
-                hip.check(lib.hk_memcpy_d2d(b.ptr, first.ptr, wbytes), "copy")
-            ptrs = (ctypes.c_void_p * copies)(*[b.ptr for b in bufs])
+            pool = hip.DeviceBuffer(stride * copies)
+            for i in range(copies):
+                hip.check(lib.hk_memcpy_d2d(pool.ptr + i * stride, first.ptr, wbytes), "copy")
+            bufs = [first, pool]
+            ptrs = (ctypes.c_void_p * copies)(*[pool.ptr + i * stride for i in range(copies)])
             sbuf = hip.DeviceBuffer.from_array(scale) if scale is not None else None
             sptrs = (ctypes.c_void_p * copies)(*([sbuf.ptr] * copies)) if sbuf else None
             ev0, ev1 = hip.Event(), hip.Event()
-            hip.check(lib.hk_gemv_repeat(ptrs, sptrs, copies, x.ptr, y.ptr, m, k, copies, None), "warm")
+            # two warm rotations: every copy's pages have been touched by a
+            # launch before the timed ones
+            hip.check(lib.hk_gemv_repeat(ptrs, sptrs, copies, x.ptr, y.ptr, m, k, 2 * copies, None), "warm")
+            # the timed call replays the graph this untimed one captures
+            hip.check(lib.hk_gemv_repeat(ptrs, sptrs, copies, x.ptr, y.ptr, m, k, launches, None), "capture")
             ev0.record(None)
             hip.check(lib.hk_gemv_repeat(ptrs, sptrs, copies, x.ptr, y.ptr, m, k, launches, None), "gemv")
             ev1.record(None)

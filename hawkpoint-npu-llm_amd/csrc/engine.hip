@@ -1105,17 +1105,83 @@ int hk_engine_launch_part_repeat(hk_engine* e, int32_t part, int32_t count) {
   return 0;
 }
 
+namespace {
+// hk_gemv_repeat's captured graphs, one per argument set (a timed call is a
+// replay of the graph its untimed twin captured), at most kGemvGraphs kept.
+struct GemvRepeat {
+  std::vector<const void*> w;
+  std::vector<const float*> s;
+  const uint16_t* x;
+  float* y;
+  int M, K, count, device;
+  hipGraphExec_t exec;
+};
+constexpr size_t kGemvGraphs = 32;
+std::mutex gemv_graph_mu;
+std::vector<GemvRepeat> gemv_graphs;
+}  // namespace
+
 int hk_gemv_repeat(const void* const* weights, const float* const* scales, int32_t n_weights,
                    const uint16_t* x, float* y_f32, int32_t M, int32_t K, int32_t count,
                    void* stream) {
-  if (!weights || !x || !y_f32 || n_weights <= 0 || count <= 0)
+  if (!weights || !x || !y_f32 || n_weights <= 0 || count <= 0 || count > 100000)
     return fail("hk_gemv_repeat: bad argument");
-  for (int i = 0; i < count; ++i) {
-    const int j = i % n_weights;
-    const int rc = gemv_common(weights[j], scales ? scales[j] : nullptr, x, nullptr, nullptr,
-                               nullptr, y_f32, M, K, scales != nullptr, stream);
+  auto enqueue = [&](hipStream_t s) {
+    for (int i = 0; i < count; ++i) {
+      const int j = i % n_weights;
+      const int rc = gemv_common(weights[j], scales ? scales[j] : nullptr, x, nullptr, nullptr, nullptr, y_f32,
+                                 M, K, scales != nullptr, s);
+      if (rc != 0) return rc;
+    }
+    return 0;
+  };
+  // HK_GEMV_REPEAT_GRAPH=0: direct launches (kernel tracers that do not
+  // follow graph launches); otherwise one captured graph, so the host's
+  // launch cost (about 2.5 us per launch) does not pace kernels that take
+  // about as long
+  static const bool direct = [] {
+    const char* e = getenv("HK_GEMV_REPEAT_GRAPH");
+    return e && e[0] == '0';
+  }();
+  if (direct) return enqueue(static_cast<hipStream_t>(stream));
+  int device = 0;
+  HK_CHECK(hipGetDevice(&device));
+  std::lock_guard<std::mutex> lock(gemv_graph_mu);
+  std::vector<const void*> w(weights, weights + n_weights);
+  std::vector<const float*> sc;
+  if (scales) sc.assign(scales, scales + n_weights);
+  GemvRepeat* hit = nullptr;
+  for (GemvRepeat& g : gemv_graphs)
+    if (g.w == w && g.s == sc && g.x == x && g.y == y_f32 && g.M == M && g.K == K && g.count == count &&
+        g.device == device)
+      hit = &g;
+  if (!hit) {
+    if (gemv_graphs.size() >= kGemvGraphs) {  // the oldest goes (after any replay of it has ended)
+      HK_CHECK(hipDeviceSynchronize());
+      (void)hipGraphExecDestroy(gemv_graphs.front().exec);
+      gemv_graphs.erase(gemv_graphs.begin());
+    }
+    hipStream_t cs = nullptr;
+    HK_CHECK(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
+    hipGraph_t graph = nullptr;
+    hipError_t err = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    int rc = err == hipSuccess ? enqueue(cs) : hip_fail(err, "hipStreamBeginCapture");
+    if (err == hipSuccess) {
+      const hipError_t end = hipStreamEndCapture(cs, &graph);
+      if (rc == 0 && end != hipSuccess) rc = hip_fail(end, "hipStreamEndCapture");
+    }
+    (void)hipStreamDestroy(cs);
+    hipGraphExec_t exec = nullptr;
+    if (rc == 0) {
+      const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      if (inst != hipSuccess) rc = hip_fail(inst, "hipGraphInstantiate");
+    }
+    if (graph) (void)hipGraphDestroy(graph);
     if (rc != 0) return rc;
+    gemv_graphs.push_back({std::move(w), std::move(sc), x, y_f32, M, K, count, device, exec});
+    hit = &gemv_graphs.back();
   }
+  HK_CHECK(hipGraphLaunch(hit->exec, static_cast<hipStream_t>(stream)));
   return 0;
 }
 

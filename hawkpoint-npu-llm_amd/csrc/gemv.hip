@@ -124,8 +124,8 @@ template <int LPR, bool W8, bool PAIR>
 __device__ __forceinline__ void finish_row(const GemvArgs& a, int row, bool live, int l, float a0,
                                            float a1, float b0, float b1,
                                            unsigned long long& best) {
-  float acc = group_sum<LPR>(a0 + a1);
-  float accu = PAIR ? group_sum<LPR>(b0 + b1) : 0.0f;
+  float acc = lane_sum<LPR>(a0 + a1);
+  float accu = PAIR ? lane_sum<LPR>(b0 + b1) : 0.0f;
   if (!live || l != 0) return;
   if constexpr (W8) {
     acc = acc * ldg(a.scale + row);
@@ -160,7 +160,9 @@ __device__ __forceinline__ void finish_row(const GemvArgs& a, int row, bool live
 // SwiGLU) g = wave_id, wave_id + waves_in_grid, ...; the next group's weights
 // are loaded while the current one is reduced, so a wave always has its
 // loads in flight.  Rows longer than LPR*NJ chunks take several passes.
-template <int LPR, int NJ, bool W8, bool PAIR>
+// BUF: branch-free buffer loads (always for bf16 rows; for int8 rows only
+// where they measured faster, the LM head).
+template <int LPR, int NJ, bool W8, bool PAIR, bool BUF = !W8>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   extern __shared__ float smem[];
   float* xs = smem;
@@ -189,14 +191,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   // group past the matrix takes an offset past the resource and reads zero.
   // With a branch around each load the compiler waited for all of them
   // (the next group's too) before the first product.  The host keeps the
-  // matrix below 2 GiB (32-bit offsets).  (int8 rows keep the branches:
-  // measured, the branch-free form took their GEMVs 5-25% longer, all but
-  // the LM head's.)
+  // matrix below 2 GiB (32-bit offsets).  (int8 rows keep the branches
+  // unless BUF: measured, the branch-free form took their GEMVs 5-25%
+  // longer, all but the LM head's.)
   const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, (int)((PAIR ? 2 : 1) * pair_off));
   auto load = [&](int g, int base, u32x4 (&w)[NJ], u32x4 (&u)[PAIR ? NJ : 1]) {
     const int row = g * RPW + sub;
     const bool live = g < groups && row < a.M;
-    if constexpr (W8) {
+    if constexpr (W8 && !BUF) {
       const char* wrow = static_cast<const char*>(a.W) + (size_t)(live ? row : 0) * row_bytes;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(GemvArgs a) {
         ss += hi * hi;
       }
     }
-    ss = group_sum<64>(ss);
+    ss = lane_sum<64>(ss);
     inv = 1.0f / sqrtf(ss / (float)K + a.eps);
   }
   // this lane's x chunks (normalised when asked), kept for every row group
@@ -438,6 +440,151 @@ __global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(GemvArgs a) {
   }
 }
 
+// Register-x GEMV for rows of int8 or bf16 weights, one row group (64 / LPR
+// rows) per KS waves: each of the KS waves takes a contiguous slice of the
+// row's 16-byte chunks (a split of K inside the workgroup), every lane loads
+// the x chunks of its weight chunks straight from memory (L2-resident) as
+// packed bf16 pairs, and the products run on v_dot2_f32_bf16 (int8 pairs
+// widened exactly to bf16 first).  The KS partial sums of a row meet in LDS
+// and the slice-0 wave adds them in slice order and applies the epilogue.
+// A workgroup of kWaves waves owns kWaves / KS row groups, one pass, no
+// loop.  This gives the short W8 projections (QKV, O: 36 workgroups of the
+// LDS-staged form, under one wave per CU) a wave per row group, and the long
+// bf16 rows (down_proj, K = 4864) four waves per row.
+template <int LPR, int NJ, bool W8, int KS>
+__global__ __launch_bounds__(kThreads) void gemv_rx_kernel(GemvArgs a) {
+  static_assert(kWaves % KS == 0, "whole row groups per workgroup");
+  constexpr int RPW = 64 / LPR, GPW = kWaves / KS, EPC = W8 ? 16 : 8;
+  __shared__ float part[kWaves][RPW];
+  __shared__ unsigned long long wave_keys[kWaves];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l = lane % LPR, sub = lane / LPR;
+  const int slice = wave % KS, gl = wave / KS;
+  const int K = a.K, CH = K / EPC, CHS = (CH + KS - 1) / KS, c0 = slice * CHS, c1 = min(CH, c0 + CHS);
+  const int g = blockIdx.x * GPW + gl;
+  const int row = g * RPW + sub;
+  const bool live = row < a.M;
+  const size_t row_bytes = (size_t)K * (W8 ? 1 : 2);
+
+  // weights first (the longest latency); chunks past the slice read zero
+  const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, (int)((size_t)a.M * row_bytes));
+  const unsigned rofs = (unsigned)((size_t)(live ? row : 0) * row_bytes);
+  u32x4 w[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = c0 + l + j * LPR;
+    w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, live && c < c1 ? rofs + (unsigned)c * 16u : kGemvOutside, 0, 2);
+  }
+  const uint16_t* x = a.x;
+  if (a.x_index != nullptr) {
+    int t = *a.x_index;
+    if (t >= 0) {
+      if (t >= a.vocab_limit) t = a.vocab_limit - 1;
+      x = a.x_table + (size_t)t * (size_t)K;
+      if (a.x_copy != nullptr && blockIdx.x == 0) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(x);
+        for (int i = tid; i < K / 2; i += kThreads) reinterpret_cast<uint32_t*>(a.x_copy)[i] = src[i];
+      }
+    }
+  }
+  // this lane's x values for each weight chunk as packed bf16 pairs, zero
+  // past the slice; for an RMSNorm input also the gains of the same columns
+  constexpr int XW = EPC / 2;  // x words per chunk
+  uint32_t xp[NJ][XW], gp[NJ][XW];
+  const bool norm = a.pro == PRO_NORM;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = c0 + l + j * LPR;
+    const bool ok = c < c1;
+#pragma unroll
+    for (int h = 0; h < EPC / 8; ++h) {
+      const int e0 = c * EPC + 8 * h;
+      const u32x4 v = ok ? load16(x + e0) : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 gm = ok && norm ? load16(a.gamma + e0) : u32x4{0u, 0u, 0u, 0u};
+      xp[j][4 * h] = v.x, xp[j][4 * h + 1] = v.y, xp[j][4 * h + 2] = v.z, xp[j][4 * h + 3] = v.w;
+      gp[j][4 * h] = gm.x, gp[j][4 * h + 1] = gm.y, gp[j][4 * h + 2] = gm.z, gp[j][4 * h + 3] = gm.w;
+    }
+  }
+  if (norm) {
+    // RMSNorm (cpu_backend.py:71-76): the LPR lanes of a row hold the slice's
+    // values once, so their sum of squares is the slice's; the KS slices of
+    // a row group meet in LDS (every wave holds the same x)
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int q = 0; q < XW; ++q) {
+        const float lo = bf_lo(xp[j][q]), hi = bf_hi(xp[j][q]);
+        ss += lo * lo;
+        ss += hi * hi;
+      }
+    ss = lane_sum<LPR>(ss);
+    if constexpr (KS > 1) {
+      if (lane == 0) part[wave][0] = ss;
+      __syncthreads();
+      ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) ss += part[gl * KS + k][0];
+      __syncthreads();  // part is reused for the row sums
+    }
+    const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+    // bf16((v * inv) * gamma), exact in bf16
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int q = 0; q < XW; ++q) {
+        const float n0 = round_bf16((bf_lo(xp[j][q]) * inv) * bf_lo(gp[j][q]));
+        const float n1 = round_bf16((bf_hi(xp[j][q]) * inv) * bf_hi(gp[j][q]));
+        xp[j][q] = (__float_as_uint(n0) >> 16) | (__float_as_uint(n1) & 0xffff0000u);
+      }
+  }
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t ww[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+    if constexpr (W8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a0 = dot2_bf16(i8pair_bf16(ww[q], 0), xp[j][2 * q], a0);
+        a1 = dot2_bf16(i8pair_bf16(ww[q], 2), xp[j][2 * q + 1], a1);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q += 2) {
+        a0 = dot2_bf16(ww[q], xp[j][q], a0);
+        a1 = dot2_bf16(ww[q + 1], xp[j][q + 1], a1);
+      }
+    }
+  }
+  unsigned long long best = 0ull;
+  if constexpr (KS == 1) {
+    finish_row<LPR, W8, false>(a, row, live, l, a0, a1, 0.f, 0.f, best);
+  } else {
+    const float s = lane_sum<LPR>(a0 + a1);
+    if (l == 0) part[wave][sub] = s;
+    __syncthreads();
+    if (slice == 0) {
+      float t = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) t += part[wave + k][sub];
+      // finish_row's reduction of (t, 0) over the LPR lanes: lane 0 holds t
+      finish_row<LPR, W8, false>(a, row, live, l, l == 0 ? t : 0.0f, 0.0f, 0.f, 0.f, best);
+    }
+  }
+  if (a.epi == EPI_F32_ARGMAX) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) best = umax64(best, shfl_xor_u64(best, m));
+    if (lane == 0) wave_keys[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long k = wave_keys[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; ++i) k = umax64(k, wave_keys[i]);
+      a.keys[blockIdx.x] = k;
+    }
+  }
+}
+
 }  // namespace
 
 int cu_count() {
@@ -468,13 +615,13 @@ int blocks_for(int groups) {
 // bytes of LDS each (registers limit most forms to three: a grid of four per
 // CU would leave a quarter of the workgroups to start after the others and
 // run the tail alone).  Cached per form for the last LDS size asked.
-template <int LPR, int NJ, bool W8, bool PAIR>
+template <int LPR, int NJ, bool W8, bool PAIR, bool BUF>
 int resident_per_cu(size_t lds) {
   static size_t cached_lds = 0;
   static int cached = 0;
   if (cached == 0 || cached_lds != lds) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel<LPR, NJ, W8, PAIR>, kThreads, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel<LPR, NJ, W8, PAIR, BUF>, kThreads, lds) !=
             hipSuccess ||
         n <= 0)
       n = 1;
@@ -484,17 +631,17 @@ int resident_per_cu(size_t lds) {
   return cached;
 }
 
-template <int LPR, int NJ, bool W8, bool PAIR>
+template <int LPR, int NJ, bool W8, bool PAIR, bool BUF = !W8>
 int launch_cfg(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
   constexpr int RPW = 64 / LPR;
   // x as float32 and a reduction scratch; W8 also x as packed bf16 pairs
   const size_t lds = (size_t)(a.K + 8) * sizeof(float) + (size_t)a.K * 2;
   const int needed = ((a.M + RPW - 1) / RPW + kWaves - 1) / kWaves;
-  int cap = cu_count() * resident_per_cu<LPR, NJ, W8, PAIR>(lds);
+  int cap = cu_count() * resident_per_cu<LPR, NJ, W8, PAIR, BUF>(lds);
   if (cap > kMaxPartialKeys) cap = kMaxPartialKeys;
   const int blocks = needed < cap ? needed : cap;
   if (blocks_out) *blocks_out = blocks;
-  hipLaunchKernelGGL((gemv_kernel<LPR, NJ, W8, PAIR>), dim3(blocks), dim3(kThreads), lds, stream,
+  hipLaunchKernelGGL((gemv_kernel<LPR, NJ, W8, PAIR, BUF>), dim3(blocks), dim3(kThreads), lds, stream,
                      a);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "gemv launch");
@@ -521,6 +668,15 @@ int pick_lpr(int CH) {
 template <bool W8, bool PAIR>
 int launch_shape(const GemvArgs& a, hipStream_t stream, int* blocks_out) {
   const int CH = W8 ? a.K / 16 : a.K / 8;
+  // the int8 LM head (rows of up to 96 chunks) with branch-free loads
+  if (W8 && !PAIR && a.epi == EPI_F32_ARGMAX && pick_lpr(CH) == 8) {
+    const int nj = (CH + 7) / 8;
+    if (nj <= 6) return launch_cfg<8, 6, true, false, true>(a, stream, blocks_out);
+    if (nj <= 7) return launch_cfg<8, 7, true, false, true>(a, stream, blocks_out);
+    if (nj <= 8) return launch_cfg<8, 8, true, false, true>(a, stream, blocks_out);
+    if (nj <= 10) return launch_cfg<8, 10, true, false, true>(a, stream, blocks_out);
+    return launch_cfg<8, 12, true, false, true>(a, stream, blocks_out);
+  }
   switch (pick_lpr(CH)) {
     case 8: return launch_nj<8, W8, PAIR>((CH + 7) / 8, a, stream, blocks_out);
     case 16: return launch_nj<16, W8, PAIR>((CH + 15) / 16, a, stream, blocks_out);
@@ -605,6 +761,93 @@ int launch_xreg(const XregPlan& p, const GemvArgs& a, hipStream_t stream, int* b
   return launch_xreg_nj<64, PAIR>(p.nj, a, stream, blocks_out);
 }
 
+// The register-x split plan (gemv_rx_kernel): int8 rows (split four ways
+// past 2048 columns) or bf16 rows longer than 1024 columns (split four
+// ways), when a one-pass grid fits four workgroups per CU; false otherwise.
+// HK_GEMV_RX=0 turns it off.
+struct RxPlan {
+  int lpr = 0, nj = 0, ks = 0;
+};
+
+bool rx_plan(const GemvArgs& a, bool w8, RxPlan* plan) {
+  static const bool off = [] {
+    const char* e = getenv("HK_GEMV_RX");
+    return e && e[0] == '0';
+  }();
+  // HK_GEMV_RX_SHAPE=lpr,ks (lpr 32 or 64, ks 1, 2 or 4): one launch shape
+  // for every register-x launch, for tuning sweeps
+  static const RxPlan forced = [] {
+    RxPlan f;
+    const char* e = getenv("HK_GEMV_RX_SHAPE");
+    int lpr = 0, ks = 0;
+    if (e && sscanf(e, "%d,%d", &lpr, &ks) == 2 && (lpr == 32 || lpr == 64) && (ks == 1 || ks == 2 || ks == 4)) {
+      f.lpr = lpr;
+      f.ks = ks;
+    }
+    return f;
+  }();
+  if (off || a.epi == EPI_SWIGLU) return false;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.gamma) |
+                          reinterpret_cast<uintptr_t>(a.x_table);
+  if (align & 15) return false;
+  const int CH = a.K / (w8 ? 16 : 8);
+  RxPlan p;
+  if (w8) {
+    p.ks = CH > 128 ? 4 : 1;
+    p.lpr = CH <= 32 ? 32 : 64;
+  } else {
+    if (a.K <= 1024) return false;
+    p.ks = 4;
+    p.lpr = 64;
+  }
+  if (forced.lpr) {
+    p.lpr = forced.lpr;
+    p.ks = forced.ks;
+  }
+  const int chs = (CH + p.ks - 1) / p.ks;
+  p.nj = (chs + p.lpr - 1) / p.lpr;
+  if (p.nj > 6) return false;
+  const int groups = (a.M + 64 / p.lpr - 1) / (64 / p.lpr);
+  const int blocks = (groups + kWaves / p.ks - 1) / (kWaves / p.ks);
+  int cap = cu_count() * 4;
+  if (cap > kMaxPartialKeys) cap = kMaxPartialKeys;
+  if (blocks > cap) return false;
+  *plan = p;
+  return true;
+}
+
+template <int LPR, bool W8, int KS>
+int launch_rx_nj(int nj, const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  const int groups = (a.M + 64 / LPR - 1) / (64 / LPR);
+  const int blocks = (groups + kWaves / KS - 1) / (kWaves / KS);
+  if (blocks_out) *blocks_out = blocks;
+  switch (nj) {
+    case 1: hipLaunchKernelGGL((gemv_rx_kernel<LPR, 1, W8, KS>), dim3(blocks), dim3(kThreads), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((gemv_rx_kernel<LPR, 2, W8, KS>), dim3(blocks), dim3(kThreads), 0, stream, a); break;
+    case 3: hipLaunchKernelGGL((gemv_rx_kernel<LPR, 3, W8, KS>), dim3(blocks), dim3(kThreads), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((gemv_rx_kernel<LPR, 4, W8, KS>), dim3(blocks), dim3(kThreads), 0, stream, a); break;
+    default: hipLaunchKernelGGL((gemv_rx_kernel<LPR, 6, W8, KS>), dim3(blocks), dim3(kThreads), 0, stream, a); break;
+  }
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_fail(err, "gemv launch");
+}
+
+template <bool W8, int KS>
+int launch_rx_ks(const RxPlan& p, const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  if (p.lpr == 32) return launch_rx_nj<32, W8, KS>(p.nj, a, stream, blocks_out);
+  return launch_rx_nj<64, W8, KS>(p.nj, a, stream, blocks_out);
+}
+
+template <bool W8>
+int launch_rx_w(const RxPlan& p, const GemvArgs& a, hipStream_t stream, int* blocks_out) {
+  if (p.ks == 4) return launch_rx_ks<W8, 4>(p, a, stream, blocks_out);
+  if (p.ks == 2) return launch_rx_ks<W8, 2>(p, a, stream, blocks_out);
+  return launch_rx_ks<W8, 1>(p, a, stream, blocks_out);
+}
+
+int launch_rx(const RxPlan& p, const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out) {
+  return w8 ? launch_rx_w<true>(p, a, stream, blocks_out) : launch_rx_w<false>(p, a, stream, blocks_out);
+}
 }  // namespace
 
 int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out) {
@@ -625,6 +868,8 @@ int launch_gemv(const GemvArgs& a, bool w8, hipStream_t stream, int* blocks_out)
   if (a.epi == EPI_BIAS && a.bias == nullptr) return fail("gemv: bias missing");
   if (a.epi == EPI_RESID && a.resid == nullptr) return fail("gemv: residual missing");
   if (a.epi == EPI_F32_ARGMAX && a.keys == nullptr) return fail("gemv: argmax key buffer missing");
+  RxPlan rx;
+  if (rx_plan(a, w8, &rx)) return launch_rx(rx, a, w8, stream, blocks_out);
   XregPlan plan;
   if (xreg_plan(a, w8, &plan))
     return pair ? launch_xreg<true>(plan, a, stream, blocks_out)

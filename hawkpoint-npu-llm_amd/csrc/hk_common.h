@@ -99,6 +99,34 @@ __device__ __forceinline__ u32x4 load_stream_i8_bf16(const void* p) {
   return u32x4{i8pair_bf16(q.x, 0), i8pair_bf16(q.x, 2), i8pair_bf16(q.y, 0), i8pair_bf16(q.y, 2)};
 }
 
+// Sum over each group of W adjacent lanes (W = 8, 16, 32 or 64) with DPP row
+// moves, a few cycles each against an LDS round trip per ds_bpermute step
+// (what __shfl_xor compiles to): swap neighbours (quad_perm 1,0,3,2), swap
+// pairs (2,3,0,1), pair quads (row_half_mirror), pair half-rows (row_mirror),
+// each step adding lanes that hold equal partial sums, so every lane of a
+// group ends with its total.  W = 32 adds the other row with one shuffle;
+// W = 64 adds the rows with row_bcast15 / row_bcast31 and hands lane 63's
+// total to the whole wave.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float lane_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xf, false));
+}
+template <int W>
+__device__ __forceinline__ float lane_sum(float v) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "8, 16, 32 or 64 lanes");
+  v += lane_dpp<0xb1>(v);   // quad_perm 1,0,3,2
+  v += lane_dpp<0x4e>(v);   // quad_perm 2,3,0,1
+  v += lane_dpp<0x141>(v);  // row_half_mirror
+  if constexpr (W >= 16) v += lane_dpp<0x140>(v);  // row_mirror
+  if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (W == 64) {
+    v += lane_dpp<0x142, 0xa>(v);  // row_bcast15 into rows 1 and 3
+    v += lane_dpp<0x143, 0x8>(v);  // row_bcast31 into row 3
+    v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  }
+  return v;
+}
+
 // Butterfly sum over groups of `width` adjacent lanes (width a power of two).
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {

@@ -164,8 +164,9 @@ __device__ __forceinline__ unsigned long long pword(float v, unsigned t) {
   return ((unsigned long long)t << 32) | __float_as_uint(v);
 }
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <int POL = kSc1>
 __device__ __forceinline__ unsigned long long ld_p64(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kSc1));
+  return __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POL));
 }
 
 // ---- cross-lane sums with DPP ----
@@ -804,12 +805,60 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return (g / denom) * u;
 }
 
+// ---- split-KV merge ----
+// Fold `count` published chunks (chunk j's (P @ V, max, sum) words at
+// j * kPartStride of prs, tagged ptag) into the running (mx, lsum, r) of
+// output word `lane` (threads 0..63 of one wave), chunks in order.  Each
+// round trip loads a batch of MB chunks: lane k chunk j0 + k's (max, sum)
+// pair in one 16-byte load, every lane its own output word of each chunk;
+// readlane hands the pairs to the whole wave.  No completion wait or
+// ticket: each word carries the epoch.  Returns false if the wait gave up.
+template <int PPOL, int MB>
+__device__ bool fold_partials(const PersistentArgs& a, __amdgpu_buffer_rsrc_t prs, int count, unsigned ptag,
+                              int lane, float& mx, float& lsum, float& r) {
+  static_assert(MB <= 64, "one (max, sum) pair per lane");
+  auto fold = [&](float mj, float sj, float oj) {
+    const float nm = fmaxf(mx, mj);
+    const float keep = __builtin_amdgcn_exp2f(mx - nm), f = __builtin_amdgcn_exp2f(mj - nm);
+    lsum = fmaf(sj, f, lsum * keep);
+    r = fmaf(oj, f, r * keep);
+    mx = nm;
+  };
+  for (int j0 = 0; j0 < count; j0 += MB) {
+    unsigned long long ow[MB];
+    u32x4 ms;
+    for (unsigned spins = 1;; ++spins) {
+      const int jm = j0 + lane;
+      ms = __builtin_amdgcn_raw_buffer_load_b128(
+          prs, lane < MB && jm < count ? (unsigned)(jm * kPartStride + kHeadDim) * 8u : kOutside, 0, PPOL);
+      bool have = lane >= MB || jm >= count || (ms.y == ptag && ms.w == ptag);
+#pragma unroll
+      for (int k = 0; k < MB; ++k) {
+        const int j = j0 + k;
+        ow[k] = ld_p64<PPOL>(prs, j < count ? (unsigned)(j * kPartStride + lane) * 8u : kOutside);
+        have = have && (j >= count || (unsigned)(ow[k] >> 32) == ptag);
+      }
+      if (__all(have)) break;
+      if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) return give_up(a);
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int k = 0; k < MB; ++k)
+      if (j0 + k < count)
+        fold(__uint_as_float((unsigned)__builtin_amdgcn_readlane((int)ms.x, k)),
+             __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)ms.z, k)), __uint_as_float((unsigned)ow[k]));
+  }
+  return true;
+}
+
 // ---- attention task: query head h, slots [s * kChunk, ...] of layer l ----
 // POL: cache policy of the q/k/v polls and the output store (kSc1 across
 // the device, kLocal when producers and consumers share an XCD).
 // ptag tags the split-KV partial words (ptag_of of the attention epoch); the
 // merging task loads MB chunks' words per round trip (a register budget).
-template <class S, int POL = kSc1, int MB = 8>
+// PPOL: cache policy of those partial words, kLocal when every chunk of the
+// head runs on the merging task's XCD.
+template <class S, int POL = kSc1, int MB = 8, int PPOL = POL>
 __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_q,
                                unsigned tag_a, unsigned ptag) {
   const PersistentArgs& a = *c.a;
@@ -1020,8 +1069,7 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
   // split-KV: every chunk but the last publishes its (P @ V, max, sum) as
   // tagged 64-bit words and is done; the task of the last chunk (which holds
   // slot p and has the fewest live slots) polls them and merges by
-  // log-sum-exp, chunks in order.  No completion wait or ticket: each word
-  // carries the epoch.
+  // log-sum-exp, chunks in order.
   const __amdgpu_buffer_rsrc_t prs =
       rsrc(a.partial + (size_t)h * a.max_splits * kPartStride, a.max_splits * kPartStride * 8);
   HK_STAMP_ATTN(l, 7);
@@ -1029,59 +1077,20 @@ __device__ bool attention_task(Ctx& c, int l, int h, int s, int p, unsigned tag_
     if (tid < kPartStride) {
       const float v = tid < kHeadDim ? o : tid == kHeadDim ? m : sum;
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, pword(v, ptag)), prs,
-                                            (s * kPartStride + tid) * 8, 0, kSc1);
+                                            (s * kPartStride + tid) * 8, 0, PPOL == kSc1 ? kSc1 : 0);
     }
     return true;
   }
   // (ok is true here: the q/k/v polls succeeded)
   if (tid < kHeadDim) {
-    constexpr int kMergeBatch = MB;
-    const int others = nsplit - 1;
     // one pass over the chunks in order with a running maximum (each chunk
-    // has live slots, so its maximum is finite): a batch of chunks per round
-    // trip, no separate pass for the maxima
+    // has live slots, so its maximum is finite), this task's own chunk last
     float mx = -INFINITY, lsum = 0.0f, r = 0.0f;
-    auto fold = [&](float mj, float sj, float oj) {
-      const float nm = fmaxf(mx, mj);
-      const float keep = __builtin_amdgcn_exp2f(mx - nm), f = __builtin_amdgcn_exp2f(mj - nm);
-      lsum = fmaf(sj, f, lsum * keep);
-      r = fmaf(oj, f, r * keep);
-      mx = nm;
-    };
-    // a batch of kMergeBatch chunks per round trip: lane k loads chunk
-    // j0 + k's (max, sum) pair (one 16-byte load), every lane its own output
-    // word of each chunk; readlane hands the pairs to the whole wave
-    static_assert(kMergeBatch <= 64, "one (max, sum) pair per lane");
-    for (int j0 = 0; ok && j0 < others; j0 += kMergeBatch) {
-      unsigned long long ow[kMergeBatch];
-      u32x4 ms;
-      for (unsigned spins = 1;; ++spins) {
-        const int jm = j0 + (int)tid;
-        ms = __builtin_amdgcn_raw_buffer_load_b128(
-            prs, (int)tid < kMergeBatch && jm < others ? (unsigned)(jm * kPartStride + kHeadDim) * 8u : kOutside, 0,
-            kSc1);
-        bool have = (int)tid >= kMergeBatch || jm >= others || (ms.y == ptag && ms.w == ptag);
-#pragma unroll
-        for (int k = 0; k < kMergeBatch; ++k) {
-          const int j = j0 + k;
-          ow[k] = ld_p64(prs, j < others ? (unsigned)(j * kPartStride + tid) * 8u : kOutside);
-          have = have && (j >= others || (unsigned)(ow[k] >> 32) == ptag);
-        }
-        if (__all(have)) break;
-        if (spins > a.spin_limit || ((spins & 63u) == 0u && ld_c32(a.error) != 0u)) {
-          ok = give_up(a);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k)
-        if (j0 + k < others)
-          fold(__uint_as_float((unsigned)__builtin_amdgcn_readlane((int)ms.x, k)),
-               __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)ms.z, k)),
-               __uint_as_float((unsigned)ow[k]));
-    }
-    fold(m, sum, o);  // this task's own chunk, the last
+    ok = fold_partials<PPOL, MB>(a, prs, nsplit - 1, ptag, tid, mx, lsum, r);
+    const float nm = fmaxf(mx, m);
+    const float keep = __builtin_amdgcn_exp2f(mx - nm), f = __builtin_amdgcn_exp2f(m - nm);
+    lsum = fmaf(sum, f, lsum * keep);
+    r = fmaf(o, f, r * keep);
     if (ok) store_out(tagged(f32_to_bf16(r / lsum), tag_a));
     HK_STAMP_ATTN(l, 6);
   }

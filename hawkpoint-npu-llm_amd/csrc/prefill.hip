@@ -925,10 +925,10 @@ int split_parts(int M, int N, int K) {
 // of 128 slots (slots 0..p of each token; cpu_backend.py:110-129):
 //   S^T = K Q^T        v_mfma_f32_16x16x32_bf16: bf16 products are exact, f32 sums
 //   online softmax     per token: running max m and sum l, P = exp(S / 8 - m)
-//   O^T += V^T P^T     v_mfma_f32_16x16x32_bf16 twice, on P's top 16 bits
-//                      and on the remainder: about 16 significant bits of the
-//                      float32 P (the reference's NumPy softmax), at an
-//                      eighth of the cost of float32 MFMAs
+//   O^T += V^T P^T     v_mfma_f32_16x16x32_bf16 three times, on P split
+//                      into three bf16 terms that together are the float32
+//                      P exactly (the reference's NumPy softmax), far below
+//                      the cost of float32 MFMAs
 // and out = bf16(O / l).  Computing S^T rather than S leaves lane L holding
 // P[token L % 16][slots 16 sb + 4 (L / 16) + r], which serves directly as the
 // B operand of P @ V once the MFMA's k index is read as the matching slot;

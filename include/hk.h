@@ -162,7 +162,10 @@ int hk_engine_launch_part_repeat(hk_engine* engine, int32_t part, int32_t count)
 /* Enqueue `count` GEMVs y = W_i @ x, W_i = weights[i % n_weights] (bf16, or
  * int8 with scales[i % n_weights] when `scales` is non-NULL), float32 output,
  * on `stream` -- a microbenchmark that rotates through distinct weight copies
- * so a cache cannot serve them. */
+ * so a cache cannot serve them.  The launches go out as one hipGraph,
+ * captured on the first call per argument set (the 32 most recent sets are
+ * kept), so host launch cost does not pace the GPU; HK_GEMV_REPEAT_GRAPH=0
+ * launches them directly.  No counterpart in the reference. */
 int hk_gemv_repeat(const void* const* weights, const float* const* scales, int32_t n_weights,
                    const uint16_t* x, float* y_f32, int32_t M, int32_t K, int32_t count,
                    void* stream);

@@ -39,11 +39,12 @@ The bars:
   path's;
 - the reference's top-1 count bar (within 6 of the chunked path), on every
   configuration but SmolLM2-135M bf16.  There the count moves with flips at
-  gaps below 0.07 that only the float32 summation order decides (measured:
-  engine 369/378 and per-kernel 376/378, all misses at gaps of 0.003-0.067,
-  i.e. below 0.0041 of |top1|, while the engine's logits were the closer of
-  the two, mean rel-L2 1.260e-2 against 1.271e-2), so for that one the count
-  is reported and the bar above holds its misses instead.
+  gaps below 0.07 that only the float32 summation order decides (measured on
+  one build: engine 369/378 and per-kernel 376/378, all misses at gaps of
+  0.003-0.067, i.e. below 0.0041 of |top1|, while the engine's logits were
+  the closer of the two, mean rel-L2 1.260e-2 against 1.271e-2; on a later
+  one 374 and 371), so for that one the count is reported and the bar above
+  holds its misses instead.
 """
 
 import json

@@ -123,6 +123,43 @@ def test_gemv_w8_matches_oracle(hk_lib, m, k, bias):
     _check_bf16(_read(Y, np.uint16, m), bf16.to_bits(ref), bound)
 
 
+@pytest.mark.parametrize("w8", [False, True], ids=["bf16", "w8"])
+def test_gemv_repeat_graph_replays_match_direct_launches(hk_lib, w8):
+    """hk_gemv_repeat (the GEMV microbenchmark): its captured graph, replayed
+    twice, leaves the output of the last launch's weight copy, the same
+    float32 bits as a direct GEMV of that copy."""
+    import ctypes
+
+    from runtime import hip
+
+    announce(f"gemv repeat graph w8={w8}")
+    m, k, copies, count = 896, 896, 3, 5
+    rng = np.random.default_rng(21)
+    x = _dev(bf16.to_bits(rng.normal(0, 1, k).astype(np.float32)))
+    ws, ss = [], []
+    for _ in range(copies):
+        w = bf16.round_f32(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+        if w8:
+            q, sc = quantize_per_output_channel(w)
+            ws.append(_dev(q))
+            ss.append(_dev(sc))
+        else:
+            ws.append(_dev(bf16.to_bits(w)))
+    ptrs = (ctypes.c_void_p * copies)(*[b.ptr for b in ws])
+    sptrs = (ctypes.c_void_p * copies)(*[b.ptr for b in ss]) if w8 else None
+    y, want = hip.DeviceBuffer(4 * m), hip.DeviceBuffer(4 * m)
+    last = (count - 1) % copies
+    if w8:
+        hip.check(hk_lib.hk_gemv_w8(ws[last].ptr, ss[last].ptr, x.ptr, None, None, None, want.ptr, m, k, None), "w8")
+    else:
+        hip.check(hk_lib.hk_gemv_bf16(ws[last].ptr, x.ptr, None, None, None, want.ptr, m, k, None), "bf16")
+    for _ in range(2):  # the capture, then a replay
+        y.zero()
+        hip.check(hk_lib.hk_gemv_repeat(ptrs, sptrs, copies, x.ptr, y.ptr, m, k, count, None), "repeat")
+        hip.check(hk_lib.hk_stream_sync(None), "sync")
+        np.testing.assert_array_equal(_read(y, np.uint32, m), _read(want, np.uint32, m))
+
+
 def test_gemv_residual_epilogue(hk_lib):
     from runtime import hip
 
