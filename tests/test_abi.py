@@ -82,3 +82,18 @@ def test_expert_shim_validation_without_gpu_work():
     # Colibri: nothing is up before coli_cuda_init, and a bad device list is refused
     assert lib.coli_cuda_device_count() == 0 and lib.coli_cuda_device_at(0) == -1
     assert lib.coli_cuda_init(None, 1) == 0
+
+
+def test_phase_stamp_library_exports_its_entry_point():
+    """lib/libhk_phases.so (libhk.so with the decode step's clock stamps)
+    exports what include/hk_phases.h declares; libhk.so does not."""
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "hk_phases.h").read_text(), flags=re.S)
+    names = set(re.findall(r"\b(hk_[a-z0-9_]+)\s*\(", text))
+    assert names == {"hk_phase_stamps"}
+    from runtime import hip
+
+    path = hip.LIB_PATH.parent / "libhk_phases.so"
+    assert path.is_file(), "build it first (python hawkpoint-npu-llm_amd/csrc/build.py)"
+    phases = ctypes.CDLL(str(path))
+    assert all(hasattr(phases, n) for n in names)
+    assert not any(hasattr(ctypes.CDLL(str(hip.LIB_PATH)), n) for n in names)
