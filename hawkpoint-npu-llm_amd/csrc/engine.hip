@@ -165,7 +165,7 @@ struct hk_engine {
   unsigned long long* keys = nullptr;  // [kMaxPartialKeys] LM-head argmax partials
   StepCtrl* ctrl = nullptr;
   int32_t* out_tokens = nullptr;  // [max_ctx]
-  int32_t* result = nullptr;      // [2]: last argmax token, persistent-step error word
+  int32_t* result = nullptr;      // [3]: last argmax token, persistent-step error word, prefill split error word
   // whole step in one persistent launch (persistent.hip); -1: per-kernel graph
   int pshape = -1;
   // the step may also run split by XCD (attention block on XCD 0); it does so
@@ -203,6 +203,12 @@ struct hk_engine {
   // per layer, MFMA-native copies of qkv (RoPE order), o, gate_up and down
   // for the slab GEMMs of chunks up to 64 tokens (empty: row-major weights)
   std::vector<std::array<void*, 4>> pf_native;
+  // the down slab GEMM of short prompts with K split inside an XCD
+  // (PrefillGemmArgs::slab_ws): on where the XCD split's placement check
+  // passed, unless HK_SLAB_SPLIT=0; off for good after a wait gave up
+  bool slab_split = false;
+  unsigned long long* slab_ws = nullptr;
+  unsigned slab_tag = 0;
 };
 
 namespace {
@@ -401,7 +407,7 @@ int check_persistent(hk_engine* e, const int32_t* result_host) {
   if (e->xpart) HK_CHECK(hipMemset(e->xpart, 0, (size_t)8 * e->d.hidden * 8));
   HK_CHECK(hipMemset(e->partial, 0, partial_floats(e) * sizeof(float)));
   HK_CHECK(hipMemset(e->counters, 0, e->d.q_heads * sizeof(unsigned int)));
-  HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
+  HK_CHECK(hipMemset(e->result, 0, 3 * sizeof(int32_t)));
   HK_CHECK(hipDeviceSynchronize());
   set_error("decode step abandoned: a workgroup of the persistent step waited too long for "
             "another (is another kernel occupying the GPU?); its outputs and KV slot are invalid");
@@ -499,7 +505,7 @@ void free_prefill_buffers(hk_engine* e) {
     p = nullptr;
   };
   drop(e->pf_x), drop(e->pf_h1), drop(e->pf_xn), drop(e->pf_qkv), drop(e->pf_q);
-  drop(e->pf_att), drop(e->pf_act), drop(e->pf_tokens), drop(e->pf_split);
+  drop(e->pf_att), drop(e->pf_act), drop(e->pf_tokens), drop(e->pf_split), drop(e->slab_ws);
   e->pf_rows = 0;
 }
 
@@ -523,6 +529,11 @@ int alloc_prefill_buffers(hk_engine* e, int rows) {
                                    split_ws_need(m, d.intermediate, d.hidden, true),
                                    split_ws_need(m, d.hidden, d.intermediate, false)});
   HK_TRY(dalloc(&e->pf_split, e->pf_split_floats));
+  // tagged partial sums of the K-split down slabs (N = hidden); tag 0 never
+  // matches a launch's
+  const size_t slab_words = (size_t)((d.hidden + 15) / 16) * kSlabParts * kSlabMaxTokens * 16;
+  HK_TRY(dalloc(&e->slab_ws, slab_words));
+  HK_CHECK(hipMemset(e->slab_ws, 0, slab_words * sizeof(unsigned long long)));
   return 0;
 }
 
@@ -699,6 +710,13 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     dn.kblock = kb;
     dn.split_ws = e->pf_split;
     dn.split_ws_floats = e->pf_split_floats;
+    if (slab && e->slab_split && e->slab_ws) {  // K split inside an XCD, a new tag per launch
+      if (++e->slab_tag == 0) e->slab_tag = 1;
+      dn.slab_ws = e->slab_ws;
+      dn.slab_tag = e->slab_tag;
+      dn.slab_spin = e->spin_limit;
+      dn.slab_error = reinterpret_cast<unsigned*>(e->result + 2);
+    }
     HK_TRY(launch_prefill_gemm(dn, s));
   }
   return 0;
@@ -855,13 +873,13 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
     HK_TRY(dalloc(&e->keys, kMaxPartialKeys));
     HK_TRY(dalloc(&e->ctrl, 1));
     HK_TRY(dalloc(&e->out_tokens, d.max_context));
-    HK_TRY(dalloc(&e->result, 2));
+    HK_TRY(dalloc(&e->result, 3));
     HK_CHECK(hipMemset(e->kcache, 0, kv * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->vcache, 0, kv * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->h, 0, d.hidden * sizeof(uint16_t)));
     HK_CHECK(hipMemset(e->counters, 0, d.q_heads * sizeof(unsigned int)));
     HK_CHECK(hipMemset(e->ctrl, 0, sizeof(StepCtrl)));
-    HK_CHECK(hipMemset(e->result, 0, 2 * sizeof(int32_t)));
+    HK_CHECK(hipMemset(e->result, 0, 3 * sizeof(int32_t)));
     const char* pers = getenv("HK_PERSISTENT");
     if (!(pers && pers[0] == '0') && d.layers <= kPersistentMaxLayers)
       e->pshape = persistent_shape(d.hidden, d.intermediate, d.q_heads, d.kv_heads, w8);
@@ -876,6 +894,10 @@ int hk_engine_create(const hk_model_desc* desc, const hk_model_weights* weights,
       e->xcd_split = persistent_xcd_split(e->pshape, e->stream) == 1;
       if (!e->xcd_split && split && split[0] == '1') return HK_ERR_INVALID;
     }
+    // HK_SLAB_SPLIT=0: the down slabs of short prompts unsplit; they rely on
+    // the workgroup placement the XCD split checked
+    const char* slab_split = getenv("HK_SLAB_SPLIT");
+    e->slab_split = e->xcd_split && !(slab_split && slab_split[0] == '0');
     if (e->pshape >= 0) {
       std::vector<PersistentLayer> pl(d.layers);
       for (int l = 0; l < d.layers; ++l) {
@@ -1033,10 +1055,21 @@ int hk_engine_prefill(hk_engine* e, const int32_t* tokens_host, int32_t n, int32
   if (logits_host)
     HK_CHECK(hipMemcpyAsync(logits_host, e->logits, (size_t)e->d.vocab * sizeof(float),
                             hipMemcpyDeviceToHost, e->stream));
-  if (next_token_host)
-    HK_CHECK(hipMemcpyAsync(next_token_host, e->result, sizeof(int32_t), hipMemcpyDeviceToHost,
-                            e->stream));
+  int32_t result[3] = {0, 0, 0};  // token, (step error), split-slab error
+  HK_CHECK(hipMemcpyAsync(result, e->result, sizeof(result), hipMemcpyDeviceToHost, e->stream));
   HK_CHECK(hipStreamSynchronize(e->stream));
+  if (result[2] != 0) {
+    // a K-split slab waited too long for one of its parts, or found a part
+    // on another XCD: this prefill's KV slots and logits are invalid; later
+    // prefills run the slabs unsplit
+    e->slab_split = false;
+    HK_CHECK(hipMemset(e->result + 2, 0, sizeof(int32_t)));
+    HK_CHECK(hipDeviceSynchronize());
+    set_error("prefill abandoned: a K-split GEMM waited too long for one of its parts (is another kernel "
+              "occupying the GPU?); its KV slots and logits are invalid");
+    return HK_ERR_HIP;
+  }
+  if (next_token_host) *next_token_host = result[0];
   return 0;
 }
 

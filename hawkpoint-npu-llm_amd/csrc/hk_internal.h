@@ -245,6 +245,18 @@ struct PrefillGemmArgs {
   // together (rope_row).  N = (q_heads + 2 kv_heads) * 64.
   // Slab GEMM only: the MFMA-native copy of W (launch_repack_mfma), or null
   const void* Wn;
+  // Long-K slab GEMM without RoPE, norm or SwiGLU only (the down
+  // projection): with slab_ws, K is split kSlabParts ways over workgroups of
+  // one XCD (workgroup i runs on XCD i % 8).  Parts 1.. publish their float32
+  // partial sums as tagged words (slab_tag << 32 | bits) into slab_ws, which
+  // holds ceil(N / 16) * kSlabParts * kSlabMaxTokens * 16 of them; part 0
+  // polls them from the XCD's L2, adds the parts in order and applies the
+  // epilogue.  slab_tag is nonzero and new for every launch; a wait that
+  // gives up after slab_spin polls, or a workgroup found on another XCD,
+  // sets *slab_error.
+  unsigned long long* slab_ws;
+  unsigned slab_tag, slab_spin;
+  unsigned* slab_error;
   struct {
     const float* cos_tab;  // [max_ctx, 32]
     const float* sin_tab;
@@ -256,6 +268,7 @@ struct PrefillGemmArgs {
 };
 
 constexpr int kSlabMaxTokens = 64;
+constexpr int kSlabParts = 4;  // K split of the slab GEMM with slab_ws
 constexpr int kSlabNormMaxK = 1024;
 // compute units of the current device
 int cu_count();

@@ -517,6 +517,97 @@ __device__ __forceinline__ int rope_row(int s, int r) {
   return (s >> 2) * kHeadDim + 8 * (s & 3) + (r & 7) + (r >= 8 ? kHeadDim / 2 : 0);
 }
 
+// The plain epilogues of a slab GEMM output (m, n): bf16, bias or residual
+// (k-blocked outputs and residuals: element (m, n) at ((n / 8) M + m) 8 + n % 8).
+__device__ __forceinline__ void slab_store(const PrefillGemmArgs& a, int m, int n, float x) {
+  const size_t yo = a.kblock == 2 ? ((size_t)(n >> 3) * a.M + m) * 8 + (n & 7) : (size_t)m * a.ldy + n;
+  const size_t ro = a.kblock == 2 ? yo : (size_t)m * a.ldr + n;
+  uint16_t* y = a.Y + yo;
+  switch (a.epi) {
+    case EPI_BF16:
+      *y = (uint16_t)f32_to_bf16(x);
+      break;
+    case EPI_BIAS:
+      *y = (uint16_t)f32_to_bf16(round_bf16(x) + a.bias[n]);
+      break;
+    case EPI_RESID:
+      *y = (uint16_t)f32_to_bf16(round_bf16(x) + bf16_to_f32(a.resid[ro]));
+      break;
+    default:
+      break;
+  }
+}
+
+// The K-split slab's end: each thread sums its outputs over the waves (wave
+// order); parts 1.. store them as tagged words in the XCD's L2 and are done;
+// part 0 polls those words (loads that miss the CU's L1 and read the L2),
+// adds the parts in order, scales (W8) and stores.  A tagged 64-bit word is
+// seen whole or not at all, so no flag or fence is needed; a wait gives up
+// after slab_spin polls and reports it.
+template <bool W8, int KS, int WAVES, int NB>
+__device__ void split_epilogue(const PrefillGemmArgs& a, const f32x4 (&red)[WAVES][NB][64], int slab, int part,
+                               int mb) {
+  constexpr int kLocalPol = 3;  // sc0 | nt: miss L1, read the XCD's L2
+  constexpr int E = (NB * 256 + WAVES * 64 - 1) / (WAVES * 64);  // outputs per thread
+  const int tid = threadIdx.x;
+  const int M = a.M, N = a.N, ns = 16 * slab;
+  const __amdgpu_buffer_rsrc_t ws = rsrc(a.slab_ws, ((N + 15) / 16) * KS * kSlabMaxTokens * 16 * 8);
+  const unsigned base = (unsigned)slab * KS * kSlabMaxTokens * 16;
+  float xv[E];
+  int mv[E], nv[E];
+  bool ok[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const int f = tid + i * WAVES * 64;
+    const int b = f >> 8, l = (f >> 2) & 63, r = f & 3;
+    mv[i] = 16 * b + 4 * (l >> 4) + r;
+    nv[i] = ns + (l & 15);
+    ok[i] = f < mb * 256 && mv[i] < M && nv[i] < N;
+    float x = 0.0f;
+    if (ok[i]) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) x += red[w][b][l][r];
+    }
+    xv[i] = x;
+  }
+  auto word = [&](int q, int i) { return (base + (unsigned)(q * kSlabMaxTokens + mv[i]) * 16u + (nv[i] & 15)) * 8u; };
+  if (part != 0) {
+#pragma unroll
+    for (int i = 0; i < E; ++i)
+      if (ok[i])
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{__float_as_uint(xv[i]), a.slab_tag}, ws, word(part, i), 0, 0);
+    return;
+  }
+  float pv[E][KS - 1];
+  for (unsigned spins = 1;; ++spins) {
+    bool have = true;
+#pragma unroll
+    for (int i = 0; i < E; ++i)
+#pragma unroll
+      for (int q = 1; q < KS; ++q) {
+        const u32x2_t v = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ws, ok[i] ? word(q, i) : kSlabOutside, 0, kLocalPol));
+        pv[i][q - 1] = __uint_as_float(v.x);
+        have = have && (!ok[i] || v.y == a.slab_tag);
+      }
+    if (have) break;
+    if (spins > a.slab_spin) {
+      __hip_atomic_store(a.slab_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    if (!ok[i]) continue;
+    float x = xv[i];
+#pragma unroll
+    for (int q = 0; q < KS - 1; ++q) x += pv[i][q];
+    if constexpr (W8) x *= a.scale[nv[i]];
+    slab_store(a, mv[i], nv[i], x);
+  }
+}
+
 // One batch of a wave's K steps: weight fragments (raw int8 for W8, widened
 // just before the product) and the token fragments of every block.
 template <bool PAIR, bool W8, int B, int NB>
@@ -533,9 +624,12 @@ struct SlabBatch {
 // prompt's 16-token blocks (a 40-token prompt takes three: a quarter fewer
 // token loads, products and LDS sums than the four a 64-token prompt needs).
 // TWO (gate/up with more slabs than CUs): a workgroup may take a second slab.
-template <bool PAIR, bool NORM, bool W8, int WAVES, int NB = kSlabBlocks, bool TWO = false>
+// KS > 1 (slab_ws): K split KS ways over workgroups of one XCD, the parts'
+// partial sums added by part 0 in part order (PrefillGemmArgs::slab_ws).
+template <bool PAIR, bool NORM, bool W8, int WAVES, int NB = kSlabBlocks, bool TWO = false, int KS = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a) {
   static_assert(!TWO || (PAIR && NORM), "second slabs for gate/up with the norm");
+  static_assert(KS == 1 || (!PAIR && !NORM && !TWO), "the K split is for plain slabs");
   constexpr int kSlabWaves = WAVES;
   constexpr int P = PAIR ? 2 : 1;
   constexpr int EB = W8 ? 1 : 2;  // bytes per weight
@@ -547,15 +641,32 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   __shared__ float ssq[NORM ? kSlabWaves : 1][kSlabMaxTokens];
   __shared__ float inv_s[kSlabMaxTokens];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n0 = blockIdx.x * 16;
+  // this workgroup's slab and K part: the KS parts of slab s are workgroups
+  // s % 8 + 8 (KS (s / 8) + q), q = 0..KS-1, all on XCD s % 8
+  int slab = blockIdx.x, part = 0;
+  if constexpr (KS > 1) {
+    const int xcd = blockIdx.x % 8, r = blockIdx.x / 8;
+    part = r % KS;
+    slab = xcd + 8 * (r / KS);
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if ((xcc & 15u) != (unsigned)xcd) {  // the parts would not share an L2: report, leave
+      if (tid == 0) __hip_atomic_store(a.slab_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (slab * 16 >= a.N) return;
+  }
+  const int n0 = slab * 16;
   const int M = a.M, N = a.N, K = a.K;
   const int mb = (M + 15) / 16;
   const int fr = lane & 15, fk = (lane >> 4) * 8;
-  const int steps = K / 32;
+  // this part's K steps (of 32 columns): [st0, st0 + steps)
+  const int sp = (K / 32 + KS - 1) / KS, st0 = part * sp;
+  const int steps = KS > 1 ? max(0, min(K / 32, st0 + sp) - st0) : K / 32;
   const int mine = steps > wave ? (steps - wave + kSlabWaves - 1) / kSlabWaves : 0;  // this wave's steps
   // byte offsets of this lane's weight row (and up row) and token rows at k
   // = fk; kSlabOutside for a row past the end
-  const int wrow = a.rope.on ? rope_row(blockIdx.x, fr) : n0 + fr;
+  const int wrow = a.rope.on ? rope_row(slab, fr) : n0 + fr;
   // weight piece (8 weights) of row n at k group g: row-major, or in the
   // MFMA-native copy Wn ([N/16][K/8][16] pieces: a fragment's 16 rows are one
   // run); wkm: bytes from column k to column k + 1 along a row
@@ -587,7 +698,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const int j = j0 + i;
-      const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
+      const unsigned k0 = (unsigned)(32 * (st0 + wave + kSlabWaves * j));
       const bool live = j < mine;
       const unsigned wo = live ? wofs + k0 * wkm : kSlabOutside;
       const unsigned uo = live ? uofs + k0 * wkm : kSlabOutside;
@@ -649,7 +760,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
       const unsigned uofs2 = two ? wpiece(s2 * 16 + fr + N) : kSlabOutside;
 #pragma unroll
       for (int i = 0; i < B; ++i) {
-        const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * i));
+        const unsigned k0 = (unsigned)(32 * (st0 + wave + kSlabWaves * i));
         const bool live = two && i < mine;
         const unsigned wo = live ? wofs2 + k0 * wkm : kSlabOutside, uo = live ? uofs2 + k0 * wkm : kSlabOutside;
         if constexpr (W8) {
@@ -666,7 +777,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
 #pragma unroll
     for (int i = 0; i < B; ++i)
       g[i] = __builtin_amdgcn_raw_buffer_load_b128(
-          gr, i < mine ? (unsigned)(32 * (wave + kSlabWaves * i) + fk) * 2u : kSlabOutside, 0, 0);
+          gr, i < mine ? (unsigned)(32 * (st0 + wave + kSlabWaves * i) + fk) * 2u : kSlabOutside, 0, 0);
     // squares of this lane's fragments, per token row; the four lanes of a
     // row hold its four 8-wide k groups
 #pragma unroll
@@ -730,7 +841,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
 #pragma unroll
       for (int i = 0; i < kSlabWPre; ++i) {
         const int j = g0 + i;
-        const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
+        const unsigned k0 = (unsigned)(32 * (st0 + wave + kSlabWaves * j));
         const unsigned wo = j < mine ? wofs + k0 * wkm : kSlabOutside;
         if constexpr (W8)
           wv[i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
@@ -742,7 +853,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int j = j0 + i;
-          const unsigned k0 = (unsigned)(32 * (wave + kSlabWaves * j));
+          const unsigned k0 = (unsigned)(32 * (st0 + wave + kSlabWaves * j));
 #pragma unroll
           for (int b = 0; b < NB; ++b)
             x[i][b] = __builtin_amdgcn_raw_buffer_load_b128(ar, j < mine ? aofs[b] + akm * k0 : kSlabOutside, 0, 0);
@@ -758,8 +869,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
         }
       };
       load_x(x0, g0);
+      // (the rounds stop at the wave's last step: a round past it would
+      // still wait for its loads, which read zero)
 #pragma unroll
       for (int i = 0; i < kSlabWPre; i += 4) {
+        if (g0 + i >= mine) break;
         load_x(x1, g0 + i + 2);
         __builtin_amdgcn_sched_barrier(0);
         mul_x(x0, i);
@@ -771,7 +885,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
   }
 
   for (int pass = 0; pass < 2; ++pass) {
-    const int s = pass ? s2 : (int)blockIdx.x, ns = 16 * s;
+    const int s = pass ? s2 : slab, ns = 16 * s;
     if (pass) {
       if (!two) break;
       __syncthreads();  // the first slab's sums have been read
@@ -803,6 +917,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_slab_kernel(PrefillGemmArgs a
     // values f = t, t + 64 WAVES, ... of [mb][64 lanes][4 rows] on thread t,
     // each summed over the waves in wave order, then the epilogue (the
     // rounding points of the other GEMM kernels)
+    if constexpr (KS > 1) {
+      split_epilogue<W8, KS, WAVES, NB>(a, red, slab, part, mb);
+      return;
+    }
     for (int f = tid; f < mb * 256; f += kSlabWaves * 64) {
       const int b = f >> 8, l = (f >> 2) & 63, r = f & 3;
       const int m = 16 * b + 4 * (l >> 4) + r, n = a.rope.on ? rope_row(s, l & 15) : ns + (l & 15);
@@ -1136,7 +1254,13 @@ void launch_slab_nb(const PrefillGemmArgs& a, hipStream_t stream) {
     else
       hipLaunchKernelGGL((gemm_slab_kernel<PAIR, true, W8, 16, NB>), grid, dim3(16 * 64), 0, stream, a);
   } else if constexpr (!PAIR) {
-    if (long_k)
+    // long K split kSlabParts ways inside an XCD, on 16 waves per part, when
+    // every part can be resident at once (part 0 waits for the others)
+    const int split_grid = kSlabParts * 8 * ((slabs + 7) / 8);
+    if (long_k && a.slab_ws && !a.rope.on && split_grid <= cu_count())
+      hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, 16, NB, false, kSlabParts>), dim3(split_grid),
+                         dim3(16 * 64), 0, stream, a);
+    else if (long_k)
       hipLaunchKernelGGL((gemm_slab_kernel<false, false, W8, kSlabLongWaves, NB>), grid, dim3(kSlabLongWaves * 64),
                          0, stream, a);
     else
@@ -1174,6 +1298,9 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     return fail("prefill gemm: k-blocked operands and RoPE need the slab path (M <= 64)");
   if (a.rope.on && (a.N != (a.rope.q_heads + 2 * a.rope.kv_heads) * kHeadDim || a.epi == EPI_SWIGLU))
     return fail("prefill gemm: RoPE needs the QKV projection");
+  if (a.slab_ws && (a.gamma || a.rope.on || pair || a.grp_count != nullptr || a.M > kSlabMaxTokens ||
+                    a.slab_error == nullptr || a.slab_tag == 0))
+    return fail("slab gemm: the K split is for plain slabs, with an error word and a nonzero tag");
   if (a.grp_count == nullptr && a.M <= kSlabMaxTokens) {
     if (a.gamma && a.K > kSlabNormMaxK) return fail("slab gemm: a normalised A operand needs K <= 1024");
     if (a.Wn && a.N % 16) return fail("slab gemm: the MFMA-native copy needs whole 16-row slabs");

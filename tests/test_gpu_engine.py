@@ -114,6 +114,27 @@ def test_smollm_135m_shape_decode(smol_model):
     _check_decode(smol_model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m", tol=SMOL_TOL)
 
 
+@pytest.mark.parametrize("w8", [False, True], ids=["bf16", "w8"])
+def test_hidden_1152_decode_on_the_per_kernel_path(w8):
+    """A shape the persistent step is not built for (hidden 1152, 18 query /
+    3 KV heads, intermediate 3072) decodes on the per-kernel path: its bf16
+    QKV GEMV splits K = 1152 four ways inside the workgroup with the RMSNorm
+    prologue (the sum of squares met across the slices in LDS), the W8 down
+    projection K = 3072.  Teacher-forced logits and KV slots against the
+    oracle."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    shape = dict(QWEN25_05B, hidden_size=1152, intermediate_size=3072, attention_heads=18, kv_heads=3,
+                 layers=2, vocab_size=4096)
+    model = SyntheticModel(shape, seed=9)
+    engine = QwenDecoderEngine(model, context_length=64, w8=w8)
+    try:
+        assert engine.step_kind(20) == "kernels"
+    finally:
+        engine.close()
+    _check_decode(model, _prompt(4096, 20, 19), 6, 64, w8=w8, label=f"hidden-1152-2L{' W8' if w8 else ''}")
+
+
 def test_smollm_4_layer_decode_within_1e2():
     model = SyntheticModel(SMOLLM2_135M, seed=0, layers=4)
     _check_decode(model, _prompt(49152, 35, 11), 16, 64, label="smollm2-135m-4L")

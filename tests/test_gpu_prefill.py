@@ -245,3 +245,40 @@ def test_prefill_w8_long_prompt():
     """600 tokens: the 128-token-tile W8 GEMMs (no K split)."""
     model = SyntheticModel(QWEN25_05B, seed=5, layers=2)
     _prefill_case(model, _prompt(151936, 600, 18), 4, 1024, 1e-2, "qwen-2L-600-w8", w8=True)
+
+
+def test_prefill_split_down_wait_limit(monkeypatch):
+    """Short prompts run the down projection with K split four ways inside an
+    XCD, part 0 polling the other parts' partial sums with a bounded wait.
+    With a spin limit of 0 (set from the host: the first poll that finds a
+    part missing gives up) a prefill either completes or raises RuntimeError
+    ("prefill abandoned"), every kernel exiting normally; every prefill that
+    completes matches the oracle, and after an abandon the engine runs the
+    slabs unsplit, so at most one of three prefills is abandoned."""
+    from runtime.qwen_engine import QwenDecoderEngine
+
+    announce("prefill: K-split down with a zero wait limit")
+    model = SyntheticModel(QWEN25_05B, seed=21, layers=2)
+    prompt = _prompt(151936, 40, 22)
+    monkeypatch.setenv("HK_PERSISTENT_SPIN", "0")
+    engine = QwenDecoderEngine(model, context_length=64)
+    monkeypatch.delenv("HK_PERSISTENT_SPIN")
+    oracle = OracleDecoder(model, 64)
+    ref_tokens, ref_logits = oracle.generate_greedy(prompt, 1)
+    abandoned = 0
+    try:
+        for attempt in range(3):
+            try:
+                tok, logits = engine.prefill(prompt, 0)
+            except RuntimeError as err:
+                announce(f"  prefill {attempt}: {err}")
+                assert "prefill abandoned" in str(err)
+                abandoned += 1
+                continue
+            err = rel_l2(logits, ref_logits[0])
+            announce(f"  prefill {attempt}: rel-L2 {err:.3e}")
+            assert err <= 1e-2
+            assert tok == ref_tokens[0] or near_tie(ref_logits[0])
+        assert abandoned <= 1, "after an abandon the engine runs the slabs unsplit"
+    finally:
+        engine.close()
