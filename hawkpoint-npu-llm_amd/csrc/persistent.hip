@@ -1915,10 +1915,15 @@ __global__ __launch_bounds__(kPT) void decode_step_xa_kernel(PersistentArgs args
         // ---- attention tasks (q/k/v from XCD 0, outputs back to it); the
         // next layer's MLP weights go out after them, not ahead of their
         // K/V loads and polls ----
+        // Task t runs on rank t, i.e. on XCD t % 7 + 1: when the query heads
+        // are a multiple of 7, every chunk of head h (tasks h + HQ s) runs on
+        // XCD h % 7 + 1 beside the head's merging task, and the split-KV
+        // partials stay in that XCD's L2
+        constexpr int kPartPol = S::HQ % (kXcds - 1) == 0 ? kLocal : kSc1;
         for (int t = rank; t < tasks_l; t += kPersistentGrid - kXcdWg) {
           __syncthreads();  // LDS reuse
-          if (!attention_task<S, kSc1, 16>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1), tag_of(ep + 2),
-                                           ptag_of(ep + 2)))
+          if (!attention_task<S, kSc1, 16, kPartPol>(c, l, t % S::HQ, t / S::HQ, p, tag_of(ep + 1),
+                                                     tag_of(ep + 2), ptag_of(ep + 2)))
             return;
         }
         if (l > 0) {
