@@ -267,6 +267,88 @@ constexpr int kBM = 128;
 constexpr int kBK = 64;
 constexpr int kBRow = kBK + 8;  // bf16 per LDS row (rows 144 B apart: no bank conflicts)
 
+// The epilogue of the large-M GEMMs: the tile's outputs go through LDS (ep:
+// BM x (BN + 8) bf16, free once every wave is past the last K step) so that
+// they leave as 16-byte stores of 8 outputs of a row, with the residual rows
+// read the same way.  Wave tiles: rows wm.., columns wn.. of the tile, MB x
+// NB MFMA 16 x 16 blocks (D layout: lane holds rows 4 (lane / 16) + r,
+// column lane % 16 of each block).
+template <int BM, int BN, bool PAIR, bool W8, int MB, int NB>
+__device__ __forceinline__ void tile_epilogue(const PrefillGemmArgs& a, const f32x4 (&acc)[MB][NB],
+                                              const f32x4 (&accu)[PAIR ? MB : 1][PAIR ? NB : 1], uint16_t* ep,
+                                              int m0, int n0, int wm, int wn, int tid, int lane) {
+  // LDS holds, per output,
+  // the bf16 that the epilogue's first rounding gives: the finished value
+  // for EPI_BF16 and EPI_SWIGLU, bf16(sum) (exact, the value the bias or the
+  // residual is added to) for EPI_BIAS and EPI_RESID.  The rounding points
+  // are those of the other GEMM kernels.
+  constexpr int ER = BN + 8;  // bf16 per LDS row of the tile
+  const int fr = lane & 15;
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ml = wm + 16 * i + (lane >> 4) * 4 + r, nl = wn + 16 * j + fr;
+        const int n = min(n0 + nl, a.N - 1);
+        float v = acc[i][j][r];
+        float u = 0.0f;
+        if constexpr (PAIR) u = accu[i][j][r];
+        if constexpr (W8) {
+          v *= a.scale[n];
+          if constexpr (PAIR) u *= a.scale[a.N + n];
+        }
+        uint32_t y;
+        if constexpr (PAIR)
+          y = a.epi == EPI_SWIGLU ? f32_to_bf16(silu_mul(round_bf16(v), round_bf16(u))) : f32_to_bf16(v);
+        else
+          y = f32_to_bf16(v);
+        ep[ml * ER + nl] = (uint16_t)y;
+      }
+  __syncthreads();
+  const bool add_bias = a.epi == EPI_BIAS, add_resid = a.epi == EPI_RESID;
+  for (int c = tid; c < BM * BN / 8; c += kThreads) {
+    const int ml = c / (BN / 8), nl = (c % (BN / 8)) * 8;
+    const int m = m0 + ml, n = n0 + nl;
+    if (m >= a.M || n >= a.N) continue;
+    const uint16_t* src = ep + ml * ER + nl;
+    uint16_t* y = a.Y + (size_t)m * a.ldy + n;
+    if (n + 8 > a.N) {  // a ragged last chunk of the row
+      for (int e = 0; e < a.N - n; ++e) {
+        float f = bf16_to_f32(src[e]);
+        if (add_bias) f = round_bf16(f + a.bias[n + e]);
+        if (add_resid) f = round_bf16(f + bf16_to_f32(a.resid[(size_t)m * a.ldr + n + e]));
+        y[e] = (uint16_t)f32_to_bf16(f);
+      }
+      continue;
+    }
+    u32x4 w = *reinterpret_cast<const u32x4*>(src);
+    if (add_bias || add_resid) {
+      float addend[8];
+      if (add_resid) {
+        const u32x4 rr = load16(a.resid + (size_t)m * a.ldr + n);
+        const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          addend[2 * q] = bf_lo(rw[q]);
+          addend[2 * q + 1] = bf_hi(rw[q]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) addend[e] = a.bias[n + e];
+      }
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = f32x2_to_bf16x2(bf_lo(ww[q]) + addend[2 * q], bf_hi(ww[q]) + addend[2 * q + 1]);
+      w = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    *reinterpret_cast<u32x4*>(y) = w;
+  }
+}
+
 // SPLIT (too few tiles to fill the GPU): workgroup (x, y) takes tile x
 // (token tiles varying fastest) and the y-th of gridDim.y runs of K steps,
 // and stores float32 partial sums to split_ws[y][m][outputs] (SwiGLU: up
@@ -409,79 +491,168 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
         }
     return;
   }
-  // The tile's outputs go through LDS (the operand buffers are free after
-  // the last barrier) so that they leave as 16-byte stores of 8 outputs of a
-  // row, with the residual rows read the same way.  LDS holds, per output,
-  // the bf16 that the epilogue's first rounding gives: the finished value
-  // for EPI_BF16 and EPI_SWIGLU, bf16(sum) (exact, the value the bias or the
-  // residual is added to) for EPI_BIAS and EPI_RESID.  The rounding points
-  // are those of the other GEMM kernels.
-  constexpr int ER = BN + 8;  // bf16 per LDS row of the tile
-  static_assert(BM * ER <= 2 * BM * kBRow, "the tile fits the A buffers");
-  uint16_t* ep = &As[0][0][0];
+  static_assert(BM * (BN + 8) <= 2 * BM * kBRow, "the tile fits the A buffers");
+  tile_epilogue<BM, BN, PAIR, W8, MB, NB>(a, acc, accu, &As[0][0][0], m0, n0, wm, wn, tid, lane);
+}
+
+// Large-M GEMM, bf16 weights, with a ring of NS LDS stages of 32 K each
+// filled by buffer -> LDS loads (16 bytes per lane, 1 KiB per instruction):
+// the workgroup keeps NS - 1 stages of loads in flight while it multiplies
+// one, where gemm_big_kernel's register staging keeps one.  Tiles, waves and
+// epilogue as gemm_big_kernel (128 tokens x BN outputs, 2 x 2 waves).
+// A stage row is 32 bf16 = four 16-byte pieces; piece c of tile row r sits at
+// position c ^ ring_swizzle(r), so that a fragment read (16 rows, one piece)
+// touches distinct banks in every group of 8 lanes (128 bytes) and of 16
+// lanes (256 bytes).  Every load goes through a buffer resource: rows
+// past M (tokens) or N (outputs) read zero.  Wave w's loads cover A rows
+// 16 (w AI + i) .. and weight rows 16 (w WI + i) ..; each wave waits for its
+// own loads of a stage, the barrier after that for everyone's.
+constexpr int kRK = 32;  // K per ring stage
+
+// The ring's piece position key of tile row r (only r % 16 matters):
+// 0 0 1 1 2 2 3 3 1 1 0 0 3 3 2 2.  Rows r and r + 2 (64 bytes x 2 apart,
+// the same 128-byte bank window) get different keys, and so do rows r and r
+// + 4, r + 8, r + 12 (the same 256-byte window).
+__device__ __forceinline__ int ring_swizzle(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
+// 16 bytes from LDS, issued as assembly: the caller waits (lgkmcnt) before
+// it uses the value, then passes it through lds_ready.  (The VGPR operand
+// constraints exist in the device pass only.)
+__device__ __forceinline__ bf16x8 lds_read16(const uint16_t* p) {
+  bf16x8 v;
+#if __HIP_DEVICE_COMPILE__
+  const unsigned addr = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+#endif
+  return v;
+}
+
+// n buffer -> LDS loads of 16 bytes per lane: load i of the wave fills the
+// 1 KiB at dst + 512 i (elements) from byte offsets off[i] + kb of r.  (A
+// device function: in a lambda the LDS address-space cast would be checked
+// for the host too.)
+template <int n>
+__device__ __forceinline__ void ring_loads(__amdgpu_buffer_rsrc_t r, uint16_t* dst, const unsigned* off,
+                                           unsigned kb) {
+#pragma unroll
+  for (int i = 0; i < n; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst + 16 * kRK * i), 16,
+                                             off[i] + kb, 0, 0, 0);
+}
+
+// A value of lds_read16 as used after the wait that follows the reads: an
+// empty statement after that wait, which the uses depend on.
+__device__ __forceinline__ void lds_ready(bf16x8& v) {
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("" : "+v"(v));
+#endif
+}
+
+template <int BN, bool PAIR, int NS>
+__global__ __launch_bounds__(kThreads) void gemm_ring_kernel(PrefillGemmArgs a) {
+  constexpr int BM = kBM;
+  constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
+  constexpr int MB = BM / 32, NB = BN / 32;
+  constexpr int SA = BM * kRK, SW = WR * kRK;  // bf16 per stage
+  constexpr int AI = BM / 16 / (kThreads / 64), WI = WR / 16 / (kThreads / 64);
+  constexpr int PER = AI + WI;  // loads per wave per stage
+  static_assert(AI >= 1 && WI >= 1 && NS >= 3, "ring shape");
+  static_assert(BM * (BN + 8) <= NS * (SA + SW), "the epilogue tile fits the ring");
+  __shared__ __attribute__((aligned(16))) uint16_t ring[NS][SA + SW];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int mt = (a.M + BM - 1) / BM, ntile = (a.N + BN - 1) / BN;
+  // tile order as gemm_big_kernel (each XCD a contiguous run, grouped so the
+  // tiles an XCD holds at once share token and weight tiles)
+  const int per = (mt * ntile + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (t >= mt * ntile) return;
+  const int GN = ntile <= 12 ? ntile : 4;
+  const int grp = t / (GN * mt), gn = min(GN, ntile - grp * GN), in = t - grp * GN * mt;
+  const int m0 = (in / gn) * BM;
+  const int n0 = (grp * GN + in % gn) * BN;
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  const int fr = lane & 15;
+  const int steps = a.K / kRK;
+
+  const __amdgpu_buffer_rsrc_t ra = rsrc(a.A, a.M * a.lda * 2);
+  const __amdgpu_buffer_rsrc_t rw = rsrc(a.W, (PAIR ? 2 : 1) * a.N * a.K * 2);
+  // this lane's row within a 16-row load block and the global piece it
+  // fetches (its LDS position is lane & 3)
+  const int lr = lane >> 2, lg = (lane & 3) ^ ring_swizzle(lr);
+  unsigned aoff[AI], woff[WI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) aoff[i] = (unsigned)(((m0 + 16 * (wave * AI + i) + lr) * a.lda + 8 * lg) * 2);
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int r = 16 * (wave * WI + i) + lr;  // tile row: gate rows first, then up rows
+    const int row = PAIR ? (r < BN ? n0 + r : a.N + n0 + r - BN) : n0 + r;
+    woff[i] = (unsigned)((row * a.K + 8 * lg) * 2);
+  }
+  f32x4 acc[MB][NB], accu[PAIR ? MB : 1][PAIR ? NB : 1];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int ml = wm + 16 * i + (lane >> 4) * 4 + r, nl = wn + 16 * j + fr;
-        const int n = min(n0 + nl, a.N - 1);
-        float v = acc[i][j][r];
-        float u = 0.0f;
-        if constexpr (PAIR) u = accu[i][j][r];
-        if constexpr (W8) {
-          v *= a.scale[n];
-          if constexpr (PAIR) u *= a.scale[a.N + n];
-        }
-        uint32_t y;
-        if constexpr (PAIR)
-          y = a.epi == EPI_SWIGLU ? f32_to_bf16(silu_mul(round_bf16(v), round_bf16(u))) : f32_to_bf16(v);
-        else
-          y = f32_to_bf16(v);
-        ep[ml * ER + nl] = (uint16_t)y;
-      }
-  __syncthreads();
-  const bool add_bias = a.epi == EPI_BIAS, add_resid = a.epi == EPI_RESID;
-  for (int c = tid; c < BM * BN / 8; c += kThreads) {
-    const int ml = c / (BN / 8), nl = (c % (BN / 8)) * 8;
-    const int m = m0 + ml, n = n0 + nl;
-    if (m >= a.M || n >= a.N) continue;
-    const uint16_t* src = ep + ml * ER + nl;
-    uint16_t* y = a.Y + (size_t)m * a.ldy + n;
-    if (n + 8 > a.N) {  // a ragged last chunk of the row
-      for (int e = 0; e < a.N - n; ++e) {
-        float f = bf16_to_f32(src[e]);
-        if (add_bias) f = round_bf16(f + a.bias[n + e]);
-        if (add_resid) f = round_bf16(f + bf16_to_f32(a.resid[(size_t)m * a.ldr + n + e]));
-        y[e] = (uint16_t)f32_to_bf16(f);
-      }
-      continue;
+    for (int j = 0; j < NB; ++j) {
+      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (PAIR) accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    u32x4 w = *reinterpret_cast<const u32x4*>(src);
-    if (add_bias || add_resid) {
-      float addend[8];
-      if (add_resid) {
-        const u32x4 rr = load16(a.resid + (size_t)m * a.ldr + n);
-        const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          addend[2 * q] = bf_lo(rw[q]);
-          addend[2 * q + 1] = bf_hi(rw[q]);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) addend[e] = a.bias[n + e];
-      }
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        o[q] = f32x2_to_bf16x2(bf_lo(ww[q]) + addend[2 * q], bf_hi(ww[q]) + addend[2 * q + 1]);
-      w = u32x4{o[0], o[1], o[2], o[3]};
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < steps) {
+      ring_loads<AI>(ra, &ring[st][16 * wave * AI * kRK], aoff, (unsigned)(st * kRK * 2));
+      ring_loads<WI>(rw, &ring[st][SA + 16 * wave * WI * kRK], woff, (unsigned)(st * kRK * 2));
     }
-    *reinterpret_cast<u32x4*>(y) = w;
+  // this lane's fragment piece (k 8 (lane / 16) .. of the stage) at its
+  // swizzled position in rows of its fragment (row & 15 = lane & 15)
+  const int pos = ((lane >> 4) ^ ring_swizzle(lane & 15)) * 8;
+  for (int k = 0; k < steps; ++k) {
+    // stage k has landed once at most NS - 2 later stages are in flight
+    if (k + NS - 2 < steps)
+      __builtin_amdgcn_s_waitcnt(((NS - 2) * PER & 15) | ((((NS - 2) * PER) >> 4) << 14) | (7 << 4) | (15 << 8));
+    else
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+    // A barrier without a fence, and the fragment reads in assembly: the
+    // compiler would otherwise wait for every buffer -> LDS load in flight
+    // (the later stages' too) before the barrier or before the first read.
+    // The waits above and below are the ones these reads need.
+    asm volatile("s_barrier" ::: "memory");
+    // the buffer of stage k - 1 is free: every wave is past its products
+    if (k + NS - 1 < steps) {
+      const int st = k + NS - 1;
+      ring_loads<AI>(ra, &ring[st % NS][16 * wave * AI * kRK], aoff, (unsigned)(st * kRK * 2));
+      ring_loads<WI>(rw, &ring[st % NS][SA + 16 * wave * WI * kRK], woff, (unsigned)(st * kRK * 2));
+    }
+    const uint16_t* as = &ring[k % NS][0];
+    const uint16_t* ws = as + SA;
+    bf16x8 af[MB], bf[NB], uf[PAIR ? NB : 1];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) af[i] = lds_read16(as + (wm + 16 * i + fr) * kRK + pos);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      bf[j] = lds_read16(ws + (wn + 16 * j + fr) * kRK + pos);
+      if constexpr (PAIR) uf[j] = lds_read16(ws + (BN + wn + 16 * j + fr) * kRK + pos);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // (the products take the fragments from here on: after the wait)
+#pragma unroll
+    for (int i = 0; i < MB; ++i) lds_ready(af[i]);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      lds_ready(bf[j]);
+      if constexpr (PAIR) lds_ready(uf[j]);
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        if constexpr (PAIR) accu[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], uf[j], accu[i][j], 0, 0, 0);
+      }
   }
+  __syncthreads();  // the ring becomes the epilogue's tile
+  tile_epilogue<BM, BN, PAIR, false, MB, NB>(a, acc, accu, &ring[0][0], m0, n0, wm, wn, tid, lane);
 }
 
 // ---- slab GEMM: prompts of at most 64 tokens ----
@@ -1291,6 +1462,16 @@ int launch_slab(const PrefillGemmArgs& a, hipStream_t stream) {
   return err == hipSuccess ? 0 : hip_fail(err, "slab gemm launch");
 }
 
+// HK_GEMM_RING=0 runs the long-prompt bf16 GEMMs on gemm_big_kernel
+// instead of gemm_ring_kernel (read once).
+bool ring_gemm() {
+  static const bool on = [] {
+    const char* v = std::getenv("HK_GEMM_RING");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 template <bool W8>
 int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   const bool pair = a.epi == EPI_SWIGLU;
@@ -1337,7 +1518,27 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     err = hipGetLastError();
     return err == hipSuccess ? 0 : hip_fail(err, "split reduce launch");
   }
-  if (a.grp_count == nullptr && a.M >= kBM && a.K % kBK == 0) {
+  if (!W8 && ring_gemm() && a.grp_count == nullptr && a.M >= kBM && a.K % kRK == 0) {
+    // the LDS-ring form of the 128-token tiles below (bf16 weights), with
+    // the same choice of tile width
+    const int mt = (a.M + kBM - 1) / kBM, slots = 2 * cu_count();
+    const int rounds64 = (mt * ((a.N + 63) / 64) + slots - 1) / slots;
+    const int rounds128 = (mt * ((a.N + 127) / 128) + slots - 1) / slots;
+    // when the 128-wide tiles fit one per CU (N = hidden at 4096 tokens),
+    // each takes a deeper ring: 9 stages, 144 KiB of LDS
+    const bool one_per_cu = !pair && mt * ((a.N + 127) / 128) <= cu_count();
+    const bool wide = !pair && (one_per_cu || rounds64 >= 2 * rounds128);
+    const int bn = wide ? 128 : 64;
+    const dim3 g(8 * ((mt * ((a.N + bn - 1) / bn) + 7) / 8));
+    if (pair)
+      hipLaunchKernelGGL((gemm_ring_kernel<64, true, 5>), g, dim3(kThreads), 0, stream, a);
+    else if (one_per_cu)
+      hipLaunchKernelGGL((gemm_ring_kernel<128, false, 9>), g, dim3(kThreads), 0, stream, a);
+    else if (wide)
+      hipLaunchKernelGGL((gemm_ring_kernel<128, false, 5>), g, dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gemm_ring_kernel<64, false, 6>), g, dim3(kThreads), 0, stream, a);
+  } else if (a.grp_count == nullptr && a.M >= kBM && a.K % kBK == 0) {
     // 128-token tiles, 64 or 128 outputs wide: two workgroups fit a CU, and
     // the wide tiles (about 1.7 times the work each) are taken when the
     // narrow ones would need at least twice as many rounds of workgroups
