@@ -26,6 +26,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short v4s16 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
@@ -273,10 +274,15 @@ constexpr int kBRow = kBK + 8;  // bf16 per LDS row (rows 144 B apart: no bank c
 // read the same way.  Wave tiles: rows wm.., columns wn.. of the tile, MB x
 // NB MFMA 16 x 16 blocks (D layout: lane holds rows 4 (lane / 16) + r,
 // column lane % 16 of each block).
-template <int BM, int BN, bool PAIR, bool W8, int MB, int NB>
-__device__ __forceinline__ void tile_epilogue(const PrefillGemmArgs& a, const f32x4 (&acc)[MB][NB],
-                                              const f32x4 (&accu)[PAIR ? MB : 1][PAIR ? NB : 1], uint16_t* ep,
-                                              int m0, int n0, int wm, int wn, int tid, int lane) {
+// DM 32: the blocks are MFMA 32 x 32 ones (lane holds rows 8 (r / 4) +
+// 4 (lane / 32) + r % 4, column lane % 32, r = 0..15).
+template <int DM> struct DBlock { using T = f32x4; };
+template <> struct DBlock<32> { using T = f32x16; };
+
+template <int BM, int BN, bool PAIR, bool W8, int MB, int NB, int DM = 16>
+__device__ __forceinline__ void tile_epilogue(const PrefillGemmArgs& a, const typename DBlock<DM>::T (&acc)[MB][NB],
+                                              const typename DBlock<DM>::T (&accu)[PAIR ? MB : 1][PAIR ? NB : 1],
+                                              uint16_t* ep, int m0, int n0, int wm, int wn, int tid, int lane) {
   // LDS holds, per output,
   // the bf16 that the epilogue's first rounding gives: the finished value
   // for EPI_BF16 and EPI_SWIGLU, bf16(sum) (exact, the value the bias or the
@@ -289,8 +295,9 @@ __device__ __forceinline__ void tile_epilogue(const PrefillGemmArgs& a, const f3
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int ml = wm + 16 * i + (lane >> 4) * 4 + r, nl = wn + 16 * j + fr;
+      for (int r = 0; r < (DM == 16 ? 4 : 16); ++r) {
+        const int ml = DM == 16 ? wm + 16 * i + (lane >> 4) * 4 + r : wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int nl = DM == 16 ? wn + 16 * j + fr : wn + 32 * j + (lane & 31);
         const int n = min(n0 + nl, a.N - 1);
         float v = acc[i][j][r];
         float u = 0.0f;
@@ -552,7 +559,7 @@ template <int BN, bool PAIR, int NS>
 __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(PrefillGemmArgs a) {
   constexpr int BM = kBM;
   constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
-  constexpr int MB = BM / 32, NB = BN / 32;
+  constexpr int MB = BM / 64, NB = BN / 64;  // MFMA 32 x 32 blocks per wave (64 x BN / 2 outputs)
   constexpr int SA = BM * kRK, SW = WR * kRK;  // bf16 per stage
   constexpr int AI = BM / 16 / (kThreads / 64), WI = WR / 16 / (kThreads / 64);
   constexpr int PER = AI + WI;  // loads per wave per stage
@@ -573,7 +580,7 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(PrefillGemmArgs a) 
   const int m0 = (in / gn) * BM;
   const int n0 = (grp * GN + in % gn) * BN;
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
-  const int fr = lane & 15;
+  const int fr = lane & 31;
   const int steps = a.K / kRK;
 
   const __amdgpu_buffer_rsrc_t ra = rsrc(a.A, a.M * a.lda * 2);
@@ -590,23 +597,27 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(PrefillGemmArgs a) 
     const int row = PAIR ? (r < BN ? n0 + r : a.N + n0 + r - BN) : n0 + r;
     woff[i] = (unsigned)((row * a.K + 8 * lg) * 2);
   }
-  f32x4 acc[MB][NB], accu[PAIR ? MB : 1][PAIR ? NB : 1];
+  f32x16 acc[MB][NB], accu[PAIR ? MB : 1][PAIR ? NB : 1];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (PAIR) accu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.f;
+        if constexpr (PAIR) accu[i][j][r] = 0.f;
+      }
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
     if (st < steps) {
       ring_loads<AI>(ra, &ring[st][16 * wave * AI * kRK], aoff, (unsigned)(st * kRK * 2));
       ring_loads<WI>(rw, &ring[st][SA + 16 * wave * WI * kRK], woff, (unsigned)(st * kRK * 2));
     }
-  // this lane's fragment piece (k 8 (lane / 16) .. of the stage) at its
-  // swizzled position in rows of its fragment (row & 15 = lane & 15)
-  const int pos = ((lane >> 4) ^ ring_swizzle(lane & 15)) * 8;
+  // MFMA 32 x 32 x 16: this lane's fragment piece in each 16-deep half h of
+  // the stage (k 16 h + 8 (lane / 32) ..) at its swizzled position in rows of
+  // its fragment (row & 15 = lane & 15)
+  const int pos0 = ((lane >> 5) ^ ring_swizzle(lane & 15)) * 8;
+  const int pos1 = ((2 + (lane >> 5)) ^ ring_swizzle(lane & 15)) * 8;
   for (int k = 0; k < steps; ++k) {
     // stage k has landed once at most NS - 2 later stages are in flight
     if (k + NS - 2 < steps)
@@ -626,33 +637,43 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(PrefillGemmArgs a) 
     }
     const uint16_t* as = &ring[k % NS][0];
     const uint16_t* ws = as + SA;
-    bf16x8 af[MB], bf[NB], uf[PAIR ? NB : 1];
+    bf16x8 af[2][MB], bf[2][NB], uf[2][PAIR ? NB : 1];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) af[i] = lds_read16(as + (wm + 16 * i + fr) * kRK + pos);
+    for (int h = 0; h < 2; ++h) {
+      const int pos = h ? pos1 : pos0;
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      bf[j] = lds_read16(ws + (wn + 16 * j + fr) * kRK + pos);
-      if constexpr (PAIR) uf[j] = lds_read16(ws + (BN + wn + 16 * j + fr) * kRK + pos);
+      for (int i = 0; i < MB; ++i) af[h][i] = lds_read16(as + (wm + 32 * i + fr) * kRK + pos);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        bf[h][j] = lds_read16(ws + (wn + 32 * j + fr) * kRK + pos);
+        if constexpr (PAIR) uf[h][j] = lds_read16(ws + (BN + wn + 32 * j + fr) * kRK + pos);
+      }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // (the products take the fragments from here on: after the wait)
 #pragma unroll
-    for (int i = 0; i < MB; ++i) lds_ready(af[i]);
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      lds_ready(bf[j]);
-      if constexpr (PAIR) lds_ready(uf[j]);
-    }
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
+      for (int i = 0; i < MB; ++i) lds_ready(af[h][i]);
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        if constexpr (PAIR) accu[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], uf[j], accu[i][j], 0, 0, 0);
+        lds_ready(bf[h][j]);
+        if constexpr (PAIR) lds_ready(uf[h][j]);
       }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[h][i], bf[h][j], acc[i][j], 0, 0, 0);
+          if constexpr (PAIR)
+            accu[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[h][i], uf[h][j], accu[i][j], 0, 0, 0);
+        }
   }
   __syncthreads();  // the ring becomes the epilogue's tile
-  tile_epilogue<BM, BN, PAIR, false, MB, NB>(a, acc, accu, &ring[0][0], m0, n0, wm, wn, tid, lane);
+  tile_epilogue<BM, BN, PAIR, false, MB, NB, 32>(a, acc, accu, &ring[0][0], m0, n0, wm, wn, tid, lane);
 }
 
 // ---- slab GEMM: prompts of at most 64 tokens ----
