@@ -556,7 +556,7 @@ __device__ __forceinline__ void lds_ready(bf16x8& v) {
 }
 
 template <int BN, bool PAIR, int NS>
-__global__ __launch_bounds__(kThreads) void gemm_ring_kernel(PrefillGemmArgs a) {
+__global__ __launch_bounds__(kThreads, PAIR && BN == 128 ? 2 : 1) void gemm_ring_kernel(PrefillGemmArgs a) {
   constexpr int BM = kBM;
   constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
   constexpr int MB = BM / 64, NB = BN / 64;  // MFMA 32 x 32 blocks per wave (64 x BN / 2 outputs)
@@ -1550,9 +1550,13 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     const bool one_per_cu = !pair && mt * ((a.N + 127) / 128) <= cu_count();
     const bool wide = !pair && (one_per_cu || rounds64 >= 2 * rounds128);
     const int bn = wide ? 128 : 64;
-    const dim3 g(8 * ((mt * ((a.N + bn - 1) / bn) + 7) / 8));
+    // (SwiGLU: 128 gate and 128 up rows per tile, each wave 64 tokens x 64
+    // gate + 64 up outputs, three 24 KiB stages; the kernel is held to two
+    // waves per SIMD, i.e. two workgroups per CU)
+    const int bnt = pair ? 128 : bn;
+    const dim3 g(8 * ((mt * ((a.N + bnt - 1) / bnt) + 7) / 8));
     if (pair)
-      hipLaunchKernelGGL((gemm_ring_kernel<64, true, 5>), g, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((gemm_ring_kernel<128, true, 3>), g, dim3(kThreads), 0, stream, a);
     else if (one_per_cu)
       hipLaunchKernelGGL((gemm_ring_kernel<128, false, 9>), g, dim3(kThreads), 0, stream, a);
     else if (wide)
