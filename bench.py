@@ -28,7 +28,8 @@ roofline (35-token prompt, 16 greedy tokens, 64-slot context).
 Other workloads (each prints its own JSON line): --workload experts (the
 GGML / Colibri expert shims), gemv (the isolated batch-1 GEMVs at the
 Qwen2.5-0.5B projection shapes, bf16 and W8, for kernel traces), prefill
-(batched prefill of 40- and 4064-token prompts, for kernel traces).
+(batched prefill of 40- and 4064-token prompts, for kernel traces), moe
+(the routed-expert block at 1..16 tokens, against the HBM roofline).
 """
 
 import argparse
@@ -265,10 +266,12 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--cpu-steps-one-thread", type=int, default=4)
     ap.add_argument("--no-smollm", action="store_true", help="skip the SmolLM2-135M decode line")
-    ap.add_argument("--workload", choices=("decode", "experts", "gemv", "prefill", "phases"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "experts", "gemv", "prefill", "phases", "moe"),
+                    default="decode",
                     help="experts: the GGML MUL_MAT_ID / Colibri expert-group shims; gemv: the isolated "
                     "GEMVs; prefill: batched prefills of 40 and 4064 tokens; phases: the per-layer phase "
-                    "table of the decode step from lib/libhk_phases.so (each prints its own JSON line)")
+                    "table of the decode step from lib/libhk_phases.so; moe: the routed-expert block "
+                    "(H 2048, 64 + 2 experts of I 1408, top-6) at 1..16 tokens (each prints its own JSON line)")
     ap.add_argument("--phases-model", choices=("qwen", "qwen-w8", "smollm"), default="qwen",
                     help="phases: the decoder whose step is stamped")
     ap.add_argument("--phases-long", action="store_true",
@@ -292,6 +295,9 @@ def main():
         return
     if args.workload == "phases":
         phases_main(args)
+        return
+    if args.workload == "moe":
+        moe_main(args)
         return
 
     import numpy as np
@@ -727,6 +733,132 @@ def prefill_main(args):
     out["flops_4064"] = 2.0 * 4064 * layer_params(meta) + attn
     out["flops_40"] = 2.0 * PROMPT * layer_params(meta)
     print(json.dumps(out), flush=True)
+
+
+MOE_COPIES = 3  # device copies of the MoE block cycled by the timed calls (3 x 1.14 GB)
+MOE_BATCHES = 8  # distinct random token batches per copy
+
+
+def moe_call_bytes(shape, unique_routed, tokens):
+    """Algorithmic HBM bytes of one MoE block call: the router, the gate/up and
+    down weights of every routed expert the batch selects (each read once) and
+    of the shared experts, the bf16 input and output rows, the routing."""
+    H, I, E, S, k = (shape[n] for n in ("hidden", "intermediate", "experts", "shared", "top_k"))
+    expert = (2 * I * H + H * I) * 2
+    return E * H * 2 + (unique_routed + S) * expert + 2 * tokens * H * 2 + 8 * tokens * k
+
+
+def moe_main(args):
+    """The routed-expert block (config: hidden 2048, 64 routed experts + 2
+    shared of SwiGLU intermediate 1408, top-6 from a softmax router, bf16
+    N(0, 0.02) weights, tokens N(0, 1)) at 1, 2, 4, 8 and 16 tokens.  Each
+    timed call runs hk_moe_forward (router, top-k, grouped expert GEMMs,
+    combine) on one of three device copies of the block and one of eight
+    token batches, so no call finds its experts in the 256 MB Infinity Cache
+    from the call before; HIP events around the calls; bytes are each call's
+    own selection (its distinct routed experts)."""
+    import ctypes
+
+    import numpy as np
+
+    from runtime import hip
+    from runtime.bf16 import to_bits
+    from runtime.moe import MOE_2048_64X1408, MoEBlock, synthetic_moe
+
+    shape = MOE_2048_64X1408
+    H, k = shape["hidden"], shape["top_k"]
+    hip.init(0)
+    lib = hip.lib()
+    log("building the MoE block (64 + 2 experts of 2048 -> 1408 -> 2048)")
+    router, gate_up, down = synthetic_moe(shape, seed=0)
+    blocks = [MoEBlock(router, gate_up, down, top_k=k, shared=shape["shared"], max_tokens=16)
+              for _ in range(MOE_COPIES)]
+    rng = np.random.default_rng(21)
+    xs = to_bits(rng.standard_normal((MOE_BATCHES, 16, H), dtype=np.float32))
+    xbuf = hip.DeviceBuffer.from_array(xs)
+    ybuf = hip.DeviceBuffer(2 * 16 * H)
+    ids = hip.DeviceBuffer(4 * 16 * k)
+    xptr = lambda r: xbuf.ptr + r * 16 * H * 2
+
+    def call(b, r, tokens, with_ids=False):
+        hip.check(lib.hk_moe_forward(blocks[b]._moe, ctypes.c_void_p(xptr(r)), tokens, ybuf.ptr,
+                                     ids.ptr if with_ids else None, None, None), "hk_moe_forward")
+
+    n = max(args.kernel_launches, MOE_COPIES * MOE_BATCHES)
+    rows = []
+    for tokens in (1, 2, 4, 8, 16):
+        nbytes = []
+        for r in range(MOE_BATCHES):  # each batch's selection (the copies route alike)
+            call(0, r, tokens, with_ids=True)
+            hip.check(lib.hk_stream_sync(None), "sync")
+            sel = ids.read(np.int32, tokens * k)
+            nbytes.append(moe_call_bytes(shape, len(set(sel.tolist())), tokens))
+        order = [(i % MOE_COPIES, (i // MOE_COPIES) % MOE_BATCHES) for i in range(n)]
+        for b, r in order:  # warm
+            call(b, r, tokens)
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(None)
+        for b, r in order:
+            call(b, r, tokens)
+        e1.record(None)
+        hip.check(lib.hk_stream_sync(None), "sync")
+        us = e0.elapsed_ms(e1) * 1e3 / n
+        mean_bytes = sum(nbytes[r] for _, r in order) / n
+        gbs = mean_bytes / (us * 1e-6) / 1e9
+        rows.append({"tokens": tokens, "us_per_call": round(us, 2), "bytes_per_call": int(mean_bytes),
+                     "hbm_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"MoE block, {tokens} token(s): {us:.1f} us per call, {mean_bytes / 1e6:.1f} MB, "
+            f"{gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of the HBM peak)")
+    best = max(rows, key=lambda r: r["frac"])
+    result = {
+        "metric": "MoE block calls/s at 16 tokens, experts from HBM",
+        "value": round(1e6 / rows[-1]["us_per_call"], 1),
+        "unit": "calls/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": n,
+        "ms_per_step": round(rows[-1]["us_per_call"] / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "routed-expert block: hidden 2048, 64 routed + 2 shared experts, SwiGLU "
+            "intermediate 1408, top-6 softmax router, bf16 N(0,0.02) weights, tokens N(0,1); calls "
+            f"cycle {MOE_COPIES} device copies of the block x {MOE_BATCHES} token batches",
+            **shape,
+        },
+        "by_tokens": rows,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "the whole hk_moe_forward call (router, plan, grouped gate/up + SwiGLU, down, "
+            f"combine) at {best['tokens']} token(s)",
+            "achieved": best["hbm_gbs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": best["frac"],
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        from threadpoolctl import threadpool_limits
+
+        from oracle.moe import moe_forward
+
+        log("timing the CPU oracle (one token per call)")
+        calls, t0 = 0, time.perf_counter()
+        with threadpool_limits(limits=1):
+            while time.perf_counter() - t0 < 10.0 or calls == 0:
+                moe_forward(xs[calls % MOE_BATCHES, :1], router, gate_up, down, top_k=k, shared=shape["shared"])
+                calls += 1
+        elapsed = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": round(calls / elapsed, 3), "unit": "calls/s (1 token)", "cores": 1,
+                                  "kind": "port",
+                                  "sample": f"{calls} one-token block calls through oracle/moe.py, one BLAS thread"}
+    for b in blocks:
+        b.close()
+    print(json.dumps(result), flush=True)
 
 
 EXPERTS, EXPERT_ROWS, EXPERT_COLS = 8, 2048, 2048  # the reference's 8 expert slots of 2048 x 2048

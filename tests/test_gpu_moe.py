@@ -55,6 +55,30 @@ def test_moe_block_matches_oracle(block, moe_weights, tokens):
         assert err <= 1e-2, (t, err)
 
 
+def test_moe_block_beyond_16_tokens_matches_oracle(moe_weights):
+    """24 tokens: groups of more than 16 rows run on the grouped tile GEMM
+    (up to 16 on the expert slabs), and the top-k waves take two tokens each."""
+    from runtime.moe import MoEBlock
+
+    router, gate_up, down = moe_weights
+    announce("moe block T=24 (grouped tile GEMM)")
+    b = MoEBlock(router, gate_up, down, top_k=6, shared=2, max_tokens=32)
+    try:
+        rng = np.random.default_rng(124)
+        x = bf16.to_bits(rng.normal(0, 1, (24, 2048)).astype(np.float32))
+        y, ids, w = b.forward(x)
+    finally:
+        b.close()
+    ref_y, ref_ids, ref_w = moe_forward(x, router, gate_up, down, top_k=6, shared=2)
+    for t in range(24):
+        if not np.array_equal(ids[t], ref_ids[t]):
+            _, _, probs = route(router, bf16.from_bits(x[t]), 6)
+            assert min(_tie_gap(probs, k) for k in range(1, 7)) < 1e-6, (t, ids[t], ref_ids[t])
+            continue
+        np.testing.assert_allclose(w[t], ref_w[t], rtol=1e-5, atol=1e-7)
+        assert rel_l2(bf16.from_bits(y[t]), bf16.from_bits(ref_y[t])) <= 1e-2, t
+
+
 def test_moe_experts_with_given_routing(block, moe_weights):
     """The MUL_MAT_ID form with caller ids equals the routed forward."""
     announce("moe experts with given ids")
@@ -67,6 +91,31 @@ def test_moe_experts_with_given_routing(block, moe_weights):
     bad[0, 0] = 64
     with pytest.raises(ValueError):
         block.experts(x, bad, w)
+
+
+def test_moe_experts_repeated_ids_beyond_16_rows(block, moe_weights):
+    """Caller ids may name one expert several times per token: 3 tokens x 6
+    times expert 3 is 18 rows for one expert, more than the expert slabs
+    take, so the grouped tile GEMM runs; against the oracle's experts and
+    combine (oracle/moe.py moe_forward's order)."""
+    from oracle.moe import expert_forward
+
+    router, gate_up, down = moe_weights
+    announce("moe experts, one expert named 18 times")
+    rng = np.random.default_rng(9)
+    x = bf16.to_bits(rng.normal(0, 1, (3, 2048)).astype(np.float32))
+    ids = np.full((3, 6), 3, dtype=np.int32)
+    w = rng.uniform(0.05, 0.3, (3, 6)).astype(np.float32)
+    y = block.experts(x, ids, w)
+    for t in range(3):
+        xt = bf16.from_bits(x[t])
+        e3 = expert_forward(gate_up[3], down[3], xt)
+        acc = np.zeros(2048, dtype=np.float32)
+        for k in range(6):
+            acc = acc + w[t, k] * e3
+        for s_ in range(2):
+            acc = acc + expert_forward(gate_up[64 + s_], down[64 + s_], xt)
+        assert rel_l2(bf16.from_bits(y[t]), bf16.from_bits(bf16.to_bits(acc))) <= 1e-2, t
 
 
 def test_w8_expert_gemv_reference_pattern(hk_lib):
