@@ -131,45 +131,64 @@ __device__ __forceinline__ void topk_wave(const float* logits, int t, int E, int
 
 // The grouping of the T*(K+S) (token, expert) pairs by expert, from the ids
 // in LDS, on the calling workgroup (nt threads; every thread calls it):
-// counts by LDS atomics, the offsets and the non-empty groups by one thread
-// (E + S entries), then routed expert e's slots by thread e, which walks the
-// pairs in token order (an expert appears at most once per token), and
-// shared expert s's slots (one per token) by thread E + s.  Within an expert
-// the slots follow token order, so the plan does not depend on timing.
+// counts by LDS atomics; the offsets and the non-empty groups on wave 0 (lane
+// e: routed expert e, a prefix sum across lanes, the group index from a
+// ballot; the shared experts follow the routed pairs); then routed expert
+// e's slots by thread e, which walks the pairs in token order (an expert
+// appears at most once per token from the router; repeated caller ids take
+// consecutive slots), and shared expert s's slots (one per token) by thread
+// E + s.  Within an expert the slots follow token order, so the plan does not
+// depend on timing.
 __device__ void plan_pairs(const int32_t* ids, int T, int K, int E, int S, int nt, int* counts, int* offs,
                            int32_t* grp_expert, int32_t* grp_count, int32_t* grp_offset, int32_t* n_groups,
                            int32_t* a_rows, int32_t* pair_slot) {
+  static_assert(kMaxRouted <= 64, "one lane per routed expert");
   const int tid = threadIdx.x;
   const int total = E + S, per = K + S;
   auto clamp = [&](int e) { return e < 0 ? 0 : (e >= E ? E - 1 : e); };
-  for (int e = tid; e < total; e += nt) counts[e] = e < E ? 0 : T;
+  for (int e = tid; e < E; e += nt) counts[e] = 0;
   __syncthreads();
   for (int i = tid; i < T * K; i += nt) atomicAdd(&counts[clamp(ids[i])], 1);
   __syncthreads();
-  if (tid == 0) {
-    int n = 0, off = 0;
-    for (int e = 0; e < total; ++e) {
-      offs[e] = off;
-      if (counts[e] == 0) continue;
-      grp_expert[n] = e;
-      grp_count[n] = counts[e];
-      grp_offset[n] = off;
-      off += counts[e];
-      ++n;
+  if (tid < 64) {
+    const int lane = tid;
+    const int c = lane < E ? counts[lane] : 0;
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
     }
-    *n_groups = n;
+    const unsigned long long nonempty = __ballot(c > 0);
+    const int g = __popcll(nonempty & ((1ull << lane) - 1ull));
+    const int nr = __popcll(nonempty);
+    if (lane < E) {
+      offs[lane] = incl - c;
+      if (c > 0) {
+        grp_expert[g] = lane;
+        grp_count[g] = c;
+        grp_offset[g] = incl - c;
+      }
+    }
+    if (lane < S) {  // shared expert lane: every token, after the routed pairs
+      offs[E + lane] = T * K + lane * T;
+      grp_expert[nr + lane] = E + lane;
+      grp_count[nr + lane] = T;
+      grp_offset[nr + lane] = T * K + lane * T;
+    }
+    if (lane == 0) *n_groups = nr + S;
   }
   __syncthreads();
   for (int e = tid; e < total; e += nt) {
     int slot = offs[e];
     if (e < E) {
-      for (int t = 0; t < T; ++t)
-        for (int k = 0; k < K; ++k)
-          if (clamp(ids[t * K + k]) == e) {
-            a_rows[slot] = t;
-            pair_slot[t * per + k] = slot;
-            ++slot;
-          }
+#pragma unroll 8
+      for (int i = 0; i < T * K; ++i)
+        if (clamp(ids[i]) == e) {
+          a_rows[slot] = i / K;
+          pair_slot[(i / K) * per + i % K] = slot;
+          ++slot;
+        }
     } else {
       for (int t = 0; t < T; ++t, ++slot) {
         a_rows[slot] = t;
