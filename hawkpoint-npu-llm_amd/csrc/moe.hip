@@ -260,31 +260,40 @@ constexpr int kSlabBatchE = 8;                  // K steps per wave requested at
 constexpr int kSlabMaxRowsE = 16;               // rows per expert group on expert_slab
 
 // Expert GEMM for groups of at most 16 rows (the decode batch).  Workgroup
-// (s, z) computes outputs 16 s .. + 15 of group z's expert (W + expert *
-// w_stride) for the group's rows: wave w takes the 32-column K steps w, w +
+// (s, z) computes outputs 16 s .. + 15 of group z's expert (the MFMA-native
+// copy Wn + expert * w_stride) for the group's rows: wave w takes the 32-column K steps w, w +
 // 8, ..., requests the weight fragments (and the up rows' for SwiGLU) and the
 // row fragments of up to kSlabBatchE of them at once, and multiplies on MFMA
 // 16x16x32 (rows x outputs); the waves' partial sums meet in LDS and are added
 // in wave order.  Row i of the group reads A row a_rows[offset + i] (or offset
 // + i) and writes output row offset + i.  Epilogue as the dense layer:
 // SwiGLU bf16(silu(bf16(g)) * bf16(u)), else bf16.
-template <bool PAIR>
+// TWO (without SwiGLU): the workgroup takes outputs 32 s .. + 31, the second
+// 16 in place of the up rows (one row fragment, two weight fragments per K step).
+template <bool PAIR, bool TWO = false>
 __global__ __launch_bounds__(kSlabThreads) void expert_slab_kernel(PrefillGemmArgs a) {
-  __shared__ f32x4 red[PAIR ? 2 : 1][kSlabWavesE][64];
+  static_assert(!(PAIR && TWO), "SwiGLU pairs take one slab");
+  constexpr bool U = PAIR || TWO;  // a second weight fragment per step
+  __shared__ f32x4 red[U ? 2 : 1][kSlabWavesE][64];
   const int z = blockIdx.y;
   if (z >= *a.n_groups) return;
   const int count = min(a.grp_count[z], kSlabMaxRowsE);
   const int off = a.grp_offset[z];
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * (TWO ? 32 : 16);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   const int N = a.N, K = a.K;
-  const uint16_t* W = a.W + (size_t)a.grp_expert[z] * (size_t)a.w_stride;
+  // the expert's MFMA-native copy (Wn: [rows / 16][K / 8][16] pieces of 8
+  // weights, a fragment's 16 rows one 256-byte run, a wave's K step one 1 KiB
+  // run)
+  const uint16_t* W = static_cast<const uint16_t*>(a.Wn) + (size_t)a.grp_expert[z] * (size_t)a.w_stride;
   const __amdgpu_buffer_rsrc_t wr = rsrc(W, (PAIR ? 2 : 1) * N * K * 2);
-  // this lane's weight row (and up row) and A row at column fk; rows past
-  // the ends read zero
-  const unsigned wofs = n0 + fr < N ? (unsigned)((n0 + fr) * K + fk) * 2u : 0x7ffffff0u;
-  const unsigned uofs = n0 + fr < N ? (unsigned)((N + n0 + fr) * K + fk) * 2u : 0x7ffffff0u;
+  // this lane's piece of its weight row (and up row) and its A row at column
+  // fk; rows past the ends read zero
+  auto piece = [&](int n) { return (unsigned)((((n >> 4) * (K >> 3) + (fk >> 3)) * 16 + (n & 15)) * 16); };
+  const unsigned wofs = n0 + fr < N ? piece(n0 + fr) : 0x7ffffff0u;
+  const unsigned uofs = PAIR ? (n0 + fr < N ? piece(N + n0 + fr) : 0x7ffffff0u)
+                             : (n0 + 16 + fr < N ? piece(n0 + 16 + fr) : 0x7ffffff0u);
   const int arow = fr < count ? (a.a_rows ? a.a_rows[off + fr] : off + fr) : -1;
   const __amdgpu_buffer_rsrc_t ar = rsrc(a.A + (size_t)(arow < 0 ? 0 : arow) * a.lda, arow < 0 ? 0 : K * 2);
   const unsigned aofs = (unsigned)fk * 2u;
@@ -292,46 +301,48 @@ __global__ __launch_bounds__(kSlabThreads) void expert_slab_kernel(PrefillGemmAr
   const int mine = steps > wave ? (steps - wave + kSlabWavesE - 1) / kSlabWavesE : 0;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
   for (int j0 = 0; j0 < mine; j0 += kSlabBatchE) {
-    u32x4 w[kSlabBatchE], u[PAIR ? kSlabBatchE : 1], x[kSlabBatchE];
+    u32x4 w[kSlabBatchE], u[U ? kSlabBatchE : 1], x[kSlabBatchE];
 #pragma unroll
     for (int i = 0; i < kSlabBatchE; ++i) {
       const bool live = j0 + i < mine;
-      const unsigned k0b = (unsigned)(32 * (wave + kSlabWavesE * (j0 + i))) * 2u;  // bytes
-      w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, live ? wofs + k0b : 0x7ffffff0u, 0, 2);
-      if constexpr (PAIR) u[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, live ? uofs + k0b : 0x7ffffff0u, 0, 2);
+      const int st = wave + kSlabWavesE * (j0 + i);
+      const unsigned k0b = (unsigned)(32 * st) * 2u;  // bytes along an A row
+      const unsigned k0w = (unsigned)st * 4u * 256u;  // four k groups of 16 pieces in the native copy
+      w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, live ? wofs + k0w : 0x7ffffff0u, 0, 2);
+      if constexpr (U) u[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, live ? uofs + k0w : 0x7ffffff0u, 0, 2);
       x[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, live ? aofs + k0b : 0x7ffffff0u, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < kSlabBatchE; ++i) {
       const bf16x8 xa = __builtin_bit_cast(bf16x8, x[i]);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(bf16x8, w[i]), acc, 0, 0, 0);
-      if constexpr (PAIR)
+      if constexpr (U)
         accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(bf16x8, u[i]), accu, 0, 0, 0);
     }
   }
   red[0][wave][lane] = acc;
-  if constexpr (PAIR) red[1][wave][lane] = accu;
+  if constexpr (U) red[1][wave][lane] = accu;
   __syncthreads();
   if (wave != 0) return;
   // D layout: lane holds rows 4 (lane / 16) + r, output lane % 16
-  f32x4 g = red[0][0][lane], up = PAIR ? red[1][0][lane] : f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 g = red[0][0][lane], up = U ? red[1][0][lane] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 1; w < kSlabWavesE; ++w) {
     g += red[0][w][lane];
-    if constexpr (PAIR) up += red[1][w][lane];
+    if constexpr (U) up += red[1][w][lane];
   }
   const int n = n0 + fr;
-  if (n >= N) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int i = 4 * (lane >> 4) + r;
     if (i >= count) continue;
-    uint32_t yv;
-    if constexpr (PAIR)
-      yv = f32_to_bf16(silu_mul(round_bf16(g[r]), round_bf16(up[r])));
-    else
-      yv = f32_to_bf16(g[r]);
-    a.Y[(size_t)(off + i) * a.ldy + n] = (uint16_t)yv;
+    uint16_t* y = a.Y + (size_t)(off + i) * a.ldy;
+    if constexpr (PAIR) {
+      if (n < N) y[n] = (uint16_t)f32_to_bf16(silu_mul(round_bf16(g[r]), round_bf16(up[r])));
+    } else {
+      if (n < N) y[n] = (uint16_t)f32_to_bf16(g[r]);
+      if (TWO && n + 16 < N) y[n + 16] = (uint16_t)f32_to_bf16(up[r]);
+    }
   }
 }
 
@@ -346,6 +357,8 @@ struct hk_moe {
   const uint16_t* router = nullptr;
   const uint16_t* gate_up = nullptr;
   const uint16_t* down = nullptr;
+  uint16_t* gate_up_n = nullptr;  // MFMA-native copies of every expert (expert_slab_kernel)
+  uint16_t* down_n = nullptr;
   float* logits = nullptr;       // [max_tokens * experts] router outputs
   int32_t* ids = nullptr;        // [max_tokens * top_k]
   float* weights = nullptr;      // [max_tokens * top_k]
@@ -362,7 +375,7 @@ struct hk_moe {
 namespace {
 
 void moe_free(hk_moe* m) {
-  void* bufs[] = {m->logits, m->ids, m->weights, m->grp_expert, m->grp_count, m->grp_offset, m->n_groups,
+  void* bufs[] = {m->gate_up_n, m->down_n, m->logits, m->ids, m->weights, m->grp_expert, m->grp_count, m->grp_offset, m->n_groups,
                   m->a_rows, m->pair_slot, m->act, m->out};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
@@ -387,6 +400,7 @@ int moe_run(hk_moe* m, const uint16_t* x, int T, const int32_t* ids, const float
   gu.A = x;
   gu.lda = d.hidden;
   gu.W = m->gate_up;
+  gu.Wn = m->gate_up_n;
   gu.w_stride = (long long)2 * d.intermediate * d.hidden;
   gu.Y = m->act;
   gu.ldy = d.intermediate;
@@ -403,18 +417,21 @@ int moe_run(hk_moe* m, const uint16_t* x, int T, const int32_t* ids, const float
   gu.max_rows = T;
   // at most 16 rows per group: the expert slabs (every group's rows in one
   // MFMA block); more: the grouped tile GEMM
-  const bool slab = max_rows <= kSlabMaxRowsE && d.hidden % 32 == 0 && d.intermediate % 32 == 0;
+  const bool slab = max_rows <= kSlabMaxRowsE;  // (hidden and intermediate are multiples of 32)
   if (slab) {
     hipLaunchKernelGGL(expert_slab_kernel<true>, dim3((d.intermediate + 15) / 16, max_groups), dim3(kSlabThreads),
                        0, st, gu);
     MOE_CHECK(hipGetLastError());
   } else {
-    MOE_TRY(launch_prefill_gemm(gu, st));
+    PrefillGemmArgs g = gu;
+    g.Wn = nullptr;  // (the tile GEMM reads the row-major weights)
+    MOE_TRY(launch_prefill_gemm(g, st));
   }
   PrefillGemmArgs dn = gu;
   dn.A = m->act;
   dn.lda = d.intermediate;
   dn.W = m->down;
+  dn.Wn = m->down_n;
   dn.w_stride = (long long)d.hidden * d.intermediate;
   dn.Y = m->out;
   dn.ldy = d.hidden;
@@ -423,11 +440,13 @@ int moe_run(hk_moe* m, const uint16_t* x, int T, const int32_t* ids, const float
   dn.epi = EPI_BF16;
   dn.a_rows = nullptr;
   if (slab) {
-    hipLaunchKernelGGL(expert_slab_kernel<false>, dim3((d.hidden + 15) / 16, max_groups), dim3(kSlabThreads), 0,
-                       st, dn);
+    hipLaunchKernelGGL((expert_slab_kernel<false, true>), dim3((d.hidden + 31) / 32, max_groups),
+                       dim3(kSlabThreads), 0, st, dn);
     MOE_CHECK(hipGetLastError());
   } else {
-    MOE_TRY(launch_prefill_gemm(dn, st));
+    PrefillGemmArgs g = dn;
+    g.Wn = nullptr;
+    MOE_TRY(launch_prefill_gemm(g, st));
   }
   hipLaunchKernelGGL(combine_kernel, dim3(T, (d.hidden + kThreads - 1) / kThreads), dim3(kThreads), 0, st, m->out,
                      m->pair_slot, weights, d.hidden, K, S, y);
@@ -464,6 +483,16 @@ int hk_moe_create(const hk_moe_desc* desc, const uint16_t* router, const uint16_
   const size_t pairs = (size_t)d.max_tokens * (d.top_k + d.shared);
   const size_t groups = (size_t)d.experts + d.shared;
   auto body = [&]() -> int {
+    // the MFMA-native copies, one repack per expert matrix
+    const size_t gu_n = (size_t)2 * d.intermediate * d.hidden, dn_n = (size_t)d.hidden * d.intermediate;
+    MOE_TRY(moe_alloc(&m->gate_up_n, groups * gu_n));
+    MOE_TRY(moe_alloc(&m->down_n, groups * dn_n));
+    for (size_t e = 0; e < groups; ++e) {
+      MOE_TRY(launch_repack_mfma(gate_up + e * gu_n, m->gate_up_n + e * gu_n, 2 * d.intermediate, d.hidden, 2, 0,
+                                 nullptr));
+      MOE_TRY(launch_repack_mfma(down + e * dn_n, m->down_n + e * dn_n, d.hidden, d.intermediate, 2, 0, nullptr));
+    }
+    MOE_CHECK(hipStreamSynchronize(nullptr));
     MOE_TRY(moe_alloc(&m->logits, (size_t)d.max_tokens * d.experts));
     MOE_TRY(moe_alloc(&m->ids, (size_t)d.max_tokens * d.top_k));
     MOE_TRY(moe_alloc(&m->weights, (size_t)d.max_tokens * d.top_k));

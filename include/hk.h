@@ -284,6 +284,9 @@ typedef struct hk_moe_desc {
   int32_t max_tokens;   /* largest batch, at most 256 */
 } hk_moe_desc;
 
+/* The block also makes an MFMA-native copy of every expert's gate/up and down
+ * weights (the same size again, owned by the block, freed by hk_moe_destroy);
+ * the caller's weights must stay unchanged while the block is used. */
 int hk_moe_create(const hk_moe_desc* desc, const uint16_t* router, const uint16_t* gate_up,
                   const uint16_t* down, hk_moe** out);
 
