@@ -139,16 +139,27 @@ __device__ __forceinline__ void topk_wave(const float* logits, int t, int E, int
 // consecutive slots), and shared expert s's slots (one per token) by thread
 // E + s.  Within an expert the slots follow token order, so the plan does not
 // depend on timing.
+// `tokens` (distinct: every token names an expert at most once, T <= 64):
+// routed expert e's tokens as a bit mask, and pair (t, k)'s slot is e's
+// offset plus the number of e's tokens before t, all pairs at once.
 __device__ void plan_pairs(const int32_t* ids, int T, int K, int E, int S, int nt, int* counts, int* offs,
-                           int32_t* grp_expert, int32_t* grp_count, int32_t* grp_offset, int32_t* n_groups,
-                           int32_t* a_rows, int32_t* pair_slot) {
+                           unsigned long long* tokens, bool distinct, int32_t* grp_expert, int32_t* grp_count,
+                           int32_t* grp_offset, int32_t* n_groups, int32_t* a_rows, int32_t* pair_slot) {
   static_assert(kMaxRouted <= 64, "one lane per routed expert");
   const int tid = threadIdx.x;
   const int total = E + S, per = K + S;
   auto clamp = [&](int e) { return e < 0 ? 0 : (e >= E ? E - 1 : e); };
-  for (int e = tid; e < E; e += nt) counts[e] = 0;
+  distinct = distinct && T <= 64;
+  for (int e = tid; e < E; e += nt) {
+    counts[e] = 0;
+    tokens[e] = 0ull;
+  }
   __syncthreads();
-  for (int i = tid; i < T * K; i += nt) atomicAdd(&counts[clamp(ids[i])], 1);
+  for (int i = tid; i < T * K; i += nt) {
+    const int e = clamp(ids[i]);
+    atomicAdd(&counts[e], 1);
+    if (distinct) atomicOr(&tokens[e], 1ull << (i / K));
+  }
   __syncthreads();
   if (tid < 64) {
     const int lane = tid;
@@ -179,6 +190,21 @@ __device__ void plan_pairs(const int32_t* ids, int T, int K, int E, int S, int n
     if (lane == 0) *n_groups = nr + S;
   }
   __syncthreads();
+  if (distinct) {
+    for (int i = tid; i < T * (K + S); i += nt) {
+      const int t = i / per, k = i % per;
+      int slot;
+      if (k < K) {
+        const int e = clamp(ids[t * K + k]);
+        slot = offs[e] + __popcll(tokens[e] & ((1ull << t) - 1ull));
+      } else {
+        slot = offs[E + k - K] + t;
+      }
+      a_rows[slot] = t;
+      pair_slot[t * per + k] = slot;
+    }
+    return;
+  }
   for (int e = tid; e < total; e += nt) {
     int slot = offs[e];
     if (e < E) {
@@ -207,11 +233,13 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_kernel(const float* lo
   __shared__ int32_t sids[kMaxTokens * kMaxTopK];
   __shared__ int counts[kMaxRouted + kMaxShared];
   __shared__ int offs[kMaxRouted + kMaxShared];
+  __shared__ unsigned long long tokens[kMaxRouted];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int t = wave; t < T; t += kPlanThreads / 64) topk_wave(logits, t, E, K, lane, ids, weights, sids);
   __syncthreads();
-  plan_pairs(sids, T, K, E, S, kPlanThreads, counts, offs, grp_expert, grp_count, grp_offset, n_groups, a_rows,
-             pair_slot);
+  // (the top-k of a token names each expert once)
+  plan_pairs(sids, T, K, E, S, kPlanThreads, counts, offs, tokens, true, grp_expert, grp_count, grp_offset,
+             n_groups, a_rows, pair_slot);
 }
 
 // The plan for caller-supplied ids (hk_moe_experts): the ids are copied to
@@ -223,10 +251,12 @@ __global__ __launch_bounds__(kThreads) void route_plan_kernel(const int32_t* ids
   __shared__ int32_t sids[kMaxTokens * kMaxTopK];
   __shared__ int counts[kMaxRouted + kMaxShared];
   __shared__ int offs[kMaxRouted + kMaxShared];
+  __shared__ unsigned long long tokens[kMaxRouted];
   for (int i = threadIdx.x; i < T * K; i += kThreads) sids[i] = ids[i];
   __syncthreads();
-  plan_pairs(sids, T, K, E, S, kThreads, counts, offs, grp_expert, grp_count, grp_offset, n_groups, a_rows,
-             pair_slot);
+  // (caller ids may name an expert twice for one token: the serial slots)
+  plan_pairs(sids, T, K, E, S, kThreads, counts, offs, tokens, false, grp_expert, grp_count, grp_offset, n_groups,
+             a_rows, pair_slot);
 }
 
 // y[t][d] = bf16(sum_k p_k e_k[d] + sum_s e_s[d]) in float32, ranks in order;
