@@ -174,21 +174,21 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
 // to matter).  A P @ V product summed over the three terms with bf16 V
 // gives float32 P @ V, up to the float32 summation order.
 __device__ __forceinline__ void split3_bf16(const float (&p)[8], u32x4& hi, u32x4& mid, u32x4& lo) {
-  uint32_t t[8][3];
+  // the remainders are exact (Sterbenz), and the last one has at most 8
+  // significant bits, so its float32 encoding ends in 16 zero bits: every
+  // term is the top half of a float32 word, picked in pairs by v_perm_b32
+  float r[8], q[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const uint32_t a = __float_as_uint(p[e]) & 0xffff0000u;
-    const float r = p[e] - __uint_as_float(a);
-    const uint32_t b = __float_as_uint(r) & 0xffff0000u;
-    t[e][0] = a;
-    t[e][1] = b;
-    t[e][2] = __float_as_uint(r - __uint_as_float(b)) & 0xffff0000u;
+    r[e] = p[e] - __uint_as_float(__float_as_uint(p[e]) & 0xffff0000u);
+    q[e] = r[e] - __uint_as_float(__float_as_uint(r[e]) & 0xffff0000u);
   }
+  constexpr uint32_t kTops = 0x07060302u;  // bytes 2, 3 of the second operand, then of the first
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    hi[w] = (t[2 * w][0] >> 16) | t[2 * w + 1][0];
-    mid[w] = (t[2 * w][1] >> 16) | t[2 * w + 1][1];
-    lo[w] = (t[2 * w][2] >> 16) | t[2 * w + 1][2];
+    hi[w] = __builtin_amdgcn_perm(__float_as_uint(p[2 * w + 1]), __float_as_uint(p[2 * w]), kTops);
+    mid[w] = __builtin_amdgcn_perm(__float_as_uint(r[2 * w + 1]), __float_as_uint(r[2 * w]), kTops);
+    lo[w] = __builtin_amdgcn_perm(__float_as_uint(q[2 * w + 1]), __float_as_uint(q[2 * w]), kTops);
   }
 }
 

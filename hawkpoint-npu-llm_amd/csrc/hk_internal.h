@@ -294,6 +294,7 @@ struct PrefillAttnArgs {
   int out_kblock;           // nonzero: out k-blocked with n rows (see PrefillGemmArgs::kblock)
   int rope_done;            // nonzero: qrot and the caches are written already (the QKV GEMM's RoPE)
   int n, start, q_heads, kv_heads, max_ctx;
+  int period;               // set by launch_prefill_attention: the CU count
 };
 
 // rope_append (unless rope_done) then causal attention for tokens start..start+n-1.

@@ -1243,36 +1243,78 @@ int split_parts(int M, int N, int K) {
 // P[token L % 16][slots 16 sb + 4 (L / 16) + r], which serves directly as the
 // B operand of P @ V once the MFMA's k index is read as the matching slot;
 // V^T is staged in LDS so that the A values (4 consecutive slots of one
-// dimension) are 8-byte reads.  Wave w owns tokens 16 w .. 16 w + 15 of the
-// block; all four share the K and V tiles.
+// dimension) are 8-byte reads.  A workgroup runs ST streams of four waves;
+// stream s takes KV blocks s, s + ST, ... with its own K and V tiles, and
+// wave w of each stream owns tokens 16 w .. 16 w + 15 of the block.  The
+// streams' running (max, sum, O) are folded in stream order at the end, so
+// a long query block's serial chain is 1 / ST of its blocks.
 constexpr int kFaRows = 64;                 // query tokens per workgroup
 constexpr int kFaSlots = 128;               // KV slots per block
-constexpr int kFaKRow = kHeadDim + 8;       // bf16 per K row in LDS (padding)
+// LDS row pitches (bf16): a K row 36 dwords, so the eight 16-byte fragment
+// reads of one LDS pass (rows 4 banks apart) cover all 32 banks once; a V
+// row 40 dwords, so the four rows of 32 bytes that a pass of transposed
+// 8-byte reads touches lie 8 banks apart (at 36 dwords they overlapped in
+// pairs of banks, and the V reads took two passes each)
+constexpr int kFaKRow = kHeadDim + 8;
+constexpr int kFaVRow = kHeadDim + 16;
+constexpr int kFaStreams = 2;               // KV streams per workgroup for 128-slot blocks
 // exp(s / 8 - m) = exp2(s * log2(e) / 8 - m'): the scores are kept in base-2
 // units so that each exponential is one v_exp_f32
 constexpr float kFaScale = 0.125f * 1.4426950408889634f;
 
+// The maximum and the sum over lanes L, L ^ 16, L ^ 32, L ^ 48 (a token's
+// four lane groups), the same value in each of the four: permlane32_swap of
+// two copies leaves lanes L and L ^ 32 in the two results, permlane16_swap
+// then lanes L and L ^ 16 (VALU lane swaps, where a shuffle goes through the
+// LDS).  The sum is (v_L + v_L^32) + (v_L^16 + v_L^48) in every lane.
+__device__ __forceinline__ float quad_max(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // KS: KV slots per block, kFaSlots, or 64 when the whole context fits 64
 // slots (a short prompt from slot 0: half the products of a 128-slot block,
 // whose second half is masked; the masked slots add exact zeros, so both
-// forms give the same result).
-template <int KS>
-__global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttnArgs a) {
+// forms give the same result).  With up to 128 VGPRs (four waves per SIMD
+// for ST > 1, at least two for ST = 1) the compiler keeps the MFMA sums in
+// VGPRs; in AGPRs every score and every rescale of O cost extra moves.
+template <int KS, int ST>
+__global__ __launch_bounds__(kThreads * ST, ST == 1 ? 2 : 4) void attention_prefill_kernel(PrefillAttnArgs a) {
   constexpr int kSB = KS / 16;  // 16-slot S^T blocks per KV block
   static_assert(KS == 64 || KS == kFaSlots, "64 or kFaSlots slots per block");
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[KS][kFaKRow];  // [slot][dim]
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[KS][kFaKRow];  // [slot][dim]
-  const int h = blockIdx.x;
-  const int nblk = (a.n + kFaRows - 1) / kFaRows;
-  const int qb = nblk - 1 - (int)blockIdx.y;  // the longest blocks start first
+  static_assert(kThreads == 256, "a stream is four waves");
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[ST][KS][kFaKRow];  // [stream][slot][dim]
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[ST][KS][kFaVRow];  // [stream][slot][dim]
+  // Tasks (head, query block) ranked longest first (rank r: block
+  // nblk - 1 - r / q_heads of head r % q_heads), dealt to the workgroup ids
+  // in a snake over runs of `period` ids (the CU count): the ids a CU
+  // receives are about `period` apart, so each CU's long and short tasks
+  // add up to about the same work.
+  const int nblk = (a.n + kFaRows - 1) / kFaRows, tasks = nblk * a.q_heads;
+  const int run = (int)blockIdx.x / a.period, pos = (int)blockIdx.x % a.period;
+  const int run_len = min(a.period, tasks - run * a.period);
+  const int rank = run * a.period + ((run & 1) ? run_len - 1 - pos : pos);
+  const int h = rank % a.q_heads;
+  const int qb = nblk - 1 - rank / a.q_heads;
   const int g = h / (a.q_heads / a.kv_heads);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int stream = wave >> 2, sw = wave & 3, stid = tid & (kThreads - 1);
   const int col = lane & 15, quad = lane >> 4;
-  const int tok = qb * kFaRows + wave * 16 + col;  // this lane's token
+  const int tok = qb * kFaRows + sw * 16 + col;  // this lane's token
   const bool tok_ok = tok < a.n;
   const int p = a.start + (tok_ok ? tok : 0);
   const int last_slot = a.start + min(qb * kFaRows + kFaRows - 1, a.n - 1);
   const int nkv = last_slot / KS + 1;
+  const int iters = (nkv + ST - 1) / ST;  // rounds of ST blocks
   const size_t kv_base = (size_t)g * a.max_ctx;
   const u32x4 zero = {0u, 0u, 0u, 0u};
 
@@ -1285,20 +1327,23 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
   }
 
   // tile loads through buffer resources that end at the block's last slot,
-  // so later slots read as zero with no branch: thread t takes slot t / 2,
-  // dimensions 32 (t % 2) .. + 32, of K and of V (both stay [slot][dim] in
-  // LDS; the P @ V products read V transposed with ds_read_b64_tr_b16)
-  const int ls = tid >> 1, ld0 = (tid & 1) * 32;
+  // so later slots (and the blocks past the last of a stream's final round)
+  // read as zero with no branch: load i of thread t of a stream takes slot
+  // t / 8 + 32 i, dimensions 8 (t % 8) .. + 8, of K and of V (eight lanes per
+  // 128-byte row, a wave's load one 1 KiB run; both stay [slot][dim] in LDS,
+  // and the P @ V products read V transposed with ds_read_b64_tr_b16)
+  const int ls = stid >> 3, ld0 = (stid & 7) * 8;
   const __amdgpu_buffer_rsrc_t kres = rsrc(a.kcache + kv_base * kHeadDim, (last_slot + 1) * kHeadDim * 2);
   const __amdgpu_buffer_rsrc_t vres = rsrc(a.vcache + kv_base * kHeadDim, (last_slot + 1) * kHeadDim * 2);
-  u32x4 kr[4], vr[4];
+  constexpr int kLoads = KS / 32;  // loads per thread and matrix
+  u32x4 kr[kLoads], vr[kLoads];
   auto load_tile = [&](int kb) {
-    // (threads 2 KS .. hold no slot of a 64-slot block: their offsets lie past the resources)
-    const unsigned off = ls < KS ? (unsigned)((kb * KS + ls) * kHeadDim + ld0) * 2u : 0x7ffffff0u;
+    // (a block past the last has no slot: its offsets lie past the resources)
+    const unsigned off = kb < nkv ? (unsigned)((kb * KS + ls) * kHeadDim + ld0) * 2u : 0x7ffffff0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 16 * i, 0);
-      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 16 * i, 0);
+    for (int i = 0; i < kLoads; ++i) {
+      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 32 * kHeadDim * 2 * i, 0);
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 32 * kHeadDim * 2 * i, 0);
     }
   };
 
@@ -1306,18 +1351,18 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
   f32x4 o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  load_tile(0);
-  for (int kb = 0; kb < nkv; ++kb) {
-    __syncthreads();  // the previous tile has been read
-    if (ls < KS) {
+  load_tile(stream);
+  for (int it = 0; it < iters; ++it) {
+    const int kb = it * ST + stream;
+    __syncthreads();  // the previous tiles have been read
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<u32x4*>(&Ks[ls][ld0 + 8 * i]) = kr[i];
-        *reinterpret_cast<u32x4*>(&Vs[ls][ld0 + 8 * i]) = vr[i];
-      }
+    for (int i = 0; i < kLoads; ++i) {
+      *reinterpret_cast<u32x4*>(&Ks[stream][ls + 32 * i][ld0]) = kr[i];
+      *reinterpret_cast<u32x4*>(&Vs[stream][ls + 32 * i][ld0]) = vr[i];
     }
     __syncthreads();
-    if (kb + 1 < nkv) load_tile(kb + 1);  // in flight during this tile's math
+    if (it + 1 < iters) load_tile(kb + ST);  // in flight during this tile's math
+    if (kb >= nkv) continue;  // this stream's final round holds no block (uniform per stream)
 
     // S^T blocks: lane holds slots s0 + 16 sb + 4 quad + r of token `tok`
     const int s0 = kb * KS;
@@ -1327,36 +1372,32 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
       sv[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[16 * sb + col][32 * kk + 8 * quad]);
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[stream][16 * sb + col][32 * kk + 8 * quad]);
         sv[sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[kk], sv[sb], 0, 0, 0);
       }
     }
-    float mx = -INFINITY;
     // a block whose slots all precede every token of the workgroup needs no
-    // causal mask (uniform: the block's first token and the last slot)
+    // causal mask (uniform: the block's first token and the last slot);
+    // masked scores become -inf in place
     const bool full = s0 + KS - 1 <= a.start + qb * kFaRows && qb * kFaRows + kFaRows <= a.n;
-    if (full) {
-#pragma unroll
-      for (int sb = 0; sb < kSB; ++sb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sv[sb][r] *= kFaScale;
-          mx = fmaxf(mx, sv[sb][r]);
-        }
-    } else {
+    if (!full) {
 #pragma unroll
       for (int sb = 0; sb < kSB; ++sb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int slot = s0 + 16 * sb + 4 * quad + r;
-          const float v = (tok_ok && slot <= p) ? sv[sb][r] * kFaScale : -INFINITY;
-          sv[sb][r] = v;
-          mx = fmaxf(mx, v);
+          if (!(tok_ok && slot <= p)) sv[sb][r] = -INFINITY;
         }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
+    // the maximum of the unscaled scores, scaled once: rounding is monotonic,
+    // so it is the maximum of the scaled scores
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < kSB; ++sb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[sb][r]);
+    mx = quad_max(mx);
+    const float m_new = fmaxf(m_run, mx * kFaScale);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // a token with no live slot yet
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float rs = 0.0f;
@@ -1364,20 +1405,23 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
     for (int sb = 0; sb < kSB; ++sb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_amdgcn_exp2f(sv[sb][r] - m_use);
+        // scale and shift in one rounding (a masked -inf gives exp2(-inf) = 0)
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[sb][r], kFaScale, -m_use));
         sv[sb][r] = e;
         rs += e;
       }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
-    l_run = l_run * alpha + rs;
+    l_run = l_run * alpha + quad_sum(rs);
     m_run = m_new;
+    // once the running maxima settle, alpha is 1 in every lane and the
+    // rescale (exact then) is skipped
+    if (__any(alpha != 1.0f)) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] *= alpha;
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    }
     // O^T[16 db + 4 quad + r][tok] += sum over the block's slots of V^T P^T,
     // 32 slots per bf16 MFMA: k index 8 quad + e stands for slot
     // 32 t + 16 (e / 4) + 4 quad + e % 4, the 8 P values this lane holds for
-    // blocks 2t, 2t + 1.  P (finite, in [0, 1]) goes in as three bf16 terms
+    // blocks 2t, 2t + 1.  P (finite, non-negative, 1 at most up to exp2 of a rounding) goes in as three bf16 terms
     // (split3_bf16), which together are the float32 P exactly; with two
     // (16 significant bits) about one output in 200 rounded to another bf16
     // value than the float32 P @ V.
@@ -1401,15 +1445,48 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(PrefillAttn
         // 16 db + 4 (c % 4) .. + 3.
         const int rs = 32 * t + 4 * quad + (col >> 2), rd = 16 * db + 4 * (col & 3);
         const v4s16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4s16*)&Vs[rs][rd]);
+            (__attribute__((address_space(3))) v4s16*)&Vs[stream][rs][rd]);
         const v4s16 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4s16*)&Vs[rs + 16][rd]);
+            (__attribute__((address_space(3))) v4s16*)&Vs[stream][rs + 16][rd]);
         const u32x2_t w0 = __builtin_bit_cast(u32x2_t, t0), w1 = __builtin_bit_cast(u32x2_t, t1);
         const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{w0.x, w0.y, w1.x, w1.y});
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo, o[db], 0, 0, 0);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pmid, o[db], 0, 0, 0);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi, o[db], 0, 0, 0);
       }
+    }
+  }
+  if constexpr (ST > 1) {
+    // streams 1.. leave their (max, sum, O) in LDS (over the tiles, which
+    // every stream has finished with), and stream 0 folds them in stream order
+    constexpr int kW = 18;  // floats per lane: m, l, O
+    static_assert((ST - 1) * 4 * 64 * kW * 4 <= (int)sizeof(Ks), "the exchange fits the K tiles");
+    float* xs = reinterpret_cast<float*>(&Ks[0][0][0]);
+    __syncthreads();
+    if (stream > 0) {
+      float* d = xs + (((stream - 1) * 4 + sw) * 64 + lane) * kW;
+      d[0] = m_run;
+      d[1] = l_run;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) d[2 + 4 * db + r] = o[db][r];
+    }
+    __syncthreads();
+    if (stream > 0) return;
+#pragma unroll
+    for (int q = 1; q < ST; ++q) {
+      const float* d = xs + (((q - 1) * 4 + sw) * 64 + lane) * kW;
+      const float mq = d[0];
+      const float m_new = fmaxf(m_run, mq);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float a0 = __builtin_amdgcn_exp2f(m_run - m_use), a1 = __builtin_amdgcn_exp2f(mq - m_use);
+      l_run = l_run * a0 + d[1] * a1;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[db][r] = o[db][r] * a0 + d[2 + 4 * db + r] * a1;
+      m_run = m_new;
     }
   }
   if (!tok_ok) return;
@@ -1655,11 +1732,14 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream) {
     err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(err, "rope append launch");
   }
-  const dim3 grid(a.q_heads, (a.n + kFaRows - 1) / kFaRows);
+  PrefillAttnArgs b = a;
+  b.period = cu_count();
+  const dim3 grid(a.q_heads * ((a.n + kFaRows - 1) / kFaRows));
   if (a.start + a.n <= 64)
-    hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attention_prefill_kernel<64, 1>), grid, dim3(kThreads), 0, stream, b);
   else
-    hipLaunchKernelGGL(attention_prefill_kernel<kFaSlots>, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((attention_prefill_kernel<kFaSlots, kFaStreams>), grid, dim3(kThreads * kFaStreams), 0,
+                       stream, b);
   err = hipGetLastError();
   return err == hipSuccess ? 0 : hip_fail(err, "prefill attention launch");
 }
