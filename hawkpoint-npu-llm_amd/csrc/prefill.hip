@@ -502,25 +502,34 @@ __global__ __launch_bounds__(kThreads) void gemm_big_kernel(PrefillGemmArgs a) {
   tile_epilogue<BM, BN, PAIR, W8, MB, NB>(a, acc, accu, &As[0][0][0], m0, n0, wm, wn, tid, lane);
 }
 
-// Large-M GEMM, bf16 weights, with a ring of NS LDS stages of 32 K each
-// filled by buffer -> LDS loads (16 bytes per lane, 1 KiB per instruction):
-// the workgroup keeps NS - 1 stages of loads in flight while it multiplies
-// one, where gemm_big_kernel's register staging keeps one.  Tiles, waves and
-// epilogue as gemm_big_kernel (128 tokens x BN outputs, 2 x 2 waves).
-// A stage row is 32 bf16 = four 16-byte pieces; piece c of tile row r sits at
-// position c ^ ring_swizzle(r), so that a fragment read (16 rows, one piece)
-// touches distinct banks in every group of 8 lanes (128 bytes) and of 16
-// lanes (256 bytes).  Every load goes through a buffer resource: rows
-// past M (tokens) or N (outputs) read zero.  Wave w's loads cover A rows
-// 16 (w AI + i) .. and weight rows 16 (w WI + i) ..; each wave waits for its
-// own loads of a stage, the barrier after that for everyone's.
-constexpr int kRK = 32;  // K per ring stage
+// Large-M GEMM, bf16 weights, with a ring of NS LDS stages of RK (32 or 64)
+// K each filled by buffer -> LDS loads (16 bytes per lane, 1 KiB per
+// instruction): the workgroup keeps NS - 1 stages of loads in flight while
+// it multiplies one, where gemm_big_kernel's register staging keeps one.
+// Tiles, waves and epilogue as gemm_big_kernel (128 tokens x BN outputs,
+// 2 x 2 waves).  A stage row is RK bf16 = RK / 8 16-byte pieces; piece c of
+// tile row r sits at position c ^ ring_key<RK>(r), so that a fragment read
+// (16 rows, one piece) touches distinct banks in every group of 8 lanes
+// (128 bytes) and of 16 lanes (256 bytes).  Every load goes through a buffer
+// resource: rows past M (tokens) or N (outputs) read zero.  Load i of wave w
+// covers A rows RPL (w AI + i) .. and weight rows RPL (w WI + i) .. (RPL =
+// 512 / RK rows per load); each wave waits for its own loads of a stage, the
+// barrier after that for everyone's.
+constexpr int kRK = 32;  // K per ring stage of the SwiGLU pair and of the narrower tiles
 
-// The ring's piece position key of tile row r (only r % 16 matters):
-// 0 0 1 1 2 2 3 3 1 1 0 0 3 3 2 2.  Rows r and r + 2 (64 bytes x 2 apart,
-// the same 128-byte bank window) get different keys, and so do rows r and r
-// + 4, r + 8, r + 12 (the same 256-byte window).
+// The ring's piece position key of tile row r (only r % 16 matters).  32-deep
+// stages (four pieces per 64-byte row): 0 0 1 1 2 2 3 3 1 1 0 0 3 3 2 2, so
+// rows r and r + 2 (the same 128-byte bank window) get different keys, and
+// so do rows r and r + 4, r + 8, r + 12 (the same 256-byte window).  64-deep
+// stages (eight pieces per 128-byte row): (r mod 8) ^ (r / 8 mod 2), so rows
+// r .. r + 7 (one row per 128-byte window) get eight keys, and so do the
+// eight rows of each parity among 16 (the 256-byte window holds two rows).
 __device__ __forceinline__ int ring_swizzle(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+template <int RK>
+__device__ __forceinline__ int ring_key(int r) {
+  static_assert(RK == 32 || RK == 64, "32- or 64-deep stages");
+  return RK == 32 ? ring_swizzle(r) : (r & 7) ^ ((r >> 3) & 1);
+}
 
 // 16 bytes from LDS, issued as assembly: the caller waits (lgkmcnt) before
 // it uses the value, then passes it through lds_ready.  (The VGPR operand
@@ -543,7 +552,7 @@ __device__ __forceinline__ void ring_loads(__amdgpu_buffer_rsrc_t r, uint16_t* d
                                            unsigned kb) {
 #pragma unroll
   for (int i = 0; i < n; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst + 16 * kRK * i), 16,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16,
                                              off[i] + kb, 0, 0, 0);
 }
 
@@ -555,15 +564,17 @@ __device__ __forceinline__ void lds_ready(bf16x8& v) {
 #endif
 }
 
-template <int BN, bool PAIR, int NS>
+template <int BN, bool PAIR, int NS, int RK = kRK>
 __global__ __launch_bounds__(kThreads, PAIR && BN == 128 ? 2 : 1) void gemm_ring_kernel(PrefillGemmArgs a) {
   constexpr int BM = kBM;
   constexpr int WR = PAIR ? 2 * BN : BN;  // weight rows per tile
   constexpr int MB = BM / 64, NB = BN / 64;  // MFMA 32 x 32 blocks per wave (64 x BN / 2 outputs)
-  constexpr int SA = BM * kRK, SW = WR * kRK;  // bf16 per stage
-  constexpr int AI = BM / 16 / (kThreads / 64), WI = WR / 16 / (kThreads / 64);
+  constexpr int SA = BM * RK, SW = WR * RK;  // bf16 per stage
+  constexpr int RPL = 512 / RK, PPR = RK / 8;  // rows per load, pieces per row
+  constexpr int AI = BM / RPL / (kThreads / 64), WI = WR / RPL / (kThreads / 64);
+  constexpr int NH = RK / 16;  // 16-deep MFMA steps per stage
   constexpr int PER = AI + WI;  // loads per wave per stage
-  static_assert(AI >= 1 && WI >= 1 && NS >= 3, "ring shape");
+  static_assert(AI >= 1 && WI >= 1 && NS >= 3 && (NS - 2) * (AI + WI) < 64, "ring shape");
   static_assert(BM * (BN + 8) <= NS * (SA + SW), "the epilogue tile fits the ring");
   __shared__ __attribute__((aligned(16))) uint16_t ring[NS][SA + SW];
 
@@ -581,21 +592,24 @@ __global__ __launch_bounds__(kThreads, PAIR && BN == 128 ? 2 : 1) void gemm_ring
   const int n0 = (grp * GN + in % gn) * BN;
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
   const int fr = lane & 31;
-  const int steps = a.K / kRK;
+  const int steps = a.K / RK;
 
   const __amdgpu_buffer_rsrc_t ra = rsrc(a.A, a.M * a.lda * 2);
   const __amdgpu_buffer_rsrc_t rw = rsrc(a.W, (PAIR ? 2 : 1) * a.N * a.K * 2);
-  // this lane's row within a 16-row load block and the global piece it
-  // fetches (its LDS position is lane & 3)
-  const int lr = lane >> 2, lg = (lane & 3) ^ ring_swizzle(lr);
+  // this lane's row within an RPL-row load block and the global piece it
+  // fetches into its LDS position lane % PPR
+  const int lr = lane / PPR, lp = lane % PPR;
   unsigned aoff[AI], woff[WI];
 #pragma unroll
-  for (int i = 0; i < AI; ++i) aoff[i] = (unsigned)(((m0 + 16 * (wave * AI + i) + lr) * a.lda + 8 * lg) * 2);
+  for (int i = 0; i < AI; ++i) {
+    const int r = RPL * (wave * AI + i) + lr;  // tile row
+    aoff[i] = (unsigned)(((m0 + r) * a.lda + 8 * (lp ^ ring_key<RK>(r))) * 2);
+  }
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
-    const int r = 16 * (wave * WI + i) + lr;  // tile row: gate rows first, then up rows
+    const int r = RPL * (wave * WI + i) + lr;  // tile row: gate rows first, then up rows
     const int row = PAIR ? (r < BN ? n0 + r : a.N + n0 + r - BN) : n0 + r;
-    woff[i] = (unsigned)((row * a.K + 8 * lg) * 2);
+    woff[i] = (unsigned)((row * a.K + 8 * (lp ^ ring_key<RK>(r))) * 2);
   }
   f32x16 acc[MB][NB], accu[PAIR ? MB : 1][PAIR ? NB : 1];
 #pragma unroll
@@ -610,14 +624,15 @@ __global__ __launch_bounds__(kThreads, PAIR && BN == 128 ? 2 : 1) void gemm_ring
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
     if (st < steps) {
-      ring_loads<AI>(ra, &ring[st][16 * wave * AI * kRK], aoff, (unsigned)(st * kRK * 2));
-      ring_loads<WI>(rw, &ring[st][SA + 16 * wave * WI * kRK], woff, (unsigned)(st * kRK * 2));
+      ring_loads<AI>(ra, &ring[st][512 * wave * AI], aoff, (unsigned)(st * RK * 2));
+      ring_loads<WI>(rw, &ring[st][SA + 512 * wave * WI], woff, (unsigned)(st * RK * 2));
     }
-  // MFMA 32 x 32 x 16: this lane's fragment piece in each 16-deep half h of
+  // MFMA 32 x 32 x 16: this lane's fragment piece in each 16-deep step h of
   // the stage (k 16 h + 8 (lane / 32) ..) at its swizzled position in rows of
   // its fragment (row & 15 = lane & 15)
-  const int pos0 = ((lane >> 5) ^ ring_swizzle(lane & 15)) * 8;
-  const int pos1 = ((2 + (lane >> 5)) ^ ring_swizzle(lane & 15)) * 8;
+  int pos[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) pos[h] = ((2 * h + (lane >> 5)) ^ ring_key<RK>(lane & 15)) * 8;
   for (int k = 0; k < steps; ++k) {
     // stage k has landed once at most NS - 2 later stages are in flight
     if (k + NS - 2 < steps)
@@ -632,27 +647,26 @@ __global__ __launch_bounds__(kThreads, PAIR && BN == 128 ? 2 : 1) void gemm_ring
     // the buffer of stage k - 1 is free: every wave is past its products
     if (k + NS - 1 < steps) {
       const int st = k + NS - 1;
-      ring_loads<AI>(ra, &ring[st % NS][16 * wave * AI * kRK], aoff, (unsigned)(st * kRK * 2));
-      ring_loads<WI>(rw, &ring[st % NS][SA + 16 * wave * WI * kRK], woff, (unsigned)(st * kRK * 2));
+      ring_loads<AI>(ra, &ring[st % NS][512 * wave * AI], aoff, (unsigned)(st * RK * 2));
+      ring_loads<WI>(rw, &ring[st % NS][SA + 512 * wave * WI], woff, (unsigned)(st * RK * 2));
     }
     const uint16_t* as = &ring[k % NS][0];
     const uint16_t* ws = as + SA;
-    bf16x8 af[2][MB], bf[2][NB], uf[2][PAIR ? NB : 1];
+    bf16x8 af[NH][MB], bf[NH][NB], uf[NH][PAIR ? NB : 1];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int pos = h ? pos1 : pos0;
+    for (int h = 0; h < NH; ++h) {
 #pragma unroll
-      for (int i = 0; i < MB; ++i) af[h][i] = lds_read16(as + (wm + 32 * i + fr) * kRK + pos);
+      for (int i = 0; i < MB; ++i) af[h][i] = lds_read16(as + (wm + 32 * i + fr) * RK + pos[h]);
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        bf[h][j] = lds_read16(ws + (wn + 32 * j + fr) * kRK + pos);
-        if constexpr (PAIR) uf[h][j] = lds_read16(ws + (BN + wn + 32 * j + fr) * kRK + pos);
+        bf[h][j] = lds_read16(ws + (wn + 32 * j + fr) * RK + pos[h]);
+        if constexpr (PAIR) uf[h][j] = lds_read16(ws + (BN + wn + 32 * j + fr) * RK + pos[h]);
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // (the products take the fragments from here on: after the wait)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < NH; ++h) {
 #pragma unroll
       for (int i = 0; i < MB; ++i) lds_ready(af[h][i]);
 #pragma unroll
@@ -662,7 +676,7 @@ __global__ __launch_bounds__(kThreads, PAIR && BN == 128 ? 2 : 1) void gemm_ring
       }
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NH; ++h)
 #pragma unroll
       for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -1634,6 +1648,8 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     const dim3 g(8 * ((mt * ((a.N + bnt - 1) / bnt) + 7) / 8));
     if (pair)
       hipLaunchKernelGGL((gemm_ring_kernel<128, true, 3>), g, dim3(kThreads), 0, stream, a);
+    else if (one_per_cu && a.K % 64 == 0)
+      hipLaunchKernelGGL((gemm_ring_kernel<128, false, 4, 64>), g, dim3(kThreads), 0, stream, a);
     else if (one_per_cu)
       hipLaunchKernelGGL((gemm_ring_kernel<128, false, 9>), g, dim3(kThreads), 0, stream, a);
     else if (wide)
