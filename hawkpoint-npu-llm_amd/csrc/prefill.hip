@@ -1637,9 +1637,12 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     const int rounds64 = (mt * ((a.N + 63) / 64) + slots - 1) / slots;
     const int rounds128 = (mt * ((a.N + 127) / 128) + slots - 1) / slots;
     // when the 128-wide tiles fit one per CU (N = hidden at 4096 tokens),
-    // each takes a deeper ring: 9 stages, 144 KiB of LDS
+    // 64-wide tiles on three 64-deep stages (72 KiB of LDS) run two per CU
+    // instead, with K a multiple of 64; else the 128-wide tiles take a
+    // deeper ring, 9 stages, 144 KiB of LDS
     const bool one_per_cu = !pair && mt * ((a.N + 127) / 128) <= cu_count();
-    const bool wide = !pair && (one_per_cu || rounds64 >= 2 * rounds128);
+    const bool deep64 = one_per_cu && a.K % 64 == 0;
+    const bool wide = !pair && !deep64 && (one_per_cu || rounds64 >= 2 * rounds128);
     const int bn = wide ? 128 : 64;
     // (SwiGLU: 128 gate and 128 up rows per tile, each wave 64 tokens x 64
     // gate + 64 up outputs, three 24 KiB stages; the kernel is held to two
@@ -1648,8 +1651,8 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     const dim3 g(8 * ((mt * ((a.N + bnt - 1) / bnt) + 7) / 8));
     if (pair)
       hipLaunchKernelGGL((gemm_ring_kernel<128, true, 3>), g, dim3(kThreads), 0, stream, a);
-    else if (one_per_cu && a.K % 64 == 0)
-      hipLaunchKernelGGL((gemm_ring_kernel<128, false, 4, 64>), g, dim3(kThreads), 0, stream, a);
+    else if (deep64)
+      hipLaunchKernelGGL((gemm_ring_kernel<64, false, 3, 64>), g, dim3(kThreads), 0, stream, a);
     else if (one_per_cu)
       hipLaunchKernelGGL((gemm_ring_kernel<128, false, 9>), g, dim3(kThreads), 0, stream, a);
     else if (wide)
