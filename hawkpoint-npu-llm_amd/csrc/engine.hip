@@ -623,7 +623,11 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     q.K = H;
     q.epi = lw.qkv_bias ? EPI_BIAS : EPI_BF16;
     q.kblock = fused_norm ? 1 : 0;
-    if (fused_norm) {  // RoPE and the KV append in the QKV epilogue (no q/k/v rows, no rope_append launch)
+    // RoPE and the KV append in the QKV epilogue (no q/k/v rows, no
+    // rope_append launch): the slab GEMMs with the fused norm, and the
+    // 128-token tiles
+    const bool rope_fused = fused_norm || prefill_rope_fusable(n, H);
+    if (rope_fused) {
       q.rope.cos_tab = e->w.rope_cos;
       q.rope.sin_tab = e->w.rope_sin;
       q.rope.qrot = e->pf_q;
@@ -649,7 +653,7 @@ int prefill_chunk(hk_engine* e, const int32_t* tokens_dev, int n, int start) {
     at.out = e->pf_att;
     at.ld_out = QD;
     at.out_kblock = kb;
-    at.rope_done = fused_norm ? 1 : 0;
+    at.rope_done = rope_fused ? 1 : 0;
     at.n = n;
     at.start = start;
     at.q_heads = d.q_heads;

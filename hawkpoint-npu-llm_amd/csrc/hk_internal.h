@@ -238,11 +238,13 @@ struct PrefillGemmArgs {
   // of an MFMA fragment are one 256-byte run (lda, ldy, ldr unused).  A only
   // with kblock = 1, all three with kblock = 2.
   int kblock;
-  // Slab GEMM only, the QKV projection: with rope.on the epilogue applies
-  // RoPE and writes the rotated queries to rope.qrot and the rotated keys and
-  // the values to the caches at slots rope.start.. (rope_append_kernel's job;
-  // Y is not written).  The slabs then take the rows of each RoPE pair
-  // together (rope_row).  N = (q_heads + 2 kv_heads) * 64.
+  // The QKV projection (slab GEMM, or 128-token tiles when
+  // prefill_rope_fusable): with rope.on the epilogue applies RoPE and writes
+  // the rotated queries to rope.qrot and the rotated keys and the values to
+  // the caches at slots rope.start.. (rope_append_kernel's job; Y is not
+  // written).  The slabs then take the rows of each RoPE pair together
+  // (rope_row); a 128-token tile holds whole heads.  N = (q_heads + 2
+  // kv_heads) * 64.
   // Slab GEMM only: the MFMA-native copy of W (launch_repack_mfma), or null
   const void* Wn;
   // Long-K slab GEMM without RoPE, norm or SwiGLU only (the down
@@ -297,6 +299,9 @@ struct PrefillAttnArgs {
   int period;               // set by launch_prefill_attention: the CU count
 };
 
+// Whether a QKV GEMM of M > 64 tokens and K inputs can apply RoPE and the KV
+// append in its epilogue (PrefillGemmArgs::rope; the 128-token tiles).
+bool prefill_rope_fusable(int M, int K);
 // rope_append (unless rope_done) then causal attention for tokens start..start+n-1.
 int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream);
 int launch_embed_rows(const int32_t* tokens, int n, int vocab, const uint16_t* table, int H,

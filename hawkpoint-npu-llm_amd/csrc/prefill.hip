@@ -279,6 +279,56 @@ constexpr int kBRow = kBK + 8;  // bf16 per LDS row (rows 144 B apart: no bank c
 template <int DM> struct DBlock { using T = f32x4; };
 template <> struct DBlock<32> { using T = f32x16; };
 
+// The QKV epilogue with RoPE and the KV append (rope_append_kernel's
+// arithmetic) for outputs n .. n + 7 of token row m: src holds their
+// bf16(sum), partner the bf16(sum) of the RoPE partners n ^ 32 .. (the tiles
+// start at multiples of 64 outputs, so a head's 64 rows share a tile); the
+// bias is added as in the plain epilogue, then q and k rotate and go to the
+// rotated queries and the key cache, v to the value cache, at slot
+// rope.start + m.
+__device__ __forceinline__ void rope_chunk(const PrefillGemmArgs& a, const uint16_t* src, const uint16_t* partner, int m,
+                                           int n) {
+  const auto& at = a.rope;
+  const int hd = n / kHeadDim, j = n % kHeadDim, p = at.start + m;
+  const int np = n ^ (kHeadDim / 2);
+  const u32x4 w = *reinterpret_cast<const u32x4*>(src), wp = *reinterpret_cast<const u32x4*>(partner);
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, wwp[4] = {wp.x, wp.y, wp.z, wp.w};
+  float v[8], vp[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[2 * q] = bf_lo(ww[q]);
+    v[2 * q + 1] = bf_hi(ww[q]);
+    vp[2 * q] = bf_lo(wwp[q]);
+    vp[2 * q + 1] = bf_hi(wwp[q]);
+  }
+  if (a.bias) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] = round_bf16(v[e] + a.bias[n + e]);
+      vp[e] = round_bf16(vp[e] + a.bias[np + e]);
+    }
+  }
+  uint32_t o[4];
+  uint16_t* dst;
+  if (hd < at.q_heads + at.kv_heads) {
+    const float* ct = at.cos_tab + (size_t)p * (kHeadDim / 2) + (j & (kHeadDim / 2 - 1));
+    const float* st = at.sin_tab + (size_t)p * (kHeadDim / 2) + (j & (kHeadDim / 2 - 1));
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)  // first half: x1 c - x2 s; second half: x2 c + x1 s (x1 the first-half value)
+      r[e] = j < kHeadDim / 2 ? v[e] * ct[e] - vp[e] * st[e] : v[e] * ct[e] + vp[e] * st[e];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = f32x2_to_bf16x2(r[2 * q], r[2 * q + 1]);
+    dst = hd < at.q_heads ? at.qrot + (size_t)m * at.q_heads * kHeadDim + (size_t)hd * kHeadDim + j
+                          : at.kcache + ((size_t)(hd - at.q_heads) * at.max_ctx + p) * kHeadDim + j;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = f32x2_to_bf16x2(v[2 * q], v[2 * q + 1]);
+    dst = at.vcache + ((size_t)(hd - at.q_heads - at.kv_heads) * at.max_ctx + p) * kHeadDim + j;
+  }
+  *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
 template <int BM, int BN, bool PAIR, bool W8, int MB, int NB, int DM = 16>
 __device__ __forceinline__ void tile_epilogue(const PrefillGemmArgs& a, const typename DBlock<DM>::T (&acc)[MB][NB],
                                               const typename DBlock<DM>::T (&accu)[PAIR ? MB : 1][PAIR ? NB : 1],
@@ -320,6 +370,12 @@ __device__ __forceinline__ void tile_epilogue(const PrefillGemmArgs& a, const ty
     const int m = m0 + ml, n = n0 + nl;
     if (m >= a.M || n >= a.N) continue;
     const uint16_t* src = ep + ml * ER + nl;
+    if constexpr (!PAIR) {
+      if (a.rope.on) {
+        rope_chunk(a, src, ep + ml * ER + (nl ^ (kHeadDim / 2)), m, n);
+        continue;
+      }
+    }
     uint16_t* y = a.Y + (size_t)m * a.ldy + n;
     if (n + 8 > a.N) {  // a ragged last chunk of the row
       for (int e = 0; e < a.N - n; ++e) {
@@ -1587,8 +1643,10 @@ bool ring_gemm() {
 template <bool W8>
 int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   const bool pair = a.epi == EPI_SWIGLU;
-  if ((a.kblock || a.rope.on) && !(a.grp_count == nullptr && a.M <= kSlabMaxTokens))
-    return fail("prefill gemm: k-blocked operands and RoPE need the slab path (M <= 64)");
+  const bool slab_path = a.grp_count == nullptr && a.M <= kSlabMaxTokens;
+  if (a.kblock && !slab_path) return fail("prefill gemm: k-blocked operands need the slab path (M <= 64)");
+  if (a.rope.on && !slab_path && (a.grp_count != nullptr || !prefill_rope_fusable(a.M, a.K)))
+    return fail("prefill gemm: RoPE needs the slab path (M <= 64) or 128-token tiles with K a multiple of 64");
   if (a.rope.on && (a.N != (a.rope.q_heads + 2 * a.rope.kv_heads) * kHeadDim || a.epi == EPI_SWIGLU))
     return fail("prefill gemm: RoPE needs the QKV projection");
   if (a.slab_ws && (a.gamma || a.rope.on || pair || a.grp_count != nullptr || a.M > kSlabMaxTokens ||
@@ -1608,7 +1666,7 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
     grid.y = (a.max_rows + kTM - 1) / kTM;
     grid.z = a.max_groups;
   }
-  if (a.grp_count == nullptr && a.split_ws != nullptr && a.K % kBK == 0 && split_parts(a.M, a.N, a.K) > 1 &&
+  if (a.grp_count == nullptr && a.split_ws != nullptr && !a.rope.on && a.K % kBK == 0 && split_parts(a.M, a.N, a.K) > 1 &&
       split_ws_need(a.M, a.N, a.K, pair) <= a.split_ws_floats) {
     // too few tiles to fill the GPU: K split over ~kSplitTarget workgroups
     const int parts = split_parts(a.M, a.N, a.K);
@@ -1684,6 +1742,8 @@ int launch_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   return err == hipSuccess ? 0 : hip_fail(err, "prefill gemm launch");
 }
 }  // namespace
+
+bool prefill_rope_fusable(int M, int K) { return M > kSlabMaxTokens && M >= kBM && K % kBK == 0; }
 
 int launch_prefill_gemm(const PrefillGemmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0) return fail("prefill gemm: sizes must be positive");
