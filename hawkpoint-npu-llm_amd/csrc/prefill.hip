@@ -1491,10 +1491,11 @@ __global__ __launch_bounds__(kThreads * ST, ST == 1 ? 2 : 4) void attention_pref
     // O^T[16 db + 4 quad + r][tok] += sum over the block's slots of V^T P^T,
     // 32 slots per bf16 MFMA: k index 8 quad + e stands for slot
     // 32 t + 16 (e / 4) + 4 quad + e % 4, the 8 P values this lane holds for
-    // blocks 2t, 2t + 1.  P (finite, non-negative, 1 at most up to exp2 of a rounding) goes in as three bf16 terms
-    // (split3_bf16), which together are the float32 P exactly; with two
-    // (16 significant bits) about one output in 200 rounded to another bf16
-    // value than the float32 P @ V.
+    // blocks 2t, 2t + 1.  P (finite, non-negative, at most 1 up to exp2 of
+    // a rounding error) goes in as three bf16 terms (split3_bf16), which
+    // together are the float32 P exactly; with two (16 significant bits)
+    // about one output in 200 rounded to another bf16 value than the float32
+    // P @ V.
 #pragma unroll
     for (int t = 0; t < kSB / 2; ++t) {
       float pv[8];
